@@ -1,0 +1,257 @@
+/*
+ * nnx.h — C ABI of libnnunet_hip.so, the MI355X (gfx950) nnU-Net v2 inference path.
+ *
+ * Every entry point takes plain pointers, sizes and a hipStream_t (passed as void*),
+ * returns an int status (NNX_OK = 0, negative = error class) and never lets a C++
+ * exception cross the boundary.  nnx_last_error() returns the thread-local message of
+ * the last failure.  Device pointers are caller-owned unless stated otherwise; the
+ * library owns model weights and the activation/accumulator workspace it allocates at
+ * create/load time or on the first call at a new shape (never inside the tile loop).
+ *
+ * Layouts follow the reference (MedMLX/nnunet-mlx): activations are channels-last
+ * NDHWC float32 (src/nnunet_mlx/model/network.py:1-7); convolution weights are
+ * (C_out, kD, kH, kW, C_in) (src/nnunet_mlx/storage/weights.py:32-45); sliding-window
+ * volumes are channels-first (C, Z, Y, X) (src/nnunet_mlx/prediction/sliding_window.py:131).
+ */
+#ifndef NNX_H
+#define NNX_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- status codes ------------------------------------------------------------- */
+#define NNX_OK 0
+#define NNX_ERR_INVALID (-1)   /* contract violation: shapes, arguments (ContractError) */
+#define NNX_ERR_HIP (-2)       /* HIP runtime error */
+#define NNX_ERR_NONFINITE (-3) /* non-finite logits (ContractError) */
+#define NNX_ERR_STATE (-4)     /* missing/duplicate parameters, wrong call order */
+#define NNX_ERR_NOMEM (-5)     /* device allocation failed */
+
+/* Thread-local message of the last failed call on this thread.
+ * Replaces: ContractError messages, src/nnunet_mlx/errors.py:4. */
+const char* nnx_last_error(void);
+
+/* Library version string and the gfx target the code objects were built for. */
+const char* nnx_version(void);
+
+/* ---- network seam --------------------------------------------------------------
+ * Replaces the InferenceModel protocol (src/nnunet_mlx/model/types.py:17-32) built by
+ * build_model_from_plans (src/nnunet_mlx/model/factory.py:17-65) from
+ * PlainConvUNetSpec / ResidualEncoderUNetSpec (src/nnunet_mlx/model/topology.py:132,257).
+ */
+#define NNX_ARCH_PLAIN 0
+#define NNX_ARCH_RESIDUAL 1
+#define NNX_PRECISION_FP32 0
+
+typedef struct nnx_spec {
+  int arch;              /* NNX_ARCH_PLAIN or NNX_ARCH_RESIDUAL */
+  int spatial_dims;      /* 3 (2-D networks are rejected) */
+  int input_channels;
+  int num_classes;
+  int n_stages;
+  const int* features;      /* n_stages */
+  const int* kernel_sizes;  /* n_stages * 3, odd */
+  const int* strides;       /* n_stages * 3 */
+  const int* encoder_convs; /* n_stages: convs per stage (plain) or blocks per stage (residual) */
+  const int* decoder_convs; /* n_stages - 1 */
+  int conv_bias;
+  int norm_affine;
+  float norm_eps;
+  float leaky_slope;
+  int stem_channels; /* residual only; 0 means features[0] */
+  const int* bottleneck_channels; /* residual only: n_stages entries for BottleneckD, or NULL
+                                     for BasicBlockD */
+  int precision;     /* NNX_PRECISION_FP32 */
+} nnx_spec;
+
+typedef struct nnx_model nnx_model;
+
+/* Build the layer graph of a network; no weights yet.
+ * Replaces PlainConvUNet/ResidualEncoderUNet __init__ (src/nnunet_mlx/model/network.py:422-451,664-699). */
+int nnx_model_create(const nnx_spec* spec, nnx_model** out);
+
+/* Number of parameters the graph expects, and the name/shape of parameter i (reference
+ * key names, e.g. "enc0.block1.conv.weight", "up2.bias", "seg4.weight"). */
+int nnx_model_param_count(const nnx_model* model, int* count);
+int nnx_model_param_info(const nnx_model* model, int index, const char** name, int* ndim,
+                         int64_t* shape /* 5 entries */);
+
+/* Load one float32 host parameter by reference key name and MLX layout.
+ * Replaces load_inference_checkpoint's strict safetensors load
+ * (src/nnunet_mlx/storage/checkpoint.py:130-165,232-237). */
+int nnx_model_load_param(nnx_model* model, const char* name, const float* host,
+                         const int64_t* shape, int ndim);
+
+/* Check that every parameter was loaded exactly once and is finite, repack weights into
+ * the MFMA fragment layouts and upload them.  Required before nnx_forward. */
+int nnx_model_finalize(nnx_model* model);
+
+/* Let `model` use the activation workspace of `owner` (fold ensembles keep every fold's
+ * weights resident but run one fold at a time).  Calls on models sharing a workspace
+ * must be serialised by the caller. */
+int nnx_model_share_workspace(nnx_model* model, nnx_model* owner);
+
+/* Forward n channels-last tiles (n, D, H, W, C_in) -> (n, D, H, W, num_classes) float32.
+ * Replaces PlainConvUNet.__call__ / ResidualEncoderUNet.__call__
+ * (src/nnunet_mlx/model/network.py:453-464,701-728). */
+int nnx_forward(nnx_model* model, const float* d_in, float* d_out, int n, const int* spatial,
+                void* stream);
+
+void nnx_model_destroy(nnx_model* model);
+
+/* ---- sliding-window seam --------------------------------------------------------
+ * Replaces _accumulate_logits + finalizers + fold averaging
+ * (src/nnunet_mlx/prediction/sliding_window.py:158-460, src/nnunet_mlx/prediction/inference.py:93-149).
+ * Tile offsets, mirror order and the Gaussian map are computed by the host layer
+ * (bit-exact with the reference's numpy arithmetic) and passed in.
+ */
+#define NNX_ACCUM_F32 0
+#define NNX_ACCUM_NNUNET_F16 1
+
+typedef struct nnx_sw_config {
+  int channels;             /* C_in of the volume */
+  int num_classes;          /* K */
+  int64_t size[3];          /* unpadded volume size (Z, Y, X) */
+  int pad_before[3];        /* minimum zero padding before each axis (_pad_minimum) */
+  int64_t padded[3];        /* padded size = size + pad */
+  int patch[3];
+  int ntiles;
+  const int* tile_offsets;  /* host, ntiles * 3, padded coordinates, itertools.product order */
+  int nviews;               /* 1 + number of mirrored views */
+  const int* view_flips;    /* host, nviews bitmasks: 1 = axis 0 (z), 2 = axis 1 (y), 4 = axis 2 (x) */
+  int accumulation;         /* NNX_ACCUM_F32 or NNX_ACCUM_NNUNET_F16 */
+  const void* d_gaussian;   /* device, patch voxels, float32 (F32) or float16 (NNUNET_F16) */
+  int tiles_per_batch;      /* tiles sharing one forward batch (views * tiles_per_batch) */
+} nnx_sw_config;
+
+/* Forward callback for custom networks: d_in (n, *patch, C) -> d_out (n, *patch, K). */
+typedef int (*nnx_forward_fn)(void* user, const float* d_in, float* d_out, int n,
+                              const int* spatial, void* stream);
+
+/* Fold-averaged sliding-window prediction on one GPU.  d_volume is (C, Z, Y, X) float32.
+ * Outputs (either may be NULL): d_logits cropped channels-last (Z, Y, X, K) in the
+ * accumulation dtype (float32 or float16), equal to predict_device_logits /
+ * average_fold_device_logits; d_labels cropped (Z, Y, X) uint16 argmax with
+ * earliest-channel ties (predict_labels / normalized_labels).  Returns
+ * NNX_ERR_NONFINITE when any cropped logit is non-finite. */
+int nnx_sw_predict(nnx_model* const* folds, int nfolds, const nnx_sw_config* config,
+                   const float* d_volume, void* d_logits, uint16_t* d_labels, void* stream);
+
+/* Same with caller-supplied forward callbacks (one per fold). */
+int nnx_sw_predict_custom(nnx_forward_fn const* forwards, void* const* users, int nfolds,
+                          const nnx_sw_config* config, const float* d_volume, void* d_logits,
+                          uint16_t* d_labels, void* stream);
+
+/* Release the sliding-window accumulators cached by the library. */
+void nnx_sw_release(void);
+
+/* ---- kernel families (device pointers, caller-owned) ----------------------------- */
+
+/* Count non-finite float32 values; *d_count (device uint32) is overwritten.
+ * Replaces the finite checks of _validate_request (src/nnunet_mlx/prediction/sliding_window.py:470-477). */
+int nnx_count_nonfinite(const float* d_x, int64_t n, unsigned int* d_count, void* stream);
+
+/* Fused InstanceNorm (+ input bias, + optional residual add) + optional LeakyReLU over the
+ * spatial axes of a (B, S, C) float32 tensor; y may alias x.  y = max(slope*r, r) with
+ * r = fma(x + b - mean, gamma*rsqrt(var+eps), beta) (+ residual when given, before the
+ * activation).  Replaces instance_norm (src/nnunet_mlx/kernels/metal_native_norm.py:92-168)
+ * and the residual add + leaky_relu of ResidualBlock (src/nnunet_mlx/model/network.py:511-516). */
+size_t nnx_instnorm_workspace_bytes(int batch, int64_t spatial, int channels);
+int nnx_instnorm_lrelu(const float* d_x, float* d_y, int batch, int64_t spatial, int channels,
+                       const float* d_input_bias, const float* d_gamma, const float* d_beta,
+                       float eps, int apply_act, float slope, const float* d_residual,
+                       void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* Implicit-GEMM 3-D convolution on fp32 MFMA, NDHWC.  Two input pointers implement the
+ * concat-free decoder convolution conv(concat(x1, x2)) (x2 may be NULL, c2 = 0).
+ * Padding is k//2 per axis; the bias (may be NULL) is added to each output.
+ * Replaces mx.conv3d via _unbiased_convolution (src/nnunet_mlx/model/network.py:240-269)
+ * and the split concat convolution (src/nnunet_mlx/model/network.py:305-322). */
+size_t nnx_conv3d_packed_floats(int cout, const int* ksize, int c1, int c2);
+int nnx_conv3d_pack_weight(const float* d_weight /* (Cout,kD,kH,kW,c1+c2) */, int cout,
+                           const int* ksize, int c1, int c2, float* d_packed, void* stream);
+int nnx_conv3d_igemm(const float* d_x1, int c1, const float* d_x2, int c2,
+                     const float* d_packed, const float* d_bias, float* d_y, int batch,
+                     const int* in_size, int cout, const int* ksize, const int* stride,
+                     void* stream);
+
+/* One-input-channel 3x3x3 stride-1 pad-1 convolution, fma over taps in (kd,kh,kw) order.
+ * Replaces single_channel_conv3d (src/nnunet_mlx/kernels/metal_single_channel_conv.py:32-97). */
+int nnx_conv3d_direct_small_cin(const float* d_x, const float* d_weight /* (Cout,3,3,3,1) */,
+                                const float* d_bias, float* d_y, int batch, const int* size,
+                                int cout, void* stream);
+
+/* Stride==kernel ConvTranspose3d as one MFMA GEMM whose epilogue writes the interleaved
+ * output directly (no transpose pass), + bias.
+ * Replaces NonOverlappingConvTranspose3d (src/nnunet_mlx/model/network.py:101-174). */
+size_t nnx_tconv3d_packed_floats(int cout, const int* ksize, int cin);
+int nnx_tconv3d_pack_weight(const float* d_weight /* (Cout,kD,kH,kW,Cin) */, int cout,
+                            const int* ksize, int cin, float* d_packed, void* stream);
+int nnx_tconv3d_gemm(const float* d_x, int cin, const float* d_packed, const float* d_bias,
+                     float* d_y, int batch, const int* in_size, int cout, const int* ksize,
+                     void* stream);
+
+/* 1x1x1 convolution with bias (segmentation head), NDHWC.
+ * Replaces seg{n-1} (src/nnunet_mlx/model/network.py:804-808,875-876). */
+int nnx_conv1x1(const float* d_x, int cin, const float* d_weight /* (Cout,1,1,1,Cin) */,
+                const float* d_bias, float* d_y, int64_t voxels, int cout, void* stream);
+
+/* Gather the tile at `offset` (padded coordinates) of a (C,Z,Y,X) volume, with virtual
+ * zero padding, into nviews channels-last copies, view v flipped along view_flips[v].
+ * Replaces volume[slices][None] + mx.flip/mx.contiguous
+ * (src/nnunet_mlx/prediction/sliding_window.py:407-411,516-517). */
+int nnx_sw_gather_flip(const float* d_volume, int channels, const int64_t* size,
+                       const int* pad_before, const int* offset, const int* patch,
+                       const int* view_flips, int nviews, float* d_out, void* stream);
+
+/* Mirror-average the nviews outputs (flipped back, summed left to right in float32, / nviews)
+ * and add them Gaussian-weighted into the padded (Z,Y,X,K) accumulator and (Z,Y,X)
+ * normalizer.  F32: acc += p*g, norm += g.  NNUNET_F16: acc = f16(f32(acc) + p*f32(g)),
+ * norm = f16(norm + g).
+ * Replaces mirrored_prediction + the scatter-adds of _accumulate_logits
+ * (src/nnunet_mlx/prediction/sliding_window.py:421-436,489-527). */
+int nnx_sw_accumulate(const float* d_pred, int nviews, const int* view_flips, int num_classes,
+                      const int* patch, const void* d_gaussian, const int* offset,
+                      const int64_t* padded, int accumulation, void* d_acc, void* d_norm,
+                      void* stream);
+
+/* Normalise the cropped accumulator (f32(acc)/f32(norm), cast to the accumulation dtype)
+ * into the fold total: total = normalized (first fold) or total + normalized.
+ * Replaces predict_device_logits / add_fold_device_logits finalizers
+ * (src/nnunet_mlx/prediction/sliding_window.py:242-249,285-302). */
+int nnx_sw_fold_add(const void* d_acc, const void* d_norm, int num_classes, const int64_t* padded,
+                    const int* crop_lo, const int64_t* crop_size, int accumulation, int first,
+                    void* d_total, void* stream);
+
+/* Divide the fold total by nfolds (float32, cast back; skipped for one fold), write the
+ * optional logits and the argmax labels (earliest channel on ties; 65535 and a count in
+ * *d_invalid for non-finite values).
+ * Replaces average_fold_device_logits' division and normalized_labels' argmax
+ * (src/nnunet_mlx/prediction/inference.py:140-149, src/nnunet_mlx/kernels/metal_normalized_labels.py:19-98). */
+int nnx_sw_fold_finalize(const void* d_total, int num_classes, int64_t voxels, int nfolds,
+                         int accumulation, void* d_logits, uint16_t* d_labels,
+                         unsigned int* d_invalid, void* stream);
+
+/* ---- kernel timing (no reference counterpart: measurement support) ----------------
+ * Between nnx_profile_begin and nnx_profile_end every kernel launch of the library is
+ * bracketed by HIP events on its own stream and attributed to a class (kernel name and
+ * variant) with its algorithmic FLOPs and HBM bytes.  nnx_profile_end synchronises the
+ * events; nnx_profile_read returns class `index` (0 <= index < *count). */
+int nnx_profile_begin(void);
+int nnx_profile_end(int* count);
+int nnx_profile_read(int index, const char** name, int* launches, double* milliseconds,
+                     double* flops, double* bytes);
+
+/* AvgPool3d with kernel == stride on NDHWC (residual skip path).
+ * Replaces _build_residual_skip's pool (src/nnunet_mlx/model/network.py:576-602). */
+int nnx_avgpool3d(const float* d_x, float* d_y, int batch, const int* in_size, int channels,
+                  const int* kernel, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* NNX_H */

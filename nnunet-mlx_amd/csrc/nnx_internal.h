@@ -1,0 +1,151 @@
+// Internal helpers shared by the HIP sources of libnnunet_hip.so: error plumbing,
+// launch checks and small device utilities.  Nothing here crosses the C ABI.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/nnx.h"
+
+namespace nnx {
+
+// Thrown inside the library, converted to a status code + message at the ABI boundary.
+struct Error : std::runtime_error {
+  int code;
+  Error(int c, const std::string& msg) : std::runtime_error(msg), code(c) {}
+};
+
+void set_last_error(const std::string& msg);
+
+[[noreturn]] inline void fail(int code, const std::string& msg) { throw Error(code, msg); }
+
+inline void require(bool ok, const std::string& msg) {
+  if (!ok) fail(NNX_ERR_INVALID, msg);
+}
+
+inline void hip_check(hipError_t err, const char* what) {
+  if (err != hipSuccess) {
+    fail(err == hipErrorOutOfMemory ? NNX_ERR_NOMEM : NNX_ERR_HIP,
+         std::string(what) + ": " + hipGetErrorString(err));
+  }
+}
+
+// Check the launch itself (bad configuration etc.).
+inline void launch_check(const char* name) { hip_check(hipGetLastError(), name); }
+
+// Wrap an ABI body: convert exceptions into status codes.
+template <class F>
+int guarded(F&& body) {
+  try {
+    body();
+    return NNX_OK;
+  } catch (const Error& e) {
+    set_last_error(e.what());
+    return e.code;
+  } catch (const std::bad_alloc&) {
+    set_last_error("host allocation failed");
+    return NNX_ERR_NOMEM;
+  } catch (const std::exception& e) {
+    set_last_error(e.what());
+    return NNX_ERR_STATE;
+  }
+}
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Physical workgroup ids are dealt round-robin to the 8 XCDs of an MI355X.  This maps a
+// physical id to a logical id so that each XCD receives one contiguous range of logical
+// ids (neighbouring tiles share halos and weights through that XCD's L2).  Bijective on
+// [0, n) for any n.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  constexpr int kXcd = 8;
+  const int q = n / kXcd, r = n % kXcd;
+  const int xcd = bid % kXcd, idx = bid / kXcd;
+  return xcd < r ? xcd * (q + 1) + idx : r * (q + 1) + (xcd - r) * q + idx;
+}
+
+}  // namespace nnx
+
+// Optional per-launch timing with HIP events recorded on the launch stream.  When
+// profiling is off (the default) a ProfScope costs one branch.
+namespace nnx {
+
+bool prof_enabled();
+void prof_start(const char* name, double flops, double bytes, hipStream_t st);
+void prof_stop(hipStream_t st);
+
+struct ProfScope {
+  hipStream_t st;
+  bool on;
+  ProfScope(const char* name, double flops, double bytes, hipStream_t s) : st(s), on(prof_enabled()) {
+    if (on) prof_start(name, flops, bytes, st);
+  }
+  ~ProfScope() {
+    if (on) prof_stop(st);
+  }
+};
+
+}  // namespace nnx
+
+// Kernel launcher entry points shared between the kernel files and the runtime.
+namespace nnx {
+
+struct ConvGeom {
+  int batch;
+  int in[3];
+  int out[3];
+  int k[3];
+  int s[3];
+  int p[3];
+};
+
+ConvGeom make_conv_geom(int batch, const int* in_size, const int* ksize, const int* stride);
+
+// Packed weight helpers (device layout described in nnx_conv.hip).
+int64_t conv_packed_floats(int cout, const int* ksize, int c1, int c2);
+void conv_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int c2,
+                      float* d_packed, hipStream_t st);
+void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
+                  const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st);
+void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
+                        const int* size, int cout, hipStream_t st);
+
+int64_t tconv_packed_floats(int cout, const int* ksize, int cin);
+void tconv_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float* d_packed,
+                       hipStream_t st);
+void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bias, float* y,
+                  int batch, const int* in_size, int cout, const int* ksize, hipStream_t st);
+void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y,
+             int64_t voxels, int cout, hipStream_t st);
+
+size_t instnorm_workspace_bytes(int batch, int64_t spatial, int channels);
+void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int channels,
+                    const float* input_bias, const float* gamma, const float* beta, float eps,
+                    bool act, float slope, const float* residual, void* ws, size_t ws_bytes,
+                    hipStream_t st);
+void avgpool3d(const float* x, float* y, int batch, const int* in_size, int channels,
+               const int* kernel, hipStream_t st);
+
+void count_nonfinite(const float* x, int64_t n, unsigned int* count, hipStream_t st);
+
+void sw_gather_flip(const float* vol, int channels, const int64_t* size, const int* pad_before,
+                    const int* offset, const int* patch, const int* flips, int nviews,
+                    float* out, hipStream_t st);
+void sw_accumulate(const float* pred, int nviews, const int* flips, int k, const int* patch,
+                   const void* gaussian, const int* offset, const int64_t* padded, int accum,
+                   void* acc, void* norm, hipStream_t st);
+void sw_fold_add(const void* acc, const void* norm, int k, const int64_t* padded,
+                 const int* crop_lo, const int64_t* crop_size, int accum, bool first,
+                 void* total, hipStream_t st);
+void sw_fold_finalize(const void* total, int k, int64_t voxels, int nfolds, int accum,
+                      void* logits, uint16_t* labels, unsigned int* invalid, hipStream_t st);
+void fill_zero(void* ptr, size_t bytes, hipStream_t st);
+
+}  // namespace nnx

@@ -1,0 +1,395 @@
+// Instance normalisation + LeakyReLU for channels-last (B, S, C) float32 tensors.
+//
+// Three bandwidth-bound launches (two full reads and one write of the tensor):
+//   1. norm_stats: each workgroup owns one chunk of R*vpi voxels of one sample and keeps
+//      its values in registers; it reduces the chunk sum (wavefront shuffles + LDS),
+//      forms the chunk mean, then the centred sum of squares from the same registers
+//      (two-pass inside the chunk) and writes (mean, M2) per channel.
+//   2. norm_merge: per (b, c), the chunk partials are combined with Chan's parallel
+//      update in float64, giving mean and biased variance of x + input_bias.
+//   3. norm_apply: y = max(slope*r, r), r = fma(x + b - mean, gamma*rsqrt(var+eps), beta)
+//      (+ residual before the activation), vectorised float4, in place allowed.
+#include "nnx_internal.h"
+
+namespace nnx {
+namespace {
+
+constexpr int kRows = 16;       // voxels per thread in the statistics pass
+constexpr int kMaxThreads = 256;
+
+template <int VW>
+struct Vec;
+template <>
+struct Vec<4> {
+  typedef float type __attribute__((ext_vector_type(4)));
+};
+template <>
+struct Vec<1> {
+  typedef float type;
+};
+
+template <int VW>
+__device__ __forceinline__ float lane_of(const typename Vec<VW>::type& v, int q) {
+  if constexpr (VW == 1) {
+    return v;
+  } else {
+    return v[q];
+  }
+}
+
+template <int VW>
+__global__ __launch_bounds__(kMaxThreads) void norm_stats_kernel(
+    const float* __restrict__ x, const float* __restrict__ in_bias, float2* __restrict__ partial,
+    int64_t S, int C, int vpi, int nchunks) {
+  typedef typename Vec<VW>::type V;
+  __shared__ float red[kMaxThreads * VW];
+  __shared__ float cmean[kMaxThreads * VW];
+  const int b = blockIdx.y;
+  const int chunk = blockIdx.x;
+  const int groups = C / VW;
+  const int tid = threadIdx.x;
+  const bool active = tid < vpi * groups;
+  const int g = tid % groups;
+  const int j = tid / groups;
+  const int64_t v0 = (int64_t)chunk * kRows * vpi;
+  const int64_t nvalid64 = S - v0 < (int64_t)kRows * vpi ? S - v0 : (int64_t)kRows * vpi;
+  const float n = (float)nvalid64;
+  const float* xs = x + (int64_t)b * S * C;
+
+  float bias[VW];
+#pragma unroll
+  for (int q = 0; q < VW; ++q) bias[q] = (in_bias && active) ? in_bias[g * VW + q] : 0.f;
+
+  float vals[kRows][VW];
+  bool valid[kRows];
+  float sum[VW];
+#pragma unroll
+  for (int q = 0; q < VW; ++q) sum[q] = 0.f;
+#pragma unroll
+  for (int it = 0; it < kRows; ++it) {
+    const int64_t v = v0 + (int64_t)it * vpi + j;
+    valid[it] = active && v < S;
+    V raw;
+    if (valid[it]) {
+      raw = *reinterpret_cast<const V*>(xs + v * C + g * VW);
+    } else {
+      if constexpr (VW == 1) raw = 0.f; else raw = V{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int q = 0; q < VW; ++q) {
+      float val = lane_of<VW>(raw, q);
+      if (in_bias) val = val + bias[q];
+      vals[it][q] = valid[it] ? val : 0.f;
+      sum[q] += vals[it][q];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < VW; ++q) red[tid * VW + q] = sum[q];
+  __syncthreads();
+  if (tid < groups) {
+#pragma unroll
+    for (int q = 0; q < VW; ++q) {
+      float t = 0.f;
+      for (int jj = 0; jj < vpi; ++jj) t += red[(jj * groups + tid) * VW + q];
+      cmean[tid * VW + q] = t / n;
+    }
+  }
+  __syncthreads();
+  float m2[VW];
+#pragma unroll
+  for (int q = 0; q < VW; ++q) {
+    const float mu = active ? cmean[g * VW + q] : 0.f;
+    float acc = 0.f;
+#pragma unroll
+    for (int it = 0; it < kRows; ++it) {
+      const float d = valid[it] ? vals[it][q] - mu : 0.f;
+      acc = fmaf(d, d, acc);
+    }
+    m2[q] = acc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int q = 0; q < VW; ++q) red[tid * VW + q] = m2[q];
+  __syncthreads();
+  if (tid < groups) {
+#pragma unroll
+    for (int q = 0; q < VW; ++q) {
+      float t = 0.f;
+      for (int jj = 0; jj < vpi; ++jj) t += red[(jj * groups + tid) * VW + q];
+      partial[((int64_t)b * nchunks + chunk) * C + tid * VW + q] =
+          make_float2(cmean[tid * VW + q], t);
+    }
+  }
+}
+
+// Chan et al. pairwise combination of (count, mean, M2) in float64.
+__device__ __forceinline__ void chan_merge(double& na, double& ma, double& m2a, double nb,
+                                           double mb, double m2b) {
+  if (nb == 0.0) return;
+  if (na == 0.0) {
+    na = nb;
+    ma = mb;
+    m2a = m2b;
+    return;
+  }
+  const double n = na + nb;
+  const double delta = mb - ma;
+  ma = ma + delta * (nb / n);
+  m2a = m2a + m2b + delta * delta * (na * nb / n);
+  na = n;
+}
+
+__global__ __launch_bounds__(256) void norm_merge_kernel(const float2* __restrict__ partial,
+                                                         float2* __restrict__ params,
+                                                         const float* __restrict__ gamma,
+                                                         int64_t S, int C, int nchunks,
+                                                         int chunk_vox, float eps) {
+  __shared__ double sn[256], sm[256], s2[256];
+  const int c = blockIdx.x;
+  const int b = blockIdx.y;
+  double n = 0.0, m = 0.0, m2 = 0.0;
+  for (int i = threadIdx.x; i < nchunks; i += blockDim.x) {
+    const int64_t start = (int64_t)i * chunk_vox;
+    const double cnt = (double)((S - start) < chunk_vox ? (S - start) : chunk_vox);
+    const float2 p = partial[((int64_t)b * nchunks + i) * C + c];
+    chan_merge(n, m, m2, cnt, (double)p.x, (double)p.y);
+  }
+  sn[threadIdx.x] = n;
+  sm[threadIdx.x] = m;
+  s2[threadIdx.x] = m2;
+  __syncthreads();
+  for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
+    if ((int)threadIdx.x < stride) {
+      double na = sn[threadIdx.x], ma = sm[threadIdx.x], m2a = s2[threadIdx.x];
+      chan_merge(na, ma, m2a, sn[threadIdx.x + stride], sm[threadIdx.x + stride],
+                 s2[threadIdx.x + stride]);
+      sn[threadIdx.x] = na;
+      sm[threadIdx.x] = ma;
+      s2[threadIdx.x] = m2a;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double var = s2[0] / (double)S;
+    float varf = (float)(var > 0.0 ? var : 0.0);
+    float scale = 1.0f / sqrtf(varf + eps);
+    if (gamma) scale = gamma[c] * scale;
+    params[(int64_t)b * C + c] = make_float2((float)sm[0], scale);
+  }
+}
+
+template <int VW>
+__global__ __launch_bounds__(256) void norm_apply_kernel(
+    const float* x, float* y, const float2* __restrict__ params, const float* __restrict__ in_bias,
+    const float* __restrict__ beta, const float* residual, int64_t SC, int C, int act,
+    float slope) {
+  typedef typename Vec<VW>::type V;
+  extern __shared__ float smem[];  // C * 4: mean, scale, beta, input bias
+  float* s_mean = smem;
+  float* s_scale = smem + C;
+  float* s_beta = smem + 2 * C;
+  float* s_bias = smem + 3 * C;
+  const int b = blockIdx.y;
+  for (int i = threadIdx.x; i < C; i += blockDim.x) {
+    const float2 p = params[(int64_t)b * C + i];
+    s_mean[i] = p.x;
+    s_scale[i] = p.y;
+    s_beta[i] = beta ? beta[i] : 0.f;
+    s_bias[i] = in_bias ? in_bias[i] : 0.f;
+  }
+  __syncthreads();
+  const float* xs = x + (int64_t)b * SC;
+  float* ys = y + (int64_t)b * SC;
+  const float* rs = residual ? residual + (int64_t)b * SC : nullptr;
+  const int64_t nvec = SC / VW;
+  const bool has_bias = in_bias != nullptr;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t e = i * VW;
+    const int c0 = (int)(e % C);
+    V xv = *reinterpret_cast<const V*>(xs + e);
+    V rv;
+    if (rs) rv = *reinterpret_cast<const V*>(rs + e);
+    V out;
+#pragma unroll
+    for (int q = 0; q < VW; ++q) {
+      const int c = c0 + q;
+      float v = lane_of<VW>(xv, q);
+      if (has_bias) v = v + s_bias[c];
+      float r = fmaf(v - s_mean[c], s_scale[c], s_beta[c]);
+      if (rs) r = r + lane_of<VW>(rv, q);
+      if (act) r = fmaxf(slope * r, r);
+      if constexpr (VW == 1) out = r; else out[q] = r;
+    }
+    *reinterpret_cast<V*>(ys + e) = out;
+  }
+}
+
+__global__ __launch_bounds__(256) void avgpool_kernel(const float* __restrict__ x,
+                                                      float* __restrict__ y, int64_t nout,
+                                                      int D, int H, int W, int C, int kd, int kh,
+                                                      int kw) {
+  const int od = D / kd, oh = H / kh, ow = W / kw;
+  const float inv = 1.0f / (float)(kd * kh * kw);
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nout;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % C);
+    int64_t v = i / C;
+    const int xx = (int)(v % ow);
+    v /= ow;
+    const int yy = (int)(v % oh);
+    v /= oh;
+    const int zz = (int)(v % od);
+    const int64_t b = v / od;
+    float s = 0.f;
+    for (int a = 0; a < kd; ++a)
+      for (int e = 0; e < kh; ++e)
+        for (int f = 0; f < kw; ++f)
+          s += x[((((b * D) + zz * kd + a) * H + yy * kh + e) * (int64_t)W + xx * kw + f) * C + c];
+    y[i] = s * inv;
+  }
+}
+
+__global__ __launch_bounds__(256) void nonfinite_kernel(const float* __restrict__ x, int64_t n,
+                                                        unsigned int* count) {
+  __shared__ unsigned int total;
+  if (threadIdx.x == 0) total = 0;
+  __syncthreads();
+  unsigned int local = 0;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    local += isfinite(x[i]) ? 0u : 1u;
+  if (local) atomicAdd(&total, local);
+  __syncthreads();
+  if (threadIdx.x == 0 && total) atomicAdd(count, total);
+}
+
+__global__ void fill_zero_kernel(uint32_t* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0u;
+}
+
+__global__ void fill_zero_bytes_kernel(unsigned char* p, int64_t n) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
+struct StatsLayout {
+  int vw, groups, vpi, chunk_vox;
+  int64_t nchunks;
+};
+
+StatsLayout stats_layout(int64_t spatial, int channels) {
+  StatsLayout l;
+  l.vw = channels % 4 == 0 ? 4 : 1;
+  l.groups = channels / l.vw;
+  require(l.groups <= kMaxThreads, "instance normalisation supports at most 1024 channels");
+  l.vpi = kMaxThreads / l.groups;
+  l.chunk_vox = kRows * l.vpi;
+  l.nchunks = ceil_div(spatial, l.chunk_vox);
+  return l;
+}
+
+}  // namespace
+
+size_t instnorm_workspace_bytes(int batch, int64_t spatial, int channels) {
+  const StatsLayout l = stats_layout(spatial, channels);
+  const size_t partial = (size_t)batch * l.nchunks * channels * sizeof(float2);
+  const size_t params = (size_t)batch * channels * sizeof(float2);
+  return ((partial + 255) / 256) * 256 + params;
+}
+
+void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int channels,
+                    const float* input_bias, const float* gamma, const float* beta, float eps,
+                    bool act, float slope, const float* residual, void* ws, size_t ws_bytes,
+                    hipStream_t st) {
+  require(x && y, "instance normalisation pointers must not be null");
+  require(batch >= 1 && spatial >= 1 && channels >= 1, "instance normalisation needs a non-empty tensor");
+  require(eps > 0.f, "instance-normalization epsilon must be positive");
+  require(batch <= 65535, "instance normalisation batch too large");
+  const StatsLayout l = stats_layout(spatial, channels);
+  require(l.nchunks < (1LL << 31), "instance normalisation tensor too large");
+  require(ws && ws_bytes >= instnorm_workspace_bytes(batch, spatial, channels),
+          "instance normalisation workspace too small");
+  float2* partial = reinterpret_cast<float2*>(ws);
+  const size_t partial_bytes = (size_t)batch * l.nchunks * channels * sizeof(float2);
+  float2* params = reinterpret_cast<float2*>(reinterpret_cast<char*>(ws) +
+                                             ((partial_bytes + 255) / 256) * 256);
+  const dim3 sgrid((unsigned)l.nchunks, (unsigned)batch);
+  const double nelem = (double)batch * spatial * channels;
+  {
+  ProfScope prof("instnorm_stats", 0.0, 4.0 * nelem, st);
+  if (l.vw == 4)
+    hipLaunchKernelGGL(norm_stats_kernel<4>, sgrid, dim3(kMaxThreads), 0, st, x, input_bias,
+                       partial, spatial, channels, l.vpi, (int)l.nchunks);
+  else
+    hipLaunchKernelGGL(norm_stats_kernel<1>, sgrid, dim3(kMaxThreads), 0, st, x, input_bias,
+                       partial, spatial, channels, l.vpi, (int)l.nchunks);
+  launch_check("instnorm stats");
+  }
+  {
+  ProfScope prof("instnorm_merge", 0.0, 8.0 * (double)batch * l.nchunks * channels, st);
+  hipLaunchKernelGGL(norm_merge_kernel, dim3(channels, batch), dim3(256), 0, st, partial, params,
+                     gamma, spatial, channels, (int)l.nchunks, l.chunk_vox, eps);
+  launch_check("instnorm merge");
+  }
+  ProfScope prof("instnorm_apply", 0.0, 4.0 * nelem * (residual ? 3 : 2), st);
+  const int64_t sc = spatial * channels;
+  const int64_t nvec = sc / l.vw;
+  const int64_t blocks = std::min<int64_t>(ceil_div(nvec, 256 * 4), 16384);
+  const size_t smem = (size_t)channels * 4 * sizeof(float);
+  if (l.vw == 4)
+    hipLaunchKernelGGL(norm_apply_kernel<4>, dim3((unsigned)std::max<int64_t>(blocks, 1), batch),
+                       dim3(256), smem, st, x, y, params, input_bias, beta, residual, sc,
+                       channels, act ? 1 : 0, slope);
+  else
+    hipLaunchKernelGGL(norm_apply_kernel<1>, dim3((unsigned)std::max<int64_t>(blocks, 1), batch),
+                       dim3(256), smem, st, x, y, params, input_bias, beta, residual, sc,
+                       channels, act ? 1 : 0, slope);
+  launch_check("instnorm apply");
+}
+
+void avgpool3d(const float* x, float* y, int batch, const int* in_size, int channels,
+               const int* kernel, hipStream_t st) {
+  require(x && y, "pooling pointers must not be null");
+  for (int i = 0; i < 3; ++i)
+    require(kernel[i] >= 1 && in_size[i] >= kernel[i], "invalid pooling geometry");
+  const int64_t nout = (int64_t)batch * (in_size[0] / kernel[0]) * (in_size[1] / kernel[1]) *
+                       (in_size[2] / kernel[2]) * channels;
+  const int64_t blocks = std::min<int64_t>(ceil_div(nout, 256), 65536);
+  ProfScope prof("avgpool3d", 0.0, 4.0 * (double)nout * (1 + kernel[0] * kernel[1] * kernel[2]), st);
+  hipLaunchKernelGGL(avgpool_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, y, nout,
+                     in_size[0], in_size[1], in_size[2], channels, kernel[0], kernel[1], kernel[2]);
+  launch_check("avgpool3d");
+}
+
+void count_nonfinite(const float* x, int64_t n, unsigned int* count, hipStream_t st) {
+  require(count != nullptr, "count pointer must not be null");
+  fill_zero(count, sizeof(unsigned int), st);
+  if (n <= 0) return;
+  require(x != nullptr, "input pointer must not be null");
+  const int64_t blocks = std::min<int64_t>(ceil_div(n, 256), 4096);
+  hipLaunchKernelGGL(nonfinite_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, n, count);
+  launch_check("count_nonfinite");
+}
+
+void fill_zero(void* ptr, size_t bytes, hipStream_t st) {
+  if (bytes == 0) return;
+  require(ptr != nullptr, "fill pointer must not be null");
+  if (bytes % 4 == 0 && reinterpret_cast<uintptr_t>(ptr) % 4 == 0) {
+    const int64_t n = (int64_t)(bytes / 4);
+    const int64_t blocks = std::min<int64_t>(ceil_div(n, 256), 65536);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       reinterpret_cast<uint32_t*>(ptr), n);
+  } else {
+    const int64_t n = (int64_t)bytes;
+    const int64_t blocks = std::min<int64_t>(ceil_div(n, 256), 65536);
+    hipLaunchKernelGGL(fill_zero_bytes_kernel, dim3((unsigned)blocks), dim3(256), 0, st,
+                       reinterpret_cast<unsigned char*>(ptr), n);
+  }
+  launch_check("fill_zero");
+}
+
+}  // namespace nnx

@@ -1,0 +1,267 @@
+// GPU-resident sliding-window kernels.  All arithmetic is float32 (or IEEE half where
+// the nnU-Net fp16 accumulation mode asks for it) with explicitly separate multiply and
+// add, so the per-voxel results equal the reference's numpy/MLX sequence bit for bit
+// given identical network outputs:
+//   mirror average  p = ((view0 + view1') + view2') + ... ; p = p / nviews
+//   float32 mode    acc = acc + p*g            norm = norm + g
+//   fp16 mode       acc = f16(f32(acc) + p*f32(g))   norm = f16(norm + g)
+//   finalize        q = f32(acc) / f32(norm) -> accumulation dtype; folds summed in that
+//                   dtype; average = dtype(f32(total) / f32(nfolds)); argmax with the
+//                   earliest channel winning ties, 65535 for non-finite scores.
+#include "nnx_internal.h"
+
+namespace nnx {
+namespace {
+
+struct Flips {
+  int f[8];
+};
+
+__device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
+__device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
+
+__global__ __launch_bounds__(256) void gather_flip_kernel(
+    const float* __restrict__ vol, int C, int64_t Z, int64_t Y, int64_t X, int pz, int py, int px,
+    int oz, int oy, int ox, int PZ, int PY, int PX, Flips flips, int nviews,
+    float* __restrict__ out) {
+  const int64_t pvox = (int64_t)PZ * PY * PX;
+  const int64_t zyx = Z * Y * X;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < pvox * nviews;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int v = (int)(i / pvox);
+    const int64_t p = i - (int64_t)v * pvox;
+    const int x = (int)(p % PX);
+    const int y = (int)((p / PX) % PY);
+    const int z = (int)(p / ((int64_t)PX * PY));
+    const int f = flips.f[v];
+    const int sz = (f & 1) ? PZ - 1 - z : z;
+    const int sy = (f & 2) ? PY - 1 - y : y;
+    const int sx = (f & 4) ? PX - 1 - x : x;
+    const int64_t gz = (int64_t)oz + sz - pz, gy = (int64_t)oy + sy - py, gx = (int64_t)ox + sx - px;
+    const bool inside = gz >= 0 && gz < Z && gy >= 0 && gy < Y && gx >= 0 && gx < X;
+    const int64_t src = (gz * Y + gy) * X + gx;
+    float* dst = out + i * C;
+    for (int c = 0; c < C; ++c) dst[c] = inside ? vol[(int64_t)c * zyx + src] : 0.f;
+  }
+}
+
+template <bool kHalf>
+__global__ __launch_bounds__(256) void accumulate_kernel(
+    const float* __restrict__ pred, int nviews, Flips flips, int K, int PZ, int PY, int PX,
+    const void* __restrict__ gaussian, int oz, int oy, int ox, int64_t QY, int64_t QX,
+    void* __restrict__ acc, void* __restrict__ norm) {
+  const int64_t pvox = (int64_t)PZ * PY * PX;
+  const float count = (float)nviews;
+  for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < pvox;
+       p += (int64_t)gridDim.x * blockDim.x) {
+    const int x = (int)(p % PX);
+    const int y = (int)((p / PX) % PY);
+    const int z = (int)(p / ((int64_t)PX * PY));
+    int64_t src[8];
+    for (int v = 0; v < nviews; ++v) {
+      const int f = flips.f[v];
+      const int sz = (f & 1) ? PZ - 1 - z : z;
+      const int sy = (f & 2) ? PY - 1 - y : y;
+      const int sx = (f & 4) ? PX - 1 - x : x;
+      src[v] = (int64_t)v * pvox + ((int64_t)sz * PY + sy) * PX + sx;
+    }
+    const int64_t dst = (((int64_t)oz + z) * QY + (oy + y)) * QX + (ox + x);
+    float g;
+    if constexpr (kHalf)
+      g = __half2float(reinterpret_cast<const __half*>(gaussian)[p]);
+    else
+      g = reinterpret_cast<const float*>(gaussian)[p];
+    for (int k = 0; k < K; ++k) {
+      float s = pred[src[0] * K + k];
+      for (int v = 1; v < nviews; ++v) s = add_rn(s, pred[src[v] * K + k]);
+      if (nviews > 1) s = __fdiv_rn(s, count);
+      const float w = mul_rn(s, g);
+      if constexpr (kHalf) {
+        __half* a = reinterpret_cast<__half*>(acc) + dst * K + k;
+        *a = __float2half_rn(add_rn(__half2float(*a), w));
+      } else {
+        float* a = reinterpret_cast<float*>(acc) + dst * K + k;
+        *a = add_rn(*a, w);
+      }
+    }
+    if constexpr (kHalf) {
+      __half* nrm = reinterpret_cast<__half*>(norm) + dst;
+      *nrm = __float2half_rn(add_rn(__half2float(*nrm), g));
+    } else {
+      float* nrm = reinterpret_cast<float*>(norm) + dst;
+      *nrm = add_rn(*nrm, g);
+    }
+  }
+}
+
+template <bool kHalf>
+__global__ __launch_bounds__(256) void fold_add_kernel(const void* __restrict__ acc,
+                                                       const void* __restrict__ norm, int K,
+                                                       int64_t QY, int64_t QX, int cz, int cy,
+                                                       int cx, int64_t CZ, int64_t CY,
+                                                       int64_t CX, int first,
+                                                       void* __restrict__ total) {
+  const int64_t n = CZ * CY * CX;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t x = i % CX;
+    const int64_t y = (i / CX) % CY;
+    const int64_t z = i / (CX * CY);
+    const int64_t src = ((cz + z) * QY + (cy + y)) * QX + (cx + x);
+    float den;
+    if constexpr (kHalf)
+      den = __half2float(reinterpret_cast<const __half*>(norm)[src]);
+    else
+      den = reinterpret_cast<const float*>(norm)[src];
+    for (int k = 0; k < K; ++k) {
+      float num;
+      if constexpr (kHalf)
+        num = __half2float(reinterpret_cast<const __half*>(acc)[src * K + k]);
+      else
+        num = reinterpret_cast<const float*>(acc)[src * K + k];
+      const float q = __fdiv_rn(num, den);
+      if constexpr (kHalf) {
+        __half* t = reinterpret_cast<__half*>(total) + i * K + k;
+        const __half qh = __float2half_rn(q);
+        *t = first ? qh : __float2half_rn(add_rn(__half2float(*t), __half2float(qh)));
+      } else {
+        float* t = reinterpret_cast<float*>(total) + i * K + k;
+        *t = first ? q : add_rn(*t, q);
+      }
+    }
+  }
+}
+
+template <bool kHalf>
+__global__ __launch_bounds__(256) void fold_finalize_kernel(const void* __restrict__ total, int K,
+                                                            int64_t n, int nfolds,
+                                                            void* __restrict__ logits,
+                                                            uint16_t* __restrict__ labels,
+                                                            unsigned int* invalid_count) {
+  __shared__ unsigned int block_invalid;
+  if (threadIdx.x == 0) block_invalid = 0;
+  __syncthreads();
+  unsigned int local_invalid = 0;
+  const float fn = (float)nfolds;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    float best = -INFINITY;
+    unsigned int winner = 0xffffffffu;
+    bool invalid = false;
+    for (int k = 0; k < K; ++k) {
+      float v;
+      if constexpr (kHalf) {
+        __half h = reinterpret_cast<const __half*>(total)[i * K + k];
+        if (nfolds > 1) h = __float2half_rn(__fdiv_rn(__half2float(h), fn));
+        if (logits) reinterpret_cast<__half*>(logits)[i * K + k] = h;
+        v = __half2float(h);
+      } else {
+        v = reinterpret_cast<const float*>(total)[i * K + k];
+        if (nfolds > 1) v = __fdiv_rn(v, fn);
+        if (logits) reinterpret_cast<float*>(logits)[i * K + k] = v;
+      }
+      invalid |= !isfinite(v);
+      if (v > best) {
+        best = v;
+        winner = (unsigned int)k;
+      }
+    }
+    if (labels) labels[i] = invalid ? (uint16_t)65535 : (uint16_t)winner;
+    local_invalid += invalid ? 1u : 0u;
+  }
+  if (local_invalid) atomicAdd(&block_invalid, local_invalid);
+  __syncthreads();
+  if (threadIdx.x == 0 && block_invalid && invalid_count) atomicAdd(invalid_count, block_invalid);
+}
+
+unsigned grid_for(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 65536)); }
+
+Flips make_flips(const int* flips, int nviews) {
+  require(nviews >= 1 && nviews <= 8, "between 1 and 8 mirrored views are supported");
+  Flips f{};
+  for (int v = 0; v < nviews; ++v) {
+    require(flips[v] >= 0 && flips[v] < 8, "view flip masks must be in [0, 8)");
+    f.f[v] = flips[v];
+  }
+  return f;
+}
+
+}  // namespace
+
+void sw_gather_flip(const float* vol, int channels, const int64_t* size, const int* pad_before,
+                    const int* offset, const int* patch, const int* flips, int nviews,
+                    float* out, hipStream_t st) {
+  require(vol && out, "gather pointers must not be null");
+  require(channels >= 1, "gather needs at least one channel");
+  const Flips f = make_flips(flips, nviews);
+  const int64_t n = (int64_t)patch[0] * patch[1] * patch[2] * nviews;
+  ProfScope prof("sw_gather_flip", 0.0, 4.0 * (double)n / nviews * channels * (1 + nviews), st);
+  hipLaunchKernelGGL(gather_flip_kernel, dim3(grid_for(n)), dim3(256), 0, st, vol, channels,
+                     size[0], size[1], size[2], pad_before[0], pad_before[1], pad_before[2],
+                     offset[0], offset[1], offset[2], patch[0], patch[1], patch[2], f, nviews, out);
+  launch_check("sw_gather_flip");
+}
+
+void sw_accumulate(const float* pred, int nviews, const int* flips, int k, const int* patch,
+                   const void* gaussian, const int* offset, const int64_t* padded, int accum,
+                   void* acc, void* norm, hipStream_t st) {
+  require(pred && gaussian && acc && norm, "accumulate pointers must not be null");
+  require(k >= 1, "accumulate needs at least one class");
+  for (int i = 0; i < 3; ++i)
+    require(offset[i] >= 0 && offset[i] + patch[i] <= padded[i], "tile outside the padded volume");
+  const Flips f = make_flips(flips, nviews);
+  const int64_t n = (int64_t)patch[0] * patch[1] * patch[2];
+  const double esz = accum == NNX_ACCUM_NNUNET_F16 ? 2.0 : 4.0;
+  ProfScope prof("sw_accumulate", 0.0,
+                 (double)n * (nviews * k * 4.0 + 2.0 * k * esz + 2.0 * esz + esz), st);
+  if (accum == NNX_ACCUM_NNUNET_F16)
+    hipLaunchKernelGGL(accumulate_kernel<true>, dim3(grid_for(n)), dim3(256), 0, st, pred, nviews,
+                       f, k, patch[0], patch[1], patch[2], gaussian, offset[0], offset[1],
+                       offset[2], padded[1], padded[2], acc, norm);
+  else
+    hipLaunchKernelGGL(accumulate_kernel<false>, dim3(grid_for(n)), dim3(256), 0, st, pred, nviews,
+                       f, k, patch[0], patch[1], patch[2], gaussian, offset[0], offset[1],
+                       offset[2], padded[1], padded[2], acc, norm);
+  launch_check("sw_accumulate");
+}
+
+void sw_fold_add(const void* acc, const void* norm, int k, const int64_t* padded,
+                 const int* crop_lo, const int64_t* crop_size, int accum, bool first,
+                 void* total, hipStream_t st) {
+  require(acc && norm && total, "fold pointers must not be null");
+  for (int i = 0; i < 3; ++i)
+    require(crop_lo[i] >= 0 && crop_lo[i] + crop_size[i] <= padded[i], "crop outside the volume");
+  const int64_t n = crop_size[0] * crop_size[1] * crop_size[2];
+  const double esz = accum == NNX_ACCUM_NNUNET_F16 ? 2.0 : 4.0;
+  ProfScope prof("sw_fold_add", 0.0, (double)n * (k * esz + esz + k * esz * (first ? 1 : 2)), st);
+  if (accum == NNX_ACCUM_NNUNET_F16)
+    hipLaunchKernelGGL(fold_add_kernel<true>, dim3(grid_for(n)), dim3(256), 0, st, acc, norm, k,
+                       padded[1], padded[2], crop_lo[0], crop_lo[1], crop_lo[2], crop_size[0],
+                       crop_size[1], crop_size[2], first ? 1 : 0, total);
+  else
+    hipLaunchKernelGGL(fold_add_kernel<false>, dim3(grid_for(n)), dim3(256), 0, st, acc, norm, k,
+                       padded[1], padded[2], crop_lo[0], crop_lo[1], crop_lo[2], crop_size[0],
+                       crop_size[1], crop_size[2], first ? 1 : 0, total);
+  launch_check("sw_fold_add");
+}
+
+void sw_fold_finalize(const void* total, int k, int64_t voxels, int nfolds, int accum,
+                      void* logits, uint16_t* labels, unsigned int* invalid, hipStream_t st) {
+  require(total != nullptr, "fold total must not be null");
+  require(k >= 1 && k <= 65535, "label reduction supports 1..65535 classes");
+  require(nfolds >= 1, "at least one fold");
+  if (invalid) fill_zero(invalid, sizeof(unsigned int), st);
+  if (voxels <= 0) return;
+  const double esz = accum == NNX_ACCUM_NNUNET_F16 ? 2.0 : 4.0;
+  ProfScope prof("sw_fold_finalize", 0.0,
+                 (double)voxels * (k * esz + (labels ? 2.0 : 0.0) + (logits ? k * esz : 0.0)), st);
+  if (accum == NNX_ACCUM_NNUNET_F16)
+    hipLaunchKernelGGL(fold_finalize_kernel<true>, dim3(grid_for(voxels)), dim3(256), 0, st, total,
+                       k, voxels, nfolds, logits, labels, invalid);
+  else
+    hipLaunchKernelGGL(fold_finalize_kernel<false>, dim3(grid_for(voxels)), dim3(256), 0, st,
+                       total, k, voxels, nfolds, logits, labels, invalid);
+  launch_check("sw_fold_finalize");
+}
+
+}  // namespace nnx

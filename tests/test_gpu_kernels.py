@@ -1,0 +1,329 @@
+"""Per-kernel parity of the HIP path against float64 / numpy references.
+
+Convolutions, transposed convolution and the seg head are compared with float64 torch-CPU
+operators (rel-L2 <= 1e-5 and max-abs <= 1e-4 * max|ref|, float32 accumulation over up to
+17,280 products); instance norm with a float64 restatement; the sliding-window kernels
+(gather+flip, mirror-average + Gaussian accumulation, fold add, finalize) bit for bit with
+numpy float32/float16 arithmetic in the reference's operation order.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from nnunet_mlx import _native
+from tests.helpers import dev, host, rel_l2, report, stream
+
+pytestmark = pytest.mark.gpu
+
+
+def _conv_ref64(x, w, stride):
+    xt = torch.from_numpy(x.astype(np.float64)).permute(0, 4, 1, 2, 3)
+    wt = torch.from_numpy(w.astype(np.float64)).permute(0, 4, 1, 2, 3)
+    pad = tuple(k // 2 for k in w.shape[1:4])
+    y = F.conv3d(xt, wt, None, stride=tuple(stride), padding=pad)
+    return y.permute(0, 2, 3, 4, 1).numpy()
+
+
+CONV_CASES = [
+    # batch, in_size, c1, c2, cout, kernel, stride
+    (1, (8, 8, 8), 4, 0, 8, (3, 3, 3), (1, 1, 1)),
+    (2, (16, 16, 16), 32, 0, 32, (3, 3, 3), (1, 1, 1)),
+    (1, (17, 9, 20), 32, 0, 32, (3, 3, 3), (1, 1, 1)),
+    (2, (16, 16, 16), 32, 32, 32, (3, 3, 3), (1, 1, 1)),
+    (1, (16, 16, 16), 32, 0, 64, (3, 3, 3), (2, 2, 2)),
+    (1, (15, 13, 17), 32, 0, 64, (3, 3, 3), (2, 2, 2)),
+    (1, (12, 12, 12), 64, 0, 64, (3, 3, 3), (1, 1, 1)),
+    (2, (8, 8, 8), 128, 0, 128, (3, 3, 3), (1, 1, 1)),
+    (1, (24, 24, 32), 64, 0, 128, (3, 3, 3), (1, 1, 1)),
+    (1, (4, 4, 4), 320, 320, 320, (3, 3, 3), (1, 1, 1)),
+    (1, (8, 8, 8), 256, 0, 320, (3, 3, 3), (2, 2, 2)),
+    (1, (7, 10, 8), 2, 0, 32, (3, 3, 3), (1, 2, 2)),
+    (1, (6, 8, 8), 8, 0, 16, (1, 3, 3), (1, 1, 1)),
+    (1, (8, 8, 8), 16, 0, 32, (1, 1, 1), (1, 1, 1)),
+    (1, (9, 9, 9), 3, 0, 5, (3, 3, 3), (1, 1, 1)),
+    (1, (5, 7, 6), 12, 20, 24, (3, 3, 3), (1, 1, 1)),
+]
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}-k{c[5]}-s{c[6]}")
+def test_conv3d_igemm_matches_float64(lib, case):
+    batch, size, c1, c2, cout, kernel, stride = case
+    print(f"conv case {case}", flush=True)
+    rng = np.random.default_rng(hash(case) % 2**32)
+    x1 = rng.standard_normal((batch, *size, c1)).astype(np.float32)
+    x2 = rng.standard_normal((batch, *size, c2)).astype(np.float32) if c2 else None
+    w = (rng.standard_normal((cout, *kernel, c1 + c2)) / np.sqrt((c1 + c2) * np.prod(kernel))).astype(np.float32)
+    bias = rng.standard_normal(cout).astype(np.float32)
+    out_size = [(s + 2 * (k // 2) - k) // st + 1 for s, k, st in zip(size, kernel, stride)]
+    k_c = _native.ints(kernel)
+    packed = torch.empty(lib.nnx_conv3d_packed_floats(cout, k_c, c1, c2), dtype=torch.float32, device="cuda")
+    dw = dev(w)
+    _native.check(lib.nnx_conv3d_pack_weight(dw.data_ptr(), cout, k_c, c1, c2, packed.data_ptr(), stream()))
+    dx1 = dev(x1)
+    dx2 = dev(x2) if c2 else None
+    db = dev(bias)
+    y = torch.full((batch, *out_size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_conv3d_igemm(
+        dx1.data_ptr(), c1, dx2.data_ptr() if c2 else None, c2, packed.data_ptr(), db.data_ptr(),
+        y.data_ptr(), batch, _native.ints(size), cout, k_c, _native.ints(stride), stream()))
+    got = host(y)
+    full = np.concatenate([x1, x2], axis=-1) if c2 else x1
+    ref = _conv_ref64(full, w, stride) + bias.astype(np.float64)
+    msg = report("conv", got, ref)
+    assert np.isfinite(got).all(), msg
+    assert rel_l2(got, ref) <= 1e-5, msg
+    assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
+
+
+@pytest.mark.parametrize("size,cout", [((16, 16, 16), 32), ((5, 7, 9), 8)])
+def test_direct_single_channel_conv(lib, size, cout):
+    print(f"direct conv {size} {cout}", flush=True)
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((2, *size, 1)).astype(np.float32)
+    w = (rng.standard_normal((cout, 3, 3, 3, 1)) * 0.3).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    y = torch.empty((2, *size, cout), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_conv3d_direct_small_cin(
+        dev(x).data_ptr(), dev(w).data_ptr(), dev(b).data_ptr(), y.data_ptr(), 2,
+        _native.ints(size), cout, stream()))
+    got = host(y)
+    ref = _conv_ref64(x, w, (1, 1, 1)) + b
+    assert rel_l2(got, ref) <= 1e-6, report("direct", got, ref)
+
+
+def _norm_ref64(x, in_bias, gamma, beta, eps, act, slope, residual):
+    v = x.astype(np.float64)
+    if in_bias is not None:
+        v = v + in_bias
+    axes = tuple(range(1, v.ndim - 1))
+    mean = v.mean(axis=axes, keepdims=True)
+    var = ((v - mean) ** 2).mean(axis=axes, keepdims=True)
+    r = (v - mean) / np.sqrt(var + eps)
+    if gamma is not None:
+        r = r * gamma
+    if beta is not None:
+        r = r + beta
+    if residual is not None:
+        r = r + residual
+    if act:
+        r = np.maximum(slope * r, r)
+    return r
+
+
+NORM_CASES = [
+    # batch, spatial, channels, affine, input_bias, act, residual
+    (2, (16, 16, 16), 32, False, False, True, False),
+    (1, (9, 11, 13), 32, True, True, True, False),
+    (3, (4, 4, 4), 320, True, False, True, False),
+    (1, (8, 8, 8), 64, True, True, False, True),
+    (2, (5, 6, 7), 2, True, True, True, True),
+    (1, (32, 32, 32), 128, False, True, True, False),
+]
+
+
+@pytest.mark.parametrize("case", NORM_CASES, ids=str)
+def test_instnorm_lrelu_matches_float64(lib, case):
+    batch, spatial, c, affine, use_bias, act, use_res = case
+    print(f"norm case {case}", flush=True)
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((batch, *spatial, c)) * 3 + 1.5).astype(np.float32)
+    in_bias = rng.standard_normal(c).astype(np.float32) if use_bias else None
+    gamma = (1 + 0.2 * rng.standard_normal(c)).astype(np.float32) if affine else None
+    beta = (0.3 * rng.standard_normal(c)).astype(np.float32) if affine else None
+    res = rng.standard_normal(x.shape).astype(np.float32) if use_res else None
+    S = int(np.prod(spatial))
+    nbytes = lib.nnx_instnorm_workspace_bytes(batch, S, c)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dx = dev(x)
+    y = torch.empty_like(dx)
+    keep = [dev(a) if a is not None else None for a in (in_bias, gamma, beta, res)]
+    ptrs = [k.data_ptr() if k is not None else None for k in keep]
+    _native.check(lib.nnx_instnorm_lrelu(
+        dx.data_ptr(), y.data_ptr(), batch, S, c, ptrs[0], ptrs[1], ptrs[2], 1e-5, int(act), 0.01,
+        ptrs[3], ws.data_ptr(), nbytes, stream()))
+    got = host(y)
+    ref = _norm_ref64(x, in_bias, gamma, beta, 1e-5, act, 0.01, res)
+    assert np.abs(got - ref).max() <= 2e-5, report("norm", got, ref)
+
+
+def test_instnorm_in_place_and_constant_channel(lib):
+    x = np.full((1, 6, 6, 6, 4), 0.1, dtype=np.float32)
+    x[..., 1] = np.random.default_rng(0).standard_normal((1, 6, 6, 6))
+    S = 216
+    nbytes = lib.nnx_instnorm_workspace_bytes(1, S, 4)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dx = dev(x)
+    _native.check(lib.nnx_instnorm_lrelu(dx.data_ptr(), dx.data_ptr(), 1, S, 4, None, None, None,
+                                         1e-5, 1, 0.01, None, ws.data_ptr(), nbytes, stream()))
+    got = host(dx)
+    assert np.abs(got[..., 0]).max() < 1e-4  # variance clamped, output ~0
+    ref = _norm_ref64(x, None, None, None, 1e-5, True, 0.01, None)
+    assert np.abs(got[..., 1] - ref[..., 1]).max() < 2e-5
+
+
+@pytest.mark.parametrize("case", [
+    (2, (4, 4, 4), 64, 32, (2, 2, 2)),
+    (1, (7, 5, 4), 320, 320, (1, 2, 2)),
+    (1, (8, 8, 8), 128, 64, (2, 2, 2)),
+    (1, (3, 5, 2), 6, 4, (2, 1, 2)),
+], ids=str)
+def test_tconv3d_gemm_matches_float64(lib, case):
+    batch, size, cin, cout, k = case
+    print(f"tconv case {case}", flush=True)
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((batch, *size, cin)).astype(np.float32)
+    w = (rng.standard_normal((cout, *k, cin)) / np.sqrt(cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    k_c = _native.ints(k)
+    packed = torch.empty(lib.nnx_tconv3d_packed_floats(cout, k_c, cin), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_tconv3d_pack_weight(dev(w).data_ptr(), cout, k_c, cin, packed.data_ptr(), stream()))
+    out_size = [s * kk for s, kk in zip(size, k)]
+    y = torch.full((batch, *out_size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_tconv3d_gemm(dev(x).data_ptr(), cin, packed.data_ptr(), dev(b).data_ptr(),
+                                       y.data_ptr(), batch, _native.ints(size), cout, k_c, stream()))
+    got = host(y)
+    xt = torch.from_numpy(x.astype(np.float64)).permute(0, 4, 1, 2, 3)
+    wt = torch.from_numpy(w.astype(np.float64)).permute(4, 0, 1, 2, 3)
+    ref = F.conv_transpose3d(xt, wt, torch.from_numpy(b.astype(np.float64)), stride=k)
+    ref = ref.permute(0, 2, 3, 4, 1).numpy()
+    assert np.isfinite(got).all()
+    assert rel_l2(got, ref) <= 1e-6, report("tconv", got, ref)
+
+
+def test_conv1x1_seg_head(lib):
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((2, 6, 7, 8, 32)).astype(np.float32)
+    w = rng.standard_normal((3, 1, 1, 1, 32)).astype(np.float32)
+    b = rng.standard_normal(3).astype(np.float32)
+    y = torch.empty((2, 6, 7, 8, 3), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_conv1x1(dev(x).data_ptr(), 32, dev(w).data_ptr(), dev(b).data_ptr(),
+                                  y.data_ptr(), 2 * 6 * 7 * 8, 3, stream()))
+    ref = np.einsum("nzyxc,oc->nzyxo", x.astype(np.float64), w[:, 0, 0, 0, :].astype(np.float64)) + b
+    assert rel_l2(host(y), ref) <= 1e-6
+
+
+def test_avgpool3d(lib):
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((2, 8, 6, 4, 5)).astype(np.float32)
+    y = torch.empty((2, 4, 3, 2, 5), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_avgpool3d(dev(x).data_ptr(), y.data_ptr(), 2, _native.ints((8, 6, 4)), 5,
+                                    _native.ints((2, 2, 2)), stream()))
+    ref = x.reshape(2, 4, 2, 3, 2, 2, 2, 5).astype(np.float64).mean(axis=(2, 4, 6))
+    assert np.abs(host(y) - ref).max() < 1e-6
+
+
+# ---- sliding-window kernels: bitwise ------------------------------------------------
+
+FLIPS_3AX = [0, 1, 2, 4, 3, 5, 6, 7]
+
+
+def _unflip(view: np.ndarray, mask: int) -> np.ndarray:
+    axes = tuple(a for a in range(3) if mask >> a & 1)
+    return np.flip(view, axis=axes) if axes else view
+
+
+def test_gather_flip_exact(lib):
+    rng = np.random.default_rng(8)
+    vol = rng.standard_normal((2, 9, 11, 13)).astype(np.float32)
+    pad = (2, 0, 1)
+    patch = (12, 8, 10)
+    offset = (0, 3, 4)
+    padded = np.pad(vol, [(0, 0), (pad[0], 12 - 9 - pad[0]), (0, 0), (pad[2], 1)])
+    out = torch.full((8, *patch, 2), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_sw_gather_flip(
+        dev(vol).data_ptr(), 2, _native.i64s(vol.shape[1:]), _native.ints(pad), _native.ints(offset),
+        _native.ints(patch), _native.ints(FLIPS_3AX), 8, out.data_ptr(), stream()))
+    got = host(out)
+    tile = np.moveaxis(padded[:, offset[0]:offset[0] + 12, offset[1]:offset[1] + 8, offset[2]:offset[2] + 10], 0, -1)
+    for v, mask in enumerate(FLIPS_3AX):
+        np.testing.assert_array_equal(got[v], _unflip(tile, mask))
+
+
+@pytest.mark.parametrize("fp16", [False, True])
+def test_accumulate_fold_finalize_bitwise(lib, fp16):
+    rng = np.random.default_rng(9)
+    K, patch = 3, (6, 5, 4)
+    padded = (10, 9, 7)
+    g = rng.uniform(0.01, 1.0, patch).astype(np.float16 if fp16 else np.float32)
+    acc = np.zeros((*padded, K), dtype=g.dtype)
+    norm = np.zeros(padded, dtype=g.dtype)
+    dacc, dnorm = dev(acc), dev(norm)
+    dg = dev(g)
+    offsets = [(0, 0, 0), (4, 4, 3), (2, 1, 0), (4, 0, 3)]
+    accum = _native.NNX_ACCUM_NNUNET_F16 if fp16 else _native.NNX_ACCUM_F32
+    for off in offsets:
+        pred = (rng.standard_normal((8, *patch, K)) * 4).astype(np.float32)
+        _native.check(lib.nnx_sw_accumulate(
+            dev(pred).data_ptr(), 8, _native.ints(FLIPS_3AX), K, _native.ints(patch), dg.data_ptr(),
+            _native.ints(off), _native.i64s(padded), accum, dacc.data_ptr(), dnorm.data_ptr(), stream()))
+        s = pred[0]
+        for v in range(1, 8):
+            s = s + _unflip(pred[v], FLIPS_3AX[v])
+        s = s / np.float32(8)
+        sl = tuple(slice(o, o + p) for o, p in zip(off, patch))
+        if fp16:
+            acc[sl] = (acc[sl].astype(np.float32) + s * g.astype(np.float32)[..., None]).astype(np.float16)
+            norm[sl] = norm[sl] + g
+        else:
+            acc[sl] += s * g[..., None]
+            norm[sl] += g
+    np.testing.assert_array_equal(host(dacc), acc)
+    np.testing.assert_array_equal(host(dnorm), norm)
+    # fold add (2 folds: the same accumulator twice) and finalize with crop
+    crop_lo, crop = (1, 2, 1), (8, 6, 5)
+    total = torch.empty((*crop, K), dtype=dacc.dtype, device="cuda")
+    for first in (1, 0):
+        _native.check(lib.nnx_sw_fold_add(dacc.data_ptr(), dnorm.data_ptr(), K, _native.i64s(padded),
+                                          _native.ints(crop_lo), _native.i64s(crop), accum, first,
+                                          total.data_ptr(), stream()))
+    csl = tuple(slice(o, o + c) for o, c in zip(crop_lo, crop))
+    dt = np.float16 if fp16 else np.float32
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = (acc.astype(np.float32) / norm.astype(np.float32)[..., None]).astype(dt)[csl]
+    expected_total = (q + q).astype(dt)
+    got_total = host(total)
+    np.testing.assert_array_equal(got_total, expected_total)
+    logits = torch.empty_like(total)
+    labels = torch.empty(crop, dtype=torch.int16, device="cuda")
+    invalid = torch.zeros(1, dtype=torch.int32, device="cuda")
+    _native.check(lib.nnx_sw_fold_finalize(total.data_ptr(), K, int(np.prod(crop)), 2, accum,
+                                           logits.data_ptr(), labels.data_ptr(), invalid.data_ptr(), stream()))
+    avg = (expected_total.astype(np.float32) / np.float32(2)).astype(dt)
+    np.testing.assert_array_equal(host(logits), avg)
+    finite = np.isfinite(avg.astype(np.float32)).all(axis=-1)
+    want = np.argmax(np.where(np.isfinite(avg), avg, -np.inf).astype(np.float32), axis=-1).astype(np.uint16)
+    want[~finite] = 65535
+    np.testing.assert_array_equal(host(labels).view(np.uint16), want)
+    assert int(host(invalid)[0]) == int((~finite).sum())
+
+
+def test_finalize_ties_choose_earliest_and_flags_nonfinite(lib):
+    total = np.array([[1.0, 1.0, 0.5], [0.2, 3.0, 3.0], [np.nan, 1.0, 2.0], [-np.inf, -1.0, -1.0]],
+                     dtype=np.float32)
+    labels = torch.empty(4, dtype=torch.int16, device="cuda")
+    invalid = torch.zeros(1, dtype=torch.int32, device="cuda")
+    _native.check(lib.nnx_sw_fold_finalize(dev(total).data_ptr(), 3, 4, 1, _native.NNX_ACCUM_F32, None,
+                                           labels.data_ptr(), invalid.data_ptr(), stream()))
+    np.testing.assert_array_equal(host(labels).view(np.uint16), [0, 1, 65535, 65535])
+    assert int(host(invalid)[0]) == 2
+
+
+def test_count_nonfinite(lib):
+    x = np.zeros(100000, dtype=np.float32)
+    x[[5, 77, 99999]] = [np.inf, np.nan, -np.inf]
+    count = torch.empty(1, dtype=torch.int32, device="cuda")
+    _native.check(lib.nnx_count_nonfinite(dev(x).data_ptr(), x.size, count.data_ptr(), stream()))
+    assert int(host(count)[0]) == 3
+
+
+def test_errors_are_reported(lib):
+    from nnunet_mlx.errors import ContractError
+
+    with pytest.raises(ContractError, match="odd"):
+        _native.check(lib.nnx_conv3d_igemm(None, 1, None, 0, None, None, None, 1, _native.ints((4, 4, 4)), 4,
+                                           _native.ints((2, 2, 2)), _native.ints((1, 1, 1)), stream()))
+    assert lib.nnx_last_error()

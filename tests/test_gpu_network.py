@@ -1,0 +1,92 @@
+"""Full-network forward on the HIP path vs the torch-CPU float32 oracle.
+
+Tolerances are the fp32 parity bar: max-abs <= 1e-3 and relative-L2 <= 1e-5 on the
+logits, and identical argmax labels on >= 99.99% of voxels.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from nnunet_mlx.model.network import build_network
+from nnunet_mlx.model.topology import PlainConvUNetSpec, ResidualEncoderUNetSpec
+from nnunet_mlx.storage.synthetic import random_weights
+from oracle.network import OracleNetwork
+from tests.helpers import rel_l2, report
+
+pytestmark = pytest.mark.gpu
+
+K3 = ((3, 3, 3),)
+
+
+def liver_spec(cin=1, classes=3, strides=None) -> PlainConvUNetSpec:
+    return PlainConvUNetSpec(
+        input_channels=cin, num_classes=classes, features=(32, 64, 128, 256, 320, 320),
+        kernel_sizes=K3 * 6,
+        strides=strides or ((1, 1, 1),) + ((2, 2, 2),) * 5,
+        encoder_convs=(2,) * 6, decoder_convs=(2,) * 5,
+    )
+
+
+def resenc_spec() -> ResidualEncoderUNetSpec:
+    return ResidualEncoderUNetSpec(
+        input_channels=1, num_classes=3, features=(32, 64, 128, 256, 320, 320, 320),
+        kernel_sizes=K3 * 7,
+        strides=((1, 1, 1),) + ((2, 2, 2),) * 5 + ((2, 1, 1),),
+        encoder_blocks=(1, 3, 4, 6, 6, 6, 6), decoder_convs=(1,) * 6,
+    )
+
+
+CASES = {
+    "liver-32": (liver_spec(), (32, 32, 32), 2, False),
+    "liver-32-affine": (liver_spec(), (32, 32, 32), 1, True),
+    "brats-4ch": (liver_spec(cin=4, classes=5), (32, 32, 32), 1, True),
+    "autopet-aniso": (liver_spec(cin=2, classes=2, strides=((1, 1, 1),) + ((2, 2, 2),) * 4 + ((1, 2, 2),)),
+                      (16, 32, 32), 1, True),
+    "tiny-plain": (PlainConvUNetSpec(1, 3, (4, 8), K3 * 2, ((1, 1, 1), (2, 2, 2)), (2, 2), (2,)),
+                   (8, 8, 8), 2, True),
+    "tiny-residual": (ResidualEncoderUNetSpec(1, 3, (4, 8, 16), K3 * 3, ((1, 1, 1), (2, 2, 2), (2, 2, 2)),
+                                              (1, 3, 4), (1, 1)), (8, 8, 8), 2, True),
+    "tiny-bottleneck": (ResidualEncoderUNetSpec(1, 3, (4, 8, 16), K3 * 3, ((1, 1, 1), (2, 2, 2), (2, 2, 2)),
+                                                (1, 2, 2), (1, 1), bottleneck_channels=(2, 4, 8)),
+                        (8, 8, 8), 1, True),
+    "resenc-L": (resenc_spec(), (64, 32, 32), 1, True),
+}
+
+
+@pytest.mark.parametrize("name", list(CASES))
+def test_forward_matches_oracle(device, name):
+    spec, patch, batch, affine = CASES[name]
+    print(f"network case {name} patch={patch} batch={batch}", flush=True)
+    weights = random_weights(spec, seed=1, random_affine=affine)
+    net = build_network(spec)
+    net.load_weights(weights)
+    rng = np.random.default_rng(0)
+    x = rng.standard_normal((batch, *patch, spec.input_channels)).astype(np.float32)
+    got = net(torch.from_numpy(x).to(device)).cpu().numpy()
+    residual = isinstance(spec, ResidualEncoderUNetSpec)
+    ref = OracleNetwork(spec, weights, residual=residual)(x)
+    msg = report(name, got, ref)
+    print(msg, flush=True)
+    assert got.shape == ref.shape
+    assert np.abs(got - ref).max() <= 1e-3, msg
+    assert rel_l2(got, ref) <= 1e-5, msg
+    agree = (got.argmax(-1) == ref.argmax(-1)).mean()
+    assert agree >= 0.9999, f"{msg} label agreement {agree}"
+    net.close()
+
+
+def test_forward_rejects_bad_input(device):
+    from nnunet_mlx.errors import ContractError
+
+    spec = CASES["tiny-plain"][0]
+    net = build_network(spec)
+    with pytest.raises(ContractError):
+        net(torch.zeros((1, 8, 8, 8, 1), device=device))  # weights not loaded
+    net.load_weights(random_weights(spec, seed=0))
+    with pytest.raises(ContractError):
+        net(torch.zeros((1, 8, 8, 8, 2), device=device))  # wrong channel count
+    with pytest.raises(ContractError):
+        net(torch.zeros((1, 9, 8, 8, 1), device=device))  # not divisible by the stride

@@ -1,0 +1,46 @@
+"""CPU-only checks of the C-ABI library: it loads and exports every declared symbol."""
+
+from __future__ import annotations
+
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def _declared_symbols() -> set[str]:
+    text = (ROOT / "include" / "nnx.h").read_text()
+    return set(re.findall(r"\b(nnx_[a-z0-9_]+)\s*\(", text)) - {"nnx_forward_fn"}
+
+
+def test_header_declarations_match_binding_table():
+    from nnunet_mlx import _native
+
+    assert _declared_symbols() == set(_native.EXPORTED_SYMBOLS)
+
+
+def test_library_loads_and_exports_every_symbol():
+    from nnunet_mlx import _native
+
+    if not _native.library_path().is_file():
+        pytest.fail("libnnunet_hip.so is not built; run __graft_entry__.build()")
+    lib = _native.load()
+    for name in _declared_symbols():
+        assert getattr(lib, name) is not None, name
+    assert b"gfx950" in lib.nnx_version()
+
+
+def test_error_path_without_gpu():
+    """Argument validation happens before any device call, so it works on a CPU host."""
+    from nnunet_mlx import _native
+    from nnunet_mlx.errors import ContractError
+
+    lib = _native.load()
+    rc = lib.nnx_conv3d_igemm(None, 1, None, 0, None, None, None, 1, _native.ints((4, 4, 4)), 4,
+                              _native.ints((2, 2, 2)), _native.ints((1, 1, 1)), None)
+    assert rc == _native.NNX_ERR_INVALID
+    assert b"odd" in lib.nnx_last_error()
+    with pytest.raises(ContractError):
+        _native.check(rc)
