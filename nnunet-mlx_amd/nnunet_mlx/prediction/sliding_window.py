@@ -169,7 +169,7 @@ class _Request:
         self.offsets = [tuple(o) for o in product(*steps)]
         self.flips = mirror_flip_masks(self.axes)
         gaussian = nnunet_fp16_gaussian(self.patch) if self.fp16 else gaussian_importance(self.patch)
-        self.gaussian = torch.from_numpy(np.ascontiguousarray(gaussian)).to(device)
+        self.gaussian = torch.from_numpy(np.array(gaussian, copy=True)).to(device)
         self.device = device
         if tiles_per_batch is None:
             tiles_per_batch = max(1, 8 // len(self.flips))

@@ -87,8 +87,9 @@ def test_direct_single_channel_conv(lib, size, cout):
     w = (rng.standard_normal((cout, 3, 3, 3, 1)) * 0.3).astype(np.float32)
     b = rng.standard_normal(cout).astype(np.float32)
     y = torch.empty((2, *size, cout), dtype=torch.float32, device="cuda")
+    dx, dw, db = dev(x), dev(w), dev(b)  # keep device buffers alive across the launch
     _native.check(lib.nnx_conv3d_direct_small_cin(
-        dev(x).data_ptr(), dev(w).data_ptr(), dev(b).data_ptr(), y.data_ptr(), 2,
+        dx.data_ptr(), dw.data_ptr(), db.data_ptr(), y.data_ptr(), 2,
         _native.ints(size), cout, stream()))
     got = host(y)
     ref = _conv_ref64(x, w, (1, 1, 1)) + b
@@ -180,10 +181,11 @@ def test_tconv3d_gemm_matches_float64(lib, case):
     b = rng.standard_normal(cout).astype(np.float32)
     k_c = _native.ints(k)
     packed = torch.empty(lib.nnx_tconv3d_packed_floats(cout, k_c, cin), dtype=torch.float32, device="cuda")
-    _native.check(lib.nnx_tconv3d_pack_weight(dev(w).data_ptr(), cout, k_c, cin, packed.data_ptr(), stream()))
+    dx, dw, db = dev(x), dev(w), dev(b)
+    _native.check(lib.nnx_tconv3d_pack_weight(dw.data_ptr(), cout, k_c, cin, packed.data_ptr(), stream()))
     out_size = [s * kk for s, kk in zip(size, k)]
     y = torch.full((batch, *out_size, cout), float("nan"), dtype=torch.float32, device="cuda")
-    _native.check(lib.nnx_tconv3d_gemm(dev(x).data_ptr(), cin, packed.data_ptr(), dev(b).data_ptr(),
+    _native.check(lib.nnx_tconv3d_gemm(dx.data_ptr(), cin, packed.data_ptr(), db.data_ptr(),
                                        y.data_ptr(), batch, _native.ints(size), cout, k_c, stream()))
     got = host(y)
     xt = torch.from_numpy(x.astype(np.float64)).permute(0, 4, 1, 2, 3)
@@ -200,7 +202,8 @@ def test_conv1x1_seg_head(lib):
     w = rng.standard_normal((3, 1, 1, 1, 32)).astype(np.float32)
     b = rng.standard_normal(3).astype(np.float32)
     y = torch.empty((2, 6, 7, 8, 3), dtype=torch.float32, device="cuda")
-    _native.check(lib.nnx_conv1x1(dev(x).data_ptr(), 32, dev(w).data_ptr(), dev(b).data_ptr(),
+    dx, dw, db = dev(x), dev(w), dev(b)
+    _native.check(lib.nnx_conv1x1(dx.data_ptr(), 32, dw.data_ptr(), db.data_ptr(),
                                   y.data_ptr(), 2 * 6 * 7 * 8, 3, stream()))
     ref = np.einsum("nzyxc,oc->nzyxo", x.astype(np.float64), w[:, 0, 0, 0, :].astype(np.float64)) + b
     assert rel_l2(host(y), ref) <= 1e-6
@@ -210,7 +213,8 @@ def test_avgpool3d(lib):
     rng = np.random.default_rng(6)
     x = rng.standard_normal((2, 8, 6, 4, 5)).astype(np.float32)
     y = torch.empty((2, 4, 3, 2, 5), dtype=torch.float32, device="cuda")
-    _native.check(lib.nnx_avgpool3d(dev(x).data_ptr(), y.data_ptr(), 2, _native.ints((8, 6, 4)), 5,
+    dx = dev(x)
+    _native.check(lib.nnx_avgpool3d(dx.data_ptr(), y.data_ptr(), 2, _native.ints((8, 6, 4)), 5,
                                     _native.ints((2, 2, 2)), stream()))
     ref = x.reshape(2, 4, 2, 3, 2, 2, 2, 5).astype(np.float64).mean(axis=(2, 4, 6))
     assert np.abs(host(y) - ref).max() < 1e-6
@@ -234,8 +238,9 @@ def test_gather_flip_exact(lib):
     offset = (0, 3, 4)
     padded = np.pad(vol, [(0, 0), (pad[0], 12 - 9 - pad[0]), (0, 0), (pad[2], 1)])
     out = torch.full((8, *patch, 2), float("nan"), dtype=torch.float32, device="cuda")
+    dvol = dev(vol)
     _native.check(lib.nnx_sw_gather_flip(
-        dev(vol).data_ptr(), 2, _native.i64s(vol.shape[1:]), _native.ints(pad), _native.ints(offset),
+        dvol.data_ptr(), 2, _native.i64s(vol.shape[1:]), _native.ints(pad), _native.ints(offset),
         _native.ints(patch), _native.ints(FLIPS_3AX), 8, out.data_ptr(), stream()))
     got = host(out)
     tile = np.moveaxis(padded[:, offset[0]:offset[0] + 12, offset[1]:offset[1] + 8, offset[2]:offset[2] + 10], 0, -1)
@@ -257,8 +262,9 @@ def test_accumulate_fold_finalize_bitwise(lib, fp16):
     accum = _native.NNX_ACCUM_NNUNET_F16 if fp16 else _native.NNX_ACCUM_F32
     for off in offsets:
         pred = (rng.standard_normal((8, *patch, K)) * 4).astype(np.float32)
+        dpred = dev(pred)
         _native.check(lib.nnx_sw_accumulate(
-            dev(pred).data_ptr(), 8, _native.ints(FLIPS_3AX), K, _native.ints(patch), dg.data_ptr(),
+            dpred.data_ptr(), 8, _native.ints(FLIPS_3AX), K, _native.ints(patch), dg.data_ptr(),
             _native.ints(off), _native.i64s(padded), accum, dacc.data_ptr(), dnorm.data_ptr(), stream()))
         s = pred[0]
         for v in range(1, 8):
@@ -306,7 +312,8 @@ def test_finalize_ties_choose_earliest_and_flags_nonfinite(lib):
                      dtype=np.float32)
     labels = torch.empty(4, dtype=torch.int16, device="cuda")
     invalid = torch.zeros(1, dtype=torch.int32, device="cuda")
-    _native.check(lib.nnx_sw_fold_finalize(dev(total).data_ptr(), 3, 4, 1, _native.NNX_ACCUM_F32, None,
+    dtotal = dev(total)
+    _native.check(lib.nnx_sw_fold_finalize(dtotal.data_ptr(), 3, 4, 1, _native.NNX_ACCUM_F32, None,
                                            labels.data_ptr(), invalid.data_ptr(), stream()))
     np.testing.assert_array_equal(host(labels).view(np.uint16), [0, 1, 65535, 65535])
     assert int(host(invalid)[0]) == 2
@@ -316,7 +323,8 @@ def test_count_nonfinite(lib):
     x = np.zeros(100000, dtype=np.float32)
     x[[5, 77, 99999]] = [np.inf, np.nan, -np.inf]
     count = torch.empty(1, dtype=torch.int32, device="cuda")
-    _native.check(lib.nnx_count_nonfinite(dev(x).data_ptr(), x.size, count.data_ptr(), stream()))
+    dx = dev(x)
+    _native.check(lib.nnx_count_nonfinite(dx.data_ptr(), x.size, count.data_ptr(), stream()))
     assert int(host(count)[0]) == 3
 
 

@@ -52,7 +52,7 @@ CASES = {
     "tiny-bottleneck": (ResidualEncoderUNetSpec(1, 3, (4, 8, 16), K3 * 3, ((1, 1, 1), (2, 2, 2), (2, 2, 2)),
                                                 (1, 2, 2), (1, 1), bottleneck_channels=(2, 4, 8)),
                         (8, 8, 8), 1, True),
-    "resenc-L": (resenc_spec(), (64, 32, 32), 1, True),
+    "resenc-L": (resenc_spec(), (128, 64, 64), 1, True),
 }
 
 
