@@ -70,6 +70,109 @@ def synthetic_ct(shape=VOLUME_SHAPE, seed: int = 101):
     return vol[None]
 
 
+def _short_kernel(name: str) -> str:
+    import re
+
+    name = name.replace("void ", "").replace("nnx::(anonymous namespace)::", "")
+    return re.split(r"\((?!anon)", name)[0].strip()
+
+
+def kernel_class_of(short: str) -> str | None:
+    """Map a rocprof kernel name to the profiling class bench.py reports."""
+    variants = {"igemm_kernel<8, 2, 4, 1>": "conv3d_igemm_m512n32",
+                "igemm_kernel<4, 4, 4, 1>": "conv3d_igemm_m256n64",
+                "igemm_kernel<4, 4, 2, 2>": "conv3d_igemm_m128n128",
+                "igemm_kernel<2, 4, 4, 1>": "conv3d_igemm_m128n64",
+                "igemm_kernel<2, 4, 2, 2>": "conv3d_igemm_m64n128"}
+    return variants.get(short)
+
+
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_liver_tile.md"
+
+
+def summarize_profiles(directory: str) -> None:
+    """Write the profiles/ summaries from rocprofv3 CSV output under `directory`
+    (prof_trace/liver_kernel_stats.csv, prof_fetch/fetch_counter_collection.csv,
+    prof_write/write_counter_collection.csv)."""
+    import csv
+    from collections import defaultdict
+
+    base = Path(directory)
+    out = ROOT / "profiles"
+    out.mkdir(exist_ok=True)
+    rows = list(csv.DictReader(open(base / "prof_trace" / "liver_kernel_stats.csv")))
+    lines = [
+        "# Kernel time, liver-shape sliding window (121 tiles x 8 views), warmup + 1 timed case",
+        "",
+        "Command (repo root on the MI355X box):",
+        "",
+        "    rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof_trace -o liver -- \\",
+        "        python -u bench.py --warmup 1 --steps 1 --no-cpu-baseline --no-pcie",
+        "",
+        "Calls count the warmup and the timed case (2 cases). Average = per launch.",
+        "",
+        "| kernel | calls | total ms | average us | % |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for r in rows[:16]:
+        lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | {float(r['TotalDurationNs'])/1e6:.1f} | "
+                     f"{float(r['AverageNs'])/1e3:.1f} | {float(r['Percentage']):.2f} |")
+    (out / "kernel_stats_liver.md").write_text("\n".join(lines) + "\n")
+
+    per = defaultdict(dict)
+    for name, ctr in (("prof_fetch/fetch_counter_collection.csv", "FETCH_SIZE"),
+                      ("prof_write/write_counter_collection.csv", "WRITE_SIZE")):
+        for r in csv.DictReader(open(base / name)):
+            if r["Counter_Name"] == ctr:
+                per[(int(r["Dispatch_Id"]), _short_kernel(r["Kernel_Name"]))][ctr] = float(r["Counter_Value"])
+    calib = {k[1]: v for k, v in per.items() if "neg_kernel" in k[1]}
+    (neg,) = calib.values()
+    gib_kib = 1024.0 * 1024.0
+    fetch_factor = gib_kib / neg["FETCH_SIZE"]
+    write_factor = gib_kib / neg["WRITE_SIZE"]
+    agg = defaultdict(lambda: [0, 0.0, 0.0])
+    for (_, short), v in per.items():
+        a = agg[short]
+        a[0] += 1
+        a[1] += v.get("FETCH_SIZE", 0.0) * fetch_factor * 1024
+        a[2] += v.get("WRITE_SIZE", 0.0) * write_factor * 1024
+    lines = [
+        "# HBM traffic per launch, one liver tile (8 views of 128^3) through the forward",
+        "",
+        "Commands (repo root on the MI355X box), one counter per run:",
+        "",
+        "    rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/prof_fetch -o fetch -- \\",
+        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --copy-calibration",
+        "    rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/prof_write -o write -- \\",
+        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --copy-calibration",
+        "",
+        f"Calibration: torch.neg over 1 GiB (reads 1 GiB, writes 1 GiB) reads FETCH_SIZE = "
+        f"{neg['FETCH_SIZE']:.0f} KiB and WRITE_SIZE = {neg['WRITE_SIZE']:.0f} KiB, so FETCH_SIZE is "
+        f"scaled by {fetch_factor:.4f} and WRITE_SIZE by {write_factor:.4f}.",
+        "",
+        "| kernel | launches | fetch bytes/launch | write bytes/launch | traffic bytes/launch |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for short, (n, f, w) in sorted(agg.items(), key=lambda kv: -(kv[1][1] + kv[1][2])):
+        if n == 0 or (f + w) / n < 1e6:
+            continue
+        cls = kernel_class_of(short) or short
+        lines.append(f"| `{cls}` | {n} | {f/n:.4g} | {w/n:.4g} | {(f+w)/n:.4g} |")
+    TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
+    print(f"wrote {out / 'kernel_stats_liver.md'} and {TRAFFIC_FILE}")
+
+
+def measured_traffic(kernel_class: str) -> float | None:
+    """HBM bytes per launch of `kernel_class` from the committed counter summary."""
+    if not TRAFFIC_FILE.is_file():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        cells = [c.strip().strip("`") for c in line.strip("|").split("|")]
+        if len(cells) == 5 and cells[0] == kernel_class:
+            return float(cells[4])
+    return None
+
+
 def cpu_baseline(spec, weights) -> dict:
     """Oracle forward of one 128^3 view on the host cores + one tile's accumulation,
     extrapolated to the case (968 forwards, 121 accumulations)."""
@@ -128,9 +231,17 @@ def main() -> int:
     parser.add_argument("--tiles-per-batch", type=int, default=1)
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-pcie", action="store_true")
+    parser.add_argument("--copy-calibration", action="store_true",
+                        help="first run a plain 1 GiB read + 1 GiB write elementwise kernel "
+                             "(torch.neg) whose HBM counters calibrate FETCH_SIZE/WRITE_SIZE")
+    parser.add_argument("--summarize-profiles", metavar="DIR",
+                        help="write the profiles/ summaries from rocprofv3 CSV output in DIR and exit")
     parser.add_argument("--shape", type=int, nargs=3, default=VOLUME_SHAPE[1:],
                         help="volume size (Z Y X); the default is the liver case")
     args = parser.parse_args()
+    if args.summarize_profiles:
+        summarize_profiles(args.summarize_profiles)
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
               "(tiles would shard across GPUs with one halo exchange; see the design notes). "
@@ -147,6 +258,12 @@ def main() -> int:
 
     torch.cuda.set_device(0)
     device = torch.device("cuda", 0)
+    if args.copy_calibration:
+        src = torch.ones(1 << 28, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     shape = (1, *args.shape)
     spec = liver_spec()
     weights = random_weights(spec, seed=1)
@@ -193,7 +310,8 @@ def main() -> int:
         achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 2),
                     "peak": PEAK_FP32_MFMA_TFLOPS, "unit": "TFLOP/s",
-                    "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4), "traffic": None}
+                    "frac": round(achieved / PEAK_FP32_MFMA_TFLOPS, 4),
+                    "traffic": measured_traffic(dominant)}
     else:
         achieved = d["bytes"] / (d["ms"] * 1e-3) / 1e9
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
