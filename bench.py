@@ -228,7 +228,8 @@ def main() -> int:
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=1)
     parser.add_argument("--warmup", type=int, default=1)
-    parser.add_argument("--tiles-per-batch", type=int, default=1)
+    parser.add_argument("--tiles-per-batch", type=int, default=None,
+                        help="tiles per forward batch (default: the library's, 4 tiles = 32 views)")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-pcie", action="store_true")
     parser.add_argument("--copy-calibration", action="store_true",
@@ -357,7 +358,7 @@ def main() -> int:
                          f"({nforwards} forwards), 1 fold, fp32 Gaussian accumulation, argmax labels"),
             "tiles": ntiles,
             "forwards": nforwards,
-            "views_per_forward_batch": 8 * args.tiles_per_batch,
+            "views_per_forward_batch": 8 * min(args.tiles_per_batch or 4, ntiles),
         },
         "ms_per_forward": round(step_s * 1e3 / nforwards, 3),
         "ms_per_tile": round(step_s * 1e3 / ntiles, 2),

@@ -14,6 +14,7 @@
 // K is walked in chunks of 8 input channels; inside a chunk and tap, lane slot s = l / 16
 // owns channels 2s and 2s+1, consumed by two MFMA k-steps, so every lane reads one
 // float2 of A from LDS and one float2 of B (weights) from global memory per tap.
+#include <cstdlib>
 #include <string>
 
 #include "nnx_internal.h"
@@ -125,11 +126,49 @@ struct IgemmArgs {
   int hz, hy, hx;
   int tz, ty, tx;
   int ntn, nwg;
+  float4* stats;  // optional per-tile InstanceNorm partials [b][tile][cout] (mean, M2, n, 0)
 };
 
-template <int MB, int NB, int WM, int WN>
-__global__ __launch_bounds__(64 * WM* WN) void igemm_kernel(IgemmArgs a) {
+// A zeroed 16-byte line: padding voxels of an asynchronously loaded halo read from here.
+__device__ __align__(16) float g_zero_line[4];
+
+// Decode halo float4 `f` of the current chunk into its global source (or the zero line).
+struct HaloSource {
+  const float* src;
+  int C, cb;
+};
+
+__device__ __forceinline__ const float* halo_address(const IgemmArgs& a, const HaloSource& hs,
+                                                     int f, int nf4, int b, int iz0, int iy0,
+                                                     int ix0, int hyx) {
+  const float* zero = g_zero_line;
+  if (f >= nf4) return zero;
+  const int v = f >> 1, h = f & 1;
+  const int hz_ = v / hyx;
+  const int rem = v - hz_ * hyx;
+  const int hy_ = rem / a.hx;
+  const int hx_ = rem - hy_ * a.hx;
+  const int z = iz0 + hz_, yy = iy0 + hy_, xx = ix0 + hx_;
+  if ((unsigned)z >= (unsigned)a.id || (unsigned)yy >= (unsigned)a.ih ||
+      (unsigned)xx >= (unsigned)a.iw)
+    return zero;
+  return hs.src + ((((int64_t)b * a.id + z) * a.ih + yy) * a.iw + xx) * hs.C + hs.cb + h * 4;
+}
+
+__device__ __forceinline__ HaloSource halo_source(const IgemmArgs& a, int chunk) {
+  if (chunk < a.chunks0) return HaloSource{a.x0, a.c0, chunk * kChunk};
+  return HaloSource{a.x1, a.c1, (chunk - a.chunks0) * kChunk};
+}
+
+// ASYNC: both inputs have channel counts that are multiples of 8, so every halo float4 is
+// a whole aligned 16-byte line (or padding).  The halo is double-buffered in LDS and the
+// next chunk is fetched with global_load_lds_dwordx4 (direct to LDS, no registers), one
+// load per thread per tap, so the in-order vmcnt waits for the weight prefetch never
+// wait on a whole halo.  Otherwise the halo goes through registers between barriers.
+template <int MB, int NB, int WM, int WN, bool ASYNC>
+__global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
   extern __shared__ __align__(16) float lds[];
+  constexpr int NT = 64 * WM * WN;
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -168,90 +207,229 @@ __global__ __launch_bounds__(64 * WM* WN) void igemm_kernel(IgemmArgs a) {
 
   const int hyx = a.hy * a.hx;
   const int hvox = a.hz * hyx;
-  const f2* lds2 = reinterpret_cast<const f2*>(lds);
+  const int nf4 = hvox * 2;                 // float4 lines per chunk
+  const int dpt = (nf4 + NT - 1) / NT;      // lines per thread
+  const int buf_floats = dpt * NT * 4;      // one (padded) halo buffer
+  // wave-uniform LDS base of this wave's lines in round j: (j*NT + wave*64) lines
+  const int wave_line0 = __builtin_amdgcn_readfirstlane(wave * 64);
+
+  if constexpr (ASYNC) {
+    const HaloSource hs = halo_source(a, 0);
+    for (int j = 0; j < dpt; ++j) {
+      const float* g = halo_address(a, hs, j * NT + tid, nf4, b, iz0, iy0, ix0, hyx);
+      __builtin_amdgcn_global_load_lds(
+          g, (__attribute__((address_space(3))) void*)(lds + (j * NT + wave_line0) * 4), 16, 0, 0);
+    }
+  }
 
   for (int chunk = 0; chunk < a.chunks; ++chunk) {
-    const float* src;
-    int C, cb;
-    if (chunk < a.chunks0) {
-      src = a.x0;
-      C = a.c0;
-      cb = chunk * kChunk;
+    const float* cur = lds + (ASYNC ? (chunk & 1) * buf_floats : 0);
+    if constexpr (ASYNC) {
+      __builtin_amdgcn_s_waitcnt(0);  // this thread's halo lines have landed in LDS
+      __syncthreads();                // ... and everyone's; the other buffer is free
     } else {
-      src = a.x1;
-      C = a.c1;
-      cb = (chunk - a.chunks0) * kChunk;
-    }
-    __syncthreads();
-    for (int i = tid; i < hvox * 2; i += blockDim.x) {
-      const int v = i >> 1, h = i & 1;
-      const int hz_ = v / hyx;
-      const int rem = v - hz_ * hyx;
-      const int hy_ = rem / a.hx;
-      const int hx_ = rem - hy_ * a.hx;
-      const int z = iz0 + hz_, yy = iy0 + hy_, xx = ix0 + hx_;
-      f4 val = {0.f, 0.f, 0.f, 0.f};
-      if ((unsigned)z < (unsigned)a.id && (unsigned)yy < (unsigned)a.ih &&
-          (unsigned)xx < (unsigned)a.iw) {
-        const int c = cb + h * 4;
-        const int64_t off = ((((int64_t)b * a.id + z) * a.ih + yy) * a.iw + xx) * C + c;
-        if ((C & 3) == 0) {
-          if (c < C) val = *reinterpret_cast<const f4*>(src + off);
-        } else {
+      const HaloSource hs = halo_source(a, chunk);
+      __syncthreads();
+      for (int i = tid; i < nf4; i += NT) {
+        const int v = i >> 1, h = i & 1;
+        const int hz_ = v / hyx;
+        const int rem = v - hz_ * hyx;
+        const int hy_ = rem / a.hx;
+        const int hx_ = rem - hy_ * a.hx;
+        const int z = iz0 + hz_, yy = iy0 + hy_, xx = ix0 + hx_;
+        f4 val = {0.f, 0.f, 0.f, 0.f};
+        if ((unsigned)z < (unsigned)a.id && (unsigned)yy < (unsigned)a.ih &&
+            (unsigned)xx < (unsigned)a.iw) {
+          const int c = hs.cb + h * 4;
+          const int64_t off = ((((int64_t)b * a.id + z) * a.ih + yy) * a.iw + xx) * hs.C + c;
+          if ((hs.C & 3) == 0) {
+            if (c < hs.C) val = *reinterpret_cast<const f4*>(hs.src + off);
+          } else {
 #pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (c + q < C) val[q] = src[off + q];
+            for (int q = 0; q < 4; ++q)
+              if (c + q < hs.C) val[q] = hs.src[off + q];
+          }
+        }
+        *reinterpret_cast<f4*>(lds + v * kChunk + h * 4) = val;
+      }
+      __syncthreads();
+    }
+    const f2* lds2 = reinterpret_cast<const f2*>(cur);
+    const bool prefetch = ASYNC && chunk + 1 < a.chunks;
+    const HaloSource next_hs = halo_source(a, chunk + 1 < a.chunks ? chunk + 1 : chunk);
+    float* next_buf = lds + (((chunk + 1) & 1) * buf_floats);
+
+    // Taps are walked in (kz, ky, kx) order with the next tap's A (LDS) and B (weights)
+    // fragments requested before the current tap's MFMAs, so their latency overlaps
+    // the 2*MB*NB matrix instructions.  The packed weights hold whole column groups,
+    // so the B loads need no guard.
+    const f2* wc = a.w + (int64_t)chunk * a.taps * a.nblk * 64 + nbk0 * 64 + lane;
+    const int tap_stride = a.nblk * 64;
+    f2 av[MB], bv[NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) av[mb] = lds2[hbase[mb] * 4 + slot];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bv[nb] = wc[nb * 64];
+    int kx = 0, ky = 0, kz = 0;
+    for (int tap = 0; tap < a.taps; ++tap) {
+      if (tap + 1 < a.taps) {
+        if (++kx == a.kw) {
+          kx = 0;
+          if (++ky == a.kh) {
+            ky = 0;
+            ++kz;
+          }
         }
       }
-      *reinterpret_cast<f4*>(lds + v * kChunk + h * 4) = val;
-    }
-    __syncthreads();
-    const f2* wc = a.w + (int64_t)chunk * a.taps * a.nblk * 64 + lane;
-    for (int kz = 0; kz < a.kd; ++kz) {
-      for (int ky = 0; ky < a.kh; ++ky) {
-        for (int kx = 0; kx < a.kw; ++kx) {
-          const int tap = (kz * a.kh + ky) * a.kw + kx;
-          const int toff = (kz * a.hy + ky) * a.hx + kx;
-          f2 av[MB], bv[NB];
+      const int ntap = tap + 1 < a.taps ? tap + 1 : tap;
+      const int ntoff = (kz * a.hy + ky) * a.hx + kx;
+      f2 an[MB], bn[NB];
 #pragma unroll
-          for (int mb = 0; mb < MB; ++mb) av[mb] = lds2[(hbase[mb] + toff) * 4 + slot];
-          const f2* wt = wc + ((int64_t)tap * a.nblk + nbk0) * 64;
+      for (int mb = 0; mb < MB; ++mb) an[mb] = lds2[(hbase[mb] + ntoff) * 4 + slot];
+      const f2* wt = wc + (int64_t)ntap * tap_stride;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) bn[nb] = wt[nb * 64];
+      if (prefetch && tap < dpt) {
+        // round `tap` of the next chunk's halo lines, after this tap's weight loads;
+        // rounds left over when dpt > taps are issued after the last tap
+        const float* g = halo_address(a, next_hs, tap * NT + tid, nf4, b, iz0, iy0, ix0, hyx);
+        __builtin_amdgcn_global_load_lds(
+            g, (__attribute__((address_space(3))) void*)(next_buf + (tap * NT + wave_line0) * 4),
+            16, 0, 0);
+      }
+#pragma unroll
+      for (int e = 0; e < 2; ++e)
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
           for (int nb = 0; nb < NB; ++nb)
-            bv[nb] = (nbk0 + nb < a.nblk) ? wt[nb * 64] : f2{0.f, 0.f};
+            acc[mb][nb] = mfma16x16x4(av[mb][e], bv[nb][e], acc[mb][nb]);
 #pragma unroll
-          for (int e = 0; e < 2; ++e)
+      for (int mb = 0; mb < MB; ++mb) av[mb] = an[mb];
 #pragma unroll
-            for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-              for (int nb = 0; nb < NB; ++nb)
-                acc[mb][nb] = mfma16x16x4(av[mb][e], bv[nb][e], acc[mb][nb]);
-        }
+      for (int nb = 0; nb < NB; ++nb) bv[nb] = bn[nb];
+    }
+    if (prefetch) {
+      for (int j = a.taps; j < dpt; ++j) {
+        const float* g = halo_address(a, next_hs, j * NT + tid, nf4, b, iz0, iy0, ix0, hyx);
+        __builtin_amdgcn_global_load_lds(
+            g, (__attribute__((address_space(3))) void*)(next_buf + (j * NT + wave_line0) * 4), 16,
+            0, 0);
       }
     }
   }
 
   // Epilogue: D[4*slot + r][row] of block (mb, nb) -> voxel 16*(wm*MB+mb) + 4*slot + r,
-  // channel (nbk0+nb)*16 + row; the bias is added as a separate float32 addition.
+  // channel (nbk0+nb)*16 + row; the bias is added as a separate float32 addition.  The
+  // passes below stream over the accumulator blocks and recompute voxel validity, so the
+  // epilogue needs fewer registers than the main loop (which sets the occupancy).
+  float bias_n[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = (nbk0 + nb) * 16 + row;
+    bias_n[nb] = (a.bias && n < a.cout) ? a.bias[n] : 0.f;
+  }
+  const bool has_bias = a.bias != nullptr;
+  auto voxel_ok = [&](int mb, int r, int* z, int* yy, int* xx) {
+    const int v = 16 * (wm * MB + mb) + 4 * slot + r;
+    const int vx = v % a.bx;
+    const int vy = (v / a.bx) % a.by;
+    const int vz = v / (a.bx * a.by);
+    *z = oz0 + vz;
+    *yy = oy0 + vy;
+    *xx = ox0 + vx;
+    return *z < a.od && *yy < a.oh && *xx < a.ow;
+  };
+  if (a.stats) {
+    // InstanceNorm partials of this tile, two-pass over the registers: the tile mean of
+    // every channel (lane sums, xor-shuffles over the 4 row slots, then the WM waves
+    // through LDS), then the centred sum of squares about it.
+    constexpr int NWG = 16 * NB * WN;
+    float* red = lds;  // WM * NWG floats; the halo is no longer read
+    const float cnt = (float)((a.od - oz0 < a.bz ? a.od - oz0 : a.bz) *
+                              (a.oh - oy0 < a.by ? a.oh - oy0 : a.by) *
+                              (a.ow - ox0 < a.bx ? a.ow - ox0 : a.bx));
+    float part[NB], mean[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) part[nb] = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int z, yy, xx;
+        if (voxel_ok(mb, r, &z, &yy, &xx)) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            part[nb] += has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+        }
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      part[nb] += __shfl_xor(part[nb], 16);
+      part[nb] += __shfl_xor(part[nb], 32);
+    }
+    __syncthreads();
+    if (slot == 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      float t = 0.f;
+      for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
+      mean[nb] = t / cnt;
+      part[nb] = 0.f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int z, yy, xx;
+        if (voxel_ok(mb, r, &z, &yy, &xx)) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const float v = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+            const float d = v - mean[nb];
+            part[nb] = fmaf(d, d, part[nb]);
+          }
+        }
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      part[nb] += __shfl_xor(part[nb], 16);
+      part[nb] += __shfl_xor(part[nb], 32);
+    }
+    __syncthreads();
+    if (slot == 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
+    }
+    __syncthreads();
+    if (wm == 0 && slot == 0) {
+      const int tile_s = (tzi * a.ty + tyi) * a.tx + txi;
+      const int spt = a.tz * a.ty * a.tx;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int n = (nbk0 + nb) * 16 + row;
+        float t = 0.f;
+        for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
+        if (n < a.cout)
+          a.stats[((int64_t)b * spt + tile_s) * a.cout + n] = make_float4(mean[nb], t, cnt, 0.f);
+      }
+    }
+  }
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int v = 16 * (wm * MB + mb) + 4 * slot + r;
-      const int vx = v % a.bx;
-      const int vy = (v / a.bx) % a.by;
-      const int vz = v / (a.bx * a.by);
-      const int z = oz0 + vz, yy = oy0 + vy, xx = ox0 + vx;
-      if (z < a.od && yy < a.oh && xx < a.ow) {
-        const int64_t ob = ((((int64_t)b * a.od + z) * a.oh + yy) * a.ow + xx) * a.cout;
+      int z, yy, xx;
+      if (voxel_ok(mb, r, &z, &yy, &xx)) {
+        float* yrow = a.y + ((((int64_t)b * a.od + z) * a.oh + yy) * a.ow + xx) * a.cout;
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
           const int n = (nbk0 + nb) * 16 + row;
-          if (n < a.cout) {
-            float val = acc[mb][nb][r];
-            if (a.bias) val = val + a.bias[n];
-            a.y[ob + n] = val;
-          }
+          if (n < a.cout) yrow[n] = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
         }
       }
     }
@@ -270,7 +448,11 @@ constexpr Variant kVarC{4, 4, 2, 2};  // M 128, N 128
 constexpr Variant kVarD{2, 4, 4, 1};  // M 128, N 64
 constexpr Variant kVarE{2, 4, 2, 2};  // M 64,  N 128
 
-constexpr int64_t kMaxHaloBytes = 64 * 1024;
+// LDS budget per workgroup: one halo buffer of up to 64 KB (register path) or two of up
+// to 32 KB each (asynchronous double-buffered path); lines are padded to whole rounds of
+// the 256 threads.
+constexpr int64_t kMaxLdsBytes = 64 * 1024;
+constexpr int kThreads = 256;
 
 struct Box {
   int z, y, x;
@@ -278,7 +460,11 @@ struct Box {
   int64_t tiles;
 };
 
-Box choose_box(const Variant& v, const ConvGeom& g) {
+int64_t halo_buffer_bytes(int64_t halo_voxels) {
+  return ceil_div(halo_voxels * 2, kThreads) * kThreads * 16;
+}
+
+Box choose_box(const Variant& v, const ConvGeom& g, bool double_buffer) {
   const int m = v.m();
   Box best{};
   bool have = false;
@@ -297,7 +483,7 @@ Box choose_box(const Variant& v, const ConvGeom& g) {
       c.hy = (by - 1) * g.s[1] + g.k[1];
       c.hx = (bx - 1) * g.s[2] + g.k[2];
       const int64_t halo = (int64_t)c.hz * c.hy * c.hx;
-      if (halo * kChunk * 4 > kMaxHaloBytes) continue;
+      if (halo_buffer_bytes(halo) * (double_buffer ? 2 : 1) > kMaxLdsBytes) continue;
       c.tiles = ceil_div(g.out[0], bz) * ceil_div(g.out[1], by) * ceil_div(g.out[2], bx);
       // MFMA rows actually computed (padding waste) dominate; halo traffic breaks ties.
       const double score = (double)c.tiles * m + 0.25 * (double)c.tiles * halo;
@@ -313,13 +499,20 @@ Box choose_box(const Variant& v, const ConvGeom& g) {
 }
 
 template <int MB, int NB, int WM, int WN>
-void launch_igemm(const IgemmArgs& a, int nwg, size_t lds_bytes, hipStream_t st, double flops,
+void launch_igemm(const IgemmArgs& a, int nwg, bool async, hipStream_t st, double flops,
                   double bytes) {
   static const std::string name = "conv3d_igemm_m" + std::to_string(16 * MB * WM) + "n" +
                                   std::to_string(16 * NB * WN);
+  constexpr int nt = 64 * WM * WN;
+  const int64_t lines = (int64_t)a.hz * a.hy * a.hx * 2;
+  const size_t buf_bytes = (size_t)ceil_div(lines, nt) * nt * 16;
   ProfScope prof(name.c_str(), flops, bytes, st);
-  hipLaunchKernelGGL((igemm_kernel<MB, NB, WM, WN>), dim3(nwg), dim3(64 * WM * WN), lds_bytes,
-                     st, a);
+  if (async)
+    hipLaunchKernelGGL((igemm_kernel<MB, NB, WM, WN, true>), dim3(nwg), dim3(nt), 2 * buf_bytes,
+                       st, a);
+  else
+    hipLaunchKernelGGL((igemm_kernel<MB, NB, WM, WN, false>), dim3(nwg), dim3(nt), buf_bytes, st,
+                       a);
   launch_check("conv3d_igemm");
 }
 
@@ -525,10 +718,16 @@ ConvGeom make_conv_geom(int batch, const int* in_size, const int* ksize, const i
   return g;
 }
 
+// Column blocks of the packed conv weights are padded to whole groups of kBlockGroup so
+// that every variant's workgroup (WN*NB <= 8 blocks) reads its weights unguarded.
+constexpr int kBlockGroup = 8;
+
+int conv_packed_nblk(int cout) { return (int)(ceil_div(ceil_div(cout, 16), kBlockGroup) * kBlockGroup); }
+
 int64_t conv_packed_floats(int cout, const int* ksize, int c1, int c2) {
   const int64_t taps = (int64_t)ksize[0] * ksize[1] * ksize[2];
   const int64_t chunks = ceil_div(c1, kChunk) + ceil_div(c2, kChunk);
-  const int64_t nblk = ceil_div(cout, 16);
+  const int64_t nblk = conv_packed_nblk(cout);
   return chunks * taps * nblk * 64 * 2;
 }
 
@@ -538,7 +737,7 @@ void conv_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int 
   const int taps = ksize[0] * ksize[1] * ksize[2];
   const int chunks1 = (int)ceil_div(c1, kChunk);
   const int chunks = chunks1 + (int)ceil_div(c2, kChunk);
-  const int nblk = (int)ceil_div(cout, 16);
+  const int nblk = conv_packed_nblk(cout);
   const int64_t total = (int64_t)chunks * taps * nblk * 64;
   const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 65536);
   hipLaunchKernelGGL(pack_conv_weight_kernel, dim3(blocks), dim3(256), 0, st, d_w,
@@ -546,20 +745,60 @@ void conv_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int 
   launch_check("conv3d_pack_weight");
 }
 
-void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
-                  const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st) {
-  require(x1 && y && packed, "convolution pointers must not be null");
-  require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
+namespace {
+
+struct IgemmPlan {
+  Variant v;
+  Box box;
+  bool async;
+};
+
+IgemmPlan plan_igemm(const ConvGeom& g, int cout, int c1, int c2) {
   const bool stride1 = g.s[0] == 1 && g.s[1] == 1 && g.s[2] == 1;
   const int64_t vox = (int64_t)g.out[0] * g.out[1] * g.out[2];
-  Variant v;
+  IgemmPlan p{};
   if (cout <= 32)
-    v = stride1 ? kVarA : kVarD;
+    p.v = stride1 ? kVarA : kVarD;
   else if (cout <= 64)
-    v = stride1 ? kVarB : kVarD;
+    p.v = stride1 ? kVarB : kVarD;
   else
-    v = (vox * g.batch <= 8192) ? kVarE : kVarC;
-  const Box box = choose_box(v, g);
+    p.v = (vox * g.batch <= 8192) ? kVarE : kVarC;
+  // The asynchronous path needs whole 8-channel lines and a double-buffered halo that fits.
+  // The register-staged halo measured faster than the DMA path on every liver layer
+  // (70-82 % vs 63-78 % of fp32 MFMA peak), so the DMA path is opt-in.
+  static const char* halo_mode = std::getenv("NNX_IGEMM_HALO");
+  p.async = halo_mode && std::string(halo_mode) == "async" && c1 % kChunk == 0 &&
+            c2 % kChunk == 0;
+  bool found = false;
+  if (p.async) {
+    try {
+      p.box = choose_box(p.v, g, true);
+      found = true;
+    } catch (const Error&) {
+      p.async = false;
+    }
+  }
+  if (!found) p.box = choose_box(p.v, g, false);
+  return p;
+}
+
+}  // namespace
+
+int conv_stats_tiles(const ConvGeom& g, int cout, int c1, int c2) {
+  const Box box = plan_igemm(g, cout, c1, c2).box;
+  return (int)(ceil_div(g.out[0], box.z) * ceil_div(g.out[1], box.y) * ceil_div(g.out[2], box.x));
+}
+
+void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
+                  const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st,
+                  float4* stats) {
+  require(x1 && y && packed, "convolution pointers must not be null");
+  require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
+  const IgemmPlan plan = plan_igemm(g, cout, c1, c2);
+  const Variant v = plan.v;
+  const Box box = plan.box;
+  const bool async = plan.async;
+  const int64_t vox = (int64_t)g.out[0] * g.out[1] * g.out[2];
   IgemmArgs a{};
   a.x0 = x1;
   a.x1 = x2;
@@ -577,7 +816,7 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
   a.oh = g.out[1];
   a.ow = g.out[2];
   a.cout = cout;
-  a.nblk = (int)ceil_div(cout, 16);
+  a.nblk = conv_packed_nblk(cout);
   a.kd = g.k[0];
   a.kh = g.k[1];
   a.kw = g.k[2];
@@ -601,22 +840,22 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
   const int64_t nwg = (int64_t)g.batch * a.tz * a.ty * a.tx * a.ntn;
   require(nwg < (1LL << 31), "convolution grid too large");
   a.nwg = (int)nwg;
-  const size_t lds = (size_t)box.hz * box.hy * box.hx * kChunk * sizeof(float);
+  a.stats = stats;
   // Algorithmic work: 2*C_in*C_out*taps per output voxel; bytes: input, output, weights once.
   const double out_vox = (double)g.batch * vox;
   const double in_vox = (double)g.batch * g.in[0] * g.in[1] * g.in[2];
   const double flops = 2.0 * (c1 + c2) * cout * a.taps * out_vox;
   const double bytes = 4.0 * (in_vox * (c1 + c2) + out_vox * cout + (double)a.taps * (c1 + c2) * cout);
   if (v.MB == 8)
-    launch_igemm<8, 2, 4, 1>(a, a.nwg, lds, st, flops, bytes);
+    launch_igemm<8, 2, 4, 1>(a, a.nwg, async, st, flops, bytes);
   else if (v.MB == 4 && v.WN == 1)
-    launch_igemm<4, 4, 4, 1>(a, a.nwg, lds, st, flops, bytes);
+    launch_igemm<4, 4, 4, 1>(a, a.nwg, async, st, flops, bytes);
   else if (v.MB == 4)
-    launch_igemm<4, 4, 2, 2>(a, a.nwg, lds, st, flops, bytes);
+    launch_igemm<4, 4, 2, 2>(a, a.nwg, async, st, flops, bytes);
   else if (v.WN == 1)
-    launch_igemm<2, 4, 4, 1>(a, a.nwg, lds, st, flops, bytes);
+    launch_igemm<2, 4, 4, 1>(a, a.nwg, async, st, flops, bytes);
   else
-    launch_igemm<2, 4, 2, 2>(a, a.nwg, lds, st, flops, bytes);
+    launch_igemm<2, 4, 2, 2>(a, a.nwg, async, st, flops, bytes);
 }
 
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,

@@ -112,8 +112,13 @@ ConvGeom make_conv_geom(int batch, const int* in_size, const int* ksize, const i
 int64_t conv_packed_floats(int cout, const int* ksize, int c1, int c2);
 void conv_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int c2,
                       float* d_packed, hipStream_t st);
+// When `stats` is given, the epilogue also writes InstanceNorm partials
+// stats[(b * tiles + tile) * cout + c] = (tile mean, tile M2, tile voxel count, 0) of
+// (conv + bias); `tiles` = conv_stats_tiles(...) per batch item.
 void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
-                  const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st);
+                  const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st,
+                  float4* stats = nullptr);
+int conv_stats_tiles(const ConvGeom& g, int cout, int c1, int c2);
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
                         const int* size, int cout, hipStream_t st);
 
@@ -130,6 +135,14 @@ void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int ch
                     const float* input_bias, const float* gamma, const float* beta, float eps,
                     bool act, float slope, const float* residual, void* ws, size_t ws_bytes,
                     hipStream_t st);
+// InstanceNorm from precomputed partials: merge (mean, M2, n) partials of each (b, c)
+// into (mean, gamma*rsqrt(var+eps)) params, then apply; `params` holds batch*channels float2.
+void instnorm_merge_partials(const float4* partials, int nparts, int batch, int64_t spatial,
+                             int channels, const float* gamma, float eps, float2* params,
+                             hipStream_t st);
+void instnorm_apply_params(const float* x, float* y, int batch, int64_t spatial, int channels,
+                           const float2* params, const float* input_bias, const float* beta,
+                           bool act, float slope, const float* residual, hipStream_t st);
 void avgpool3d(const float* x, float* y, int batch, const int* in_size, int channels,
                const int* kernel, hipStream_t st);
 

@@ -178,6 +178,45 @@ __global__ __launch_bounds__(256) void norm_merge_kernel(const float2* __restric
   }
 }
 
+// Same merge for partials that carry their own counts (per-tile partials written by the
+// convolution epilogue: (mean, M2, n, 0)).
+__global__ __launch_bounds__(256) void norm_merge_counted_kernel(const float4* __restrict__ partial,
+                                                                 float2* __restrict__ params,
+                                                                 const float* __restrict__ gamma,
+                                                                 int64_t S, int C, int nparts,
+                                                                 float eps) {
+  __shared__ double sn[256], sm[256], s2[256];
+  const int c = blockIdx.x;
+  const int b = blockIdx.y;
+  double n = 0.0, m = 0.0, m2 = 0.0;
+  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+    const float4 p = partial[((int64_t)b * nparts + i) * C + c];
+    chan_merge(n, m, m2, (double)p.z, (double)p.x, (double)p.y);
+  }
+  sn[threadIdx.x] = n;
+  sm[threadIdx.x] = m;
+  s2[threadIdx.x] = m2;
+  __syncthreads();
+  for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
+    if ((int)threadIdx.x < stride) {
+      double na = sn[threadIdx.x], ma = sm[threadIdx.x], m2a = s2[threadIdx.x];
+      chan_merge(na, ma, m2a, sn[threadIdx.x + stride], sm[threadIdx.x + stride],
+                 s2[threadIdx.x + stride]);
+      sn[threadIdx.x] = na;
+      sm[threadIdx.x] = ma;
+      s2[threadIdx.x] = m2a;
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    const double var = s2[0] / (double)S;
+    float varf = (float)(var > 0.0 ? var : 0.0);
+    float scale = 1.0f / sqrtf(varf + eps);
+    if (gamma) scale = gamma[c] * scale;
+    params[(int64_t)b * C + c] = make_float2((float)sm[0], scale);
+  }
+}
+
 template <int VW>
 __global__ __launch_bounds__(256) void norm_apply_kernel(
     const float* x, float* y, const float2* __restrict__ params, const float* __restrict__ in_bias,
@@ -335,12 +374,34 @@ void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int ch
                      gamma, spatial, channels, (int)l.nchunks, l.chunk_vox, eps);
   launch_check("instnorm merge");
   }
+  instnorm_apply_params(x, y, batch, spatial, channels, params, input_bias, beta, act, slope,
+                        residual, st);
+}
+
+void instnorm_merge_partials(const float4* partials, int nparts, int batch, int64_t spatial,
+                             int channels, const float* gamma, float eps, float2* params,
+                             hipStream_t st) {
+  require(partials && params, "instance normalisation partials must not be null");
+  require(nparts >= 1 && batch >= 1 && batch <= 65535 && channels >= 1, "invalid partial layout");
+  ProfScope prof("instnorm_merge", 0.0, 16.0 * (double)batch * nparts * channels, st);
+  hipLaunchKernelGGL(norm_merge_counted_kernel, dim3(channels, batch), dim3(256), 0, st, partials,
+                     params, gamma, spatial, channels, nparts, eps);
+  launch_check("instnorm merge partials");
+}
+
+void instnorm_apply_params(const float* x, float* y, int batch, int64_t spatial, int channels,
+                           const float2* params, const float* input_bias, const float* beta,
+                           bool act, float slope, const float* residual, hipStream_t st) {
+  require(x && y && params, "instance normalisation pointers must not be null");
+  require(channels <= 1024, "instance normalisation supports at most 1024 channels");
+  const int vw = channels % 4 == 0 ? 4 : 1;
+  const double nelem = (double)batch * spatial * channels;
   ProfScope prof("instnorm_apply", 0.0, 4.0 * nelem * (residual ? 3 : 2), st);
   const int64_t sc = spatial * channels;
-  const int64_t nvec = sc / l.vw;
+  const int64_t nvec = sc / vw;
   const int64_t blocks = std::min<int64_t>(ceil_div(nvec, 256 * 4), 16384);
   const size_t smem = (size_t)channels * 4 * sizeof(float);
-  if (l.vw == 4)
+  if (vw == 4)
     hipLaunchKernelGGL(norm_apply_kernel<4>, dim3((unsigned)std::max<int64_t>(blocks, 1), batch),
                        dim3(256), smem, st, x, y, params, input_bias, beta, residual, sc,
                        channels, act ? 1 : 0, slope);

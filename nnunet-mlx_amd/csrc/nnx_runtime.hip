@@ -173,6 +173,10 @@ struct Workspace {
   std::vector<std::unique_ptr<DevBuf>> bufs;
   DevBuf norm_ws;
   size_t norm_ws_bytes = 0;
+  DevBuf stats;   // per-tile InstanceNorm partials written by the conv epilogue
+  size_t stats_bytes = 0;
+  DevBuf params;  // (mean, scale) per (b, c)
+  size_t params_bytes = 0;
   float* get(size_t i) { return bufs[i]->as<float>(); }
 };
 
@@ -345,6 +349,8 @@ struct Planner {
   // During planning, records buffer sizes; during execution, hands out the same buffers.
   std::vector<size_t> sizes;
   size_t norm_ws = 0;
+  size_t stats = 0;
+  size_t params = 0;
   size_t next = 0;
   bool planning = true;
   Workspace* ws = nullptr;
@@ -367,23 +373,36 @@ struct Runner {
   void convnorm(const ConvNorm& c, const float* x1, const float* x2, const Shape3& in, float* out,
                 const Shape3& outs, const float* residual) {
     const int64_t vox = outs.vox();
-    const size_t nbytes = instnorm_workspace_bytes(n, vox, c.cout);
-    if (plan->planning) {
-      plan->norm_ws = std::max(plan->norm_ws, nbytes);
-      return;
-    }
-    const float* bias = pdev(m, c.pb);
-    if (c.direct) {
-      conv3d_direct_cin1(x1, pdev(m, c.pw), bias, out, n, in.d, c.cout, st);
-    } else {
-      const ConvGeom g = make_conv_geom(n, in.d, c.k, c.s);
-      conv3d_igemm(x1, c.cin1, x2, c.cin2, c.packed.as<float>(), bias, out, g, c.cout, st);
-    }
     // A residual block's last ConvNorm has no activation of its own; LeakyReLU follows the
     // residual addition (ResidualBlock.__call__), fused into the same apply pass.
     const bool act = c.act || residual != nullptr;
-    instnorm_lrelu(out, out, n, vox, c.cout, nullptr, pdev(m, c.pg), pdev(m, c.pbeta), m->eps,
-                   act, m->slope, residual, plan->ws->norm_ws.ptr, plan->ws->norm_ws_bytes, st);
+    if (c.direct) {
+      const size_t nbytes = instnorm_workspace_bytes(n, vox, c.cout);
+      if (plan->planning) {
+        plan->norm_ws = std::max(plan->norm_ws, nbytes);
+        return;
+      }
+      conv3d_direct_cin1(x1, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st);
+      instnorm_lrelu(out, out, n, vox, c.cout, nullptr, pdev(m, c.pg), pdev(m, c.pbeta), m->eps,
+                     act, m->slope, residual, plan->ws->norm_ws.ptr, plan->ws->norm_ws_bytes, st);
+      return;
+    }
+    // Implicit GEMM: the epilogue writes per-tile statistics, so the norm reads the
+    // tensor once (apply) instead of twice.
+    const ConvGeom g = make_conv_geom(n, in.d, c.k, c.s);
+    const int tiles = conv_stats_tiles(g, c.cout, c.cin1, c.cin2);
+    if (plan->planning) {
+      plan->stats = std::max(plan->stats, (size_t)n * tiles * c.cout * sizeof(float4));
+      plan->params = std::max(plan->params, (size_t)n * c.cout * sizeof(float2));
+      return;
+    }
+    float4* stats = plan->ws->stats.as<float4>();
+    float2* params = plan->ws->params.as<float2>();
+    conv3d_igemm(x1, c.cin1, x2, c.cin2, c.packed.as<float>(), pdev(m, c.pb), out, g, c.cout, st,
+                 stats);
+    instnorm_merge_partials(stats, tiles, n, vox, c.cout, pdev(m, c.pg), m->eps, params, st);
+    instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, pdev(m, c.pbeta), act,
+                          m->slope, residual, st);
   }
 
   // Returns the output buffer; *outs receives its spatial shape.
@@ -528,6 +547,14 @@ void ensure_workspace(nnx_model* m, int n, const Shape3& in) {
   if (plan.norm_ws > ws.norm_ws_bytes) {
     ws.norm_ws.ensure(plan.norm_ws);
     ws.norm_ws_bytes = plan.norm_ws;
+  }
+  if (plan.stats > ws.stats_bytes) {
+    ws.stats.ensure(plan.stats);
+    ws.stats_bytes = plan.stats;
+  }
+  if (plan.params > ws.params_bytes) {
+    ws.params.ensure(plan.params);
+    ws.params_bytes = plan.params;
   }
   ws.n = n;
   ws.in = in;

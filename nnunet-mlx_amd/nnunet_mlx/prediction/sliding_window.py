@@ -172,7 +172,8 @@ class _Request:
         self.gaussian = torch.from_numpy(np.array(gaussian, copy=True)).to(device)
         self.device = device
         if tiles_per_batch is None:
-            tiles_per_batch = max(1, 8 // len(self.flips))
+            # about 32 views per forward: enough workgroups for the 8^3 and 4^3 stages
+            tiles_per_batch = max(1, 32 // len(self.flips))
         self.tiles_per_batch = int(tiles_per_batch)
         self._offsets_c = _native.ints([v for o in self.offsets for v in o])
         self._flips_c = _native.ints(self.flips)
