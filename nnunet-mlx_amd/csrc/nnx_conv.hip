@@ -123,6 +123,7 @@ struct IgemmArgs {
   int kd, kh, kw, taps;
   int sd, sh, sw, pd, ph, pw;
   int bz, by, bx;
+  int lbx, lbxy;  // log2(bx), log2(bx*by): box dims are powers of two
   int hz, hy, hx;
   int tz, ty, tx;
   int ntn, nwg;
@@ -192,9 +193,9 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
     const int v = 16 * (wm * MB + mb) + row;
-    const int vx = v % a.bx;
-    const int vy = (v / a.bx) % a.by;
-    const int vz = v / (a.bx * a.by);
+    const int vx = v & (a.bx - 1);
+    const int vy = (v >> a.lbx) & (a.by - 1);
+    const int vz = v >> a.lbxy;
     hbase[mb] = ((vz * a.sd) * a.hy + vy * a.sh) * a.hx + vx * a.sw;
   }
   const int nbk0 = nt * (WN * NB) + wn * NB;
@@ -332,9 +333,9 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
   const bool has_bias = a.bias != nullptr;
   auto voxel_ok = [&](int mb, int r, int* z, int* yy, int* xx) {
     const int v = 16 * (wm * MB + mb) + 4 * slot + r;
-    const int vx = v % a.bx;
-    const int vy = (v / a.bx) % a.by;
-    const int vz = v / (a.bx * a.by);
+    const int vx = v & (a.bx - 1);
+    const int vy = (v >> a.lbx) & (a.by - 1);
+    const int vz = v >> a.lbxy;
     *z = oz0 + vz;
     *yy = oy0 + vy;
     *xx = ox0 + vx;
@@ -528,41 +529,51 @@ __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restric
                                                           int D, int H, int W, int cout) {
   __shared__ float ws[27 * 64];
   __shared__ float bs[64];
+  extern __shared__ float out_s[];  // 256 voxels x (cout + 1): padded rows, no bank conflicts
   for (int i = threadIdx.x; i < 27 * cout; i += blockDim.x) ws[i] = w[i];
   for (int i = threadIdx.x; i < cout; i += blockDim.x) bs[i] = bias ? bias[i] : 0.f;
   __syncthreads();
-  const int64_t vox = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  if (vox >= nvox) return;
-  const int xx = (int)(vox % W);
-  const int yy = (int)((vox / W) % H);
-  const int zz = (int)((vox / ((int64_t)W * H)) % D);
-  const int64_t plane = (vox / ((int64_t)W * H * D)) * D;
-  float taps[27];
+  const int64_t v0 = blockIdx.x * (int64_t)blockDim.x;
+  const int64_t vox = v0 + threadIdx.x;
+  const int stride = cout + 1;
+  if (vox < nvox) {
+    const int xx = (int)(vox % W);
+    const int yy = (int)((vox / W) % H);
+    const int zz = (int)((vox / ((int64_t)W * H)) % D);
+    const int64_t plane = (vox / ((int64_t)W * H * D)) * D;
+    float taps[27];
 #pragma unroll
-  for (int kd = 0; kd < 3; ++kd) {
-    const int d = zz + kd - 1;
+    for (int kd = 0; kd < 3; ++kd) {
+      const int d = zz + kd - 1;
 #pragma unroll
-    for (int kh = 0; kh < 3; ++kh) {
-      const int h = yy + kh - 1;
+      for (int kh = 0; kh < 3; ++kh) {
+        const int h = yy + kh - 1;
 #pragma unroll
-      for (int kw = 0; kw < 3; ++kw) {
-        const int ww = xx + kw - 1;
-        const bool inside = d >= 0 && d < D && h >= 0 && h < H && ww >= 0 && ww < W;
-        taps[(kd * 3 + kh) * 3 + kw] = inside ? x[((plane + d) * H + h) * W + ww] : 0.f;
+        for (int kw = 0; kw < 3; ++kw) {
+          const int ww = xx + kw - 1;
+          const bool inside = d >= 0 && d < D && h >= 0 && h < H && ww >= 0 && ww < W;
+          taps[(kd * 3 + kh) * 3 + kw] = inside ? x[((plane + d) * H + h) * W + ww] : 0.f;
+        }
       }
     }
-  }
-  const bool has_bias = bias != nullptr;
-  for (int c = 0; c < cout; c += 4) {
-    f4 out;
+    const bool has_bias = bias != nullptr;
+    for (int c = 0; c < cout; ++c) {
+      float sum = 0.f;
 #pragma unroll
-    for (int q = 0; q < 4; ++q) {
-      float s = 0.f;
-#pragma unroll
-      for (int t = 0; t < 27; ++t) s = fmaf(taps[t], ws[(c + q) * 27 + t], s);
-      out[q] = has_bias ? s + bs[c + q] : s;
+      for (int t = 0; t < 27; ++t) sum = fmaf(taps[t], ws[c * 27 + t], sum);
+      out_s[threadIdx.x * stride + c] = has_bias ? sum + bs[c] : sum;
     }
-    *reinterpret_cast<f4*>(y + vox * cout + c) = out;
+  }
+  __syncthreads();
+  // the block's voxels are contiguous in NDHWC: write them as one coalesced run
+  const int64_t nv = nvox - v0 < (int64_t)blockDim.x ? nvox - v0 : (int64_t)blockDim.x;
+  const int total4 = (int)(nv * cout / 4);
+  f4* dst = reinterpret_cast<f4*>(y + v0 * cout);
+  for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
+    const int e = e4 * 4;
+    const int v = e / cout, c = e - v * cout;
+    const float* src = out_s + v * stride + c;
+    dst[e4] = f4{src[0], src[1], src[2], src[3]};
   }
 }
 
@@ -588,7 +599,7 @@ struct PwArgs {
 };
 
 template <int MB, int NB, int WM, int WN>
-__global__ __launch_bounds__(64 * WM* WN) void pw_gemm_kernel(PwArgs a) {
+__global__ __launch_bounds__(64 * WM* WN, 2) void pw_gemm_kernel(PwArgs a) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -613,17 +624,28 @@ __global__ __launch_bounds__(64 * WM* WN) void pw_gemm_kernel(PwArgs a) {
   for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+  // The next chunk's A (rows of the input) and B (packed weights, whole column groups, no
+  // guard) fragments are requested before the current chunk's MFMAs.
   const f2* wl = a.w + nbk0 * 64 + lane;
-  for (int chunk = 0; chunk < a.chunks; ++chunk) {
-    const int k = chunk * kChunk + 2 * slot;
-    f2 av[MB], bv[NB];
+  const int chunk_stride = a.nblk * 64;
+  f2 av[MB], bv[NB];
+  {
+    const bool ok = 2 * slot < a.cin;
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
-      av[mb] = (k < a.cin) ? *reinterpret_cast<const f2*>(arow[mb] + chunk * kChunk)
-                           : f2{0.f, 0.f};
+      av[mb] = ok ? *reinterpret_cast<const f2*>(arow[mb]) : f2{0.f, 0.f};
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-      bv[nb] = (nbk0 + nb < a.nblk) ? wl[((int64_t)chunk * a.nblk + nb) * 64] : f2{0.f, 0.f};
+    for (int nb = 0; nb < NB; ++nb) bv[nb] = wl[nb * 64];
+  }
+  for (int chunk = 0; chunk < a.chunks; ++chunk) {
+    const int nchunk = chunk + 1 < a.chunks ? chunk + 1 : chunk;
+    const bool ok = nchunk * kChunk + 2 * slot < a.cin;
+    f2 an[MB], bn[NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+      an[mb] = ok ? *reinterpret_cast<const f2*>(arow[mb] + nchunk * kChunk) : f2{0.f, 0.f};
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bn[nb] = wl[(int64_t)nchunk * chunk_stride + nb * 64];
 #pragma unroll
     for (int e = 0; e < 2; ++e)
 #pragma unroll
@@ -631,34 +653,64 @@ __global__ __launch_bounds__(64 * WM* WN) void pw_gemm_kernel(PwArgs a) {
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb)
           acc[mb][nb] = mfma16x16x4(av[mb][e], bv[nb][e], acc[mb][nb]);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) av[mb] = an[mb];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) bv[nb] = bn[nb];
   }
+  // Output voxel of (row m, column n) = base(m) + delta(n), with base(m) the voxel
+  // (b, z*KD, y*KH, x*KW) of the output grid and delta(n) the kernel offset (az, ay, ax).
+  // Columns are decoded once; each lane's 4 consecutive rows of a block are decoded once
+  // and stepped, all in 32-bit arithmetic.
   const int ncols = a.kd * a.kh * a.kw * a.cout;
   const int od = a.id * a.kd, oh = a.ih * a.kh, ow = a.iw * a.kw;
+  int col_o[NB], col_delta[NB];
+  bool col_ok[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = (nbk0 + nb) * 16 + row;
+    col_ok[nb] = n < ncols;
+    const int o = n % a.cout;
+    const int off = n / a.cout;
+    const int ax = off % a.kw;
+    const int ay = (off / a.kw) % a.kh;
+    const int az = off / (a.kw * a.kh);
+    col_o[nb] = o;
+    col_delta[nb] = (az * oh + ay) * ow + ax;
+  }
+  const float* bias = a.bias;
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb) {
+    const int64_t mfirst = m0 + mb * 16 + 4 * slot;
+    if (mfirst >= a.M) continue;
+    int m32 = (int)mfirst;  // rows fit in 32 bits (checked on the host)
+    int xx = m32 % a.iw;
+    int t = m32 / a.iw;
+    int yy = t % a.ih;
+    t /= a.ih;
+    int zz = t % a.id;
+    int bb = t / a.id;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int64_t m = m0 + mb * 16 + 4 * slot + r;
-      if (m >= a.M) continue;
-      const int xx = (int)(m % a.iw);
-      const int yy = (int)((m / a.iw) % a.ih);
-      const int64_t zb = m / ((int64_t)a.iw * a.ih);  // b * id + z
-      const int zz = (int)(zb % a.id);
-      const int64_t bb = zb / a.id;
+      if (mfirst + r < a.M) {
+        const int64_t base = (((int64_t)bb * od + zz * a.kd) * oh + yy * a.kh) * (int64_t)ow + xx * a.kw;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const int n = (nbk0 + nb) * 16 + row;
-        if (n >= ncols) continue;
-        const int o = n % a.cout;
-        const int off = n / a.cout;
-        const int ax = off % a.kw;
-        const int ay = (off / a.kw) % a.kh;
-        const int az = off / (a.kw * a.kh);
-        const int64_t ov =
-            ((bb * od + (zz * a.kd + az)) * oh + (yy * a.kh + ay)) * (int64_t)ow + (xx * a.kw + ax);
-        float val = acc[mb][nb][r];
-        if (a.bias) val = val + a.bias[o];
-        a.y[ov * a.cout + o] = val;
+        for (int nb = 0; nb < NB; ++nb) {
+          if (!col_ok[nb]) continue;
+          float val = acc[mb][nb][r];
+          if (bias) val = val + bias[col_o[nb]];
+          a.y[(base + col_delta[nb]) * a.cout + col_o[nb]] = val;
+        }
+      }
+      if (++xx == a.iw) {
+        xx = 0;
+        if (++yy == a.ih) {
+          yy = 0;
+          if (++zz == a.id) {
+            zz = 0;
+            ++bb;
+          }
+        }
       }
     }
   }
@@ -682,19 +734,51 @@ __global__ __launch_bounds__(256) void conv1x1_kernel(const float* __restrict__ 
   for (int o = 0; o < cout; ++o) {
     float s = 0.f;
     const float* wr = ws + o * cin;
-    if ((cin & 3) == 0) {
-      for (int c = 0; c < cin; c += 4) {
-        const f4 v = *reinterpret_cast<const f4*>(xr + c);
-        s = fmaf(v[0], wr[c], s);
-        s = fmaf(v[1], wr[c + 1], s);
-        s = fmaf(v[2], wr[c + 2], s);
-        s = fmaf(v[3], wr[c + 3], s);
-      }
-    } else {
-      for (int c = 0; c < cin; ++c) s = fmaf(xr[c], wr[c], s);
-    }
+    for (int c = 0; c < cin; ++c) s = fmaf(xr[c], wr[c], s);
     y[vox * cout + o] = bias ? s + bias[o] : s;
   }
+}
+
+// Head for narrow inputs (C_in <= 63): the block's 256 input rows are loaded into LDS with
+// coalesced float4 reads (rows padded to C_in + 1 floats), each thread forms its voxel's
+// outputs (fma chain over channels, then + bias), and the outputs leave as one run.
+__global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ w,
+                                                             const float* __restrict__ bias,
+                                                             float* __restrict__ y, int64_t nvox,
+                                                             int cin, int cout) {
+  extern __shared__ float smem[];
+  float* ws = smem;                          // cout * cin
+  float* xs = smem + cout * cin;             // 256 * (cin + 1)
+  float* os = xs + 256 * (cin + 1);          // 256 * cout
+  for (int i = threadIdx.x; i < cout * cin; i += blockDim.x) ws[i] = w[i];
+  const int64_t v0 = blockIdx.x * (int64_t)blockDim.x;
+  const int nv = (int)(nvox - v0 < 256 ? nvox - v0 : 256);
+  const float4* src = reinterpret_cast<const float4*>(x + v0 * cin);
+  const int total4 = nv * cin / 4;
+  for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
+    const float4 v = src[e4];
+    const int e = e4 * 4;
+    const int r = e / cin, c = e - r * cin;
+    float* d = xs + r * (cin + 1) + c;
+    d[0] = v.x;
+    d[1] = v.y;
+    d[2] = v.z;
+    d[3] = v.w;
+  }
+  __syncthreads();
+  if ((int)threadIdx.x < nv) {
+    const float* xr = xs + threadIdx.x * (cin + 1);
+    for (int o = 0; o < cout; ++o) {
+      float s = 0.f;
+      const float* wr = ws + o * cin;
+      for (int c = 0; c < cin; ++c) s = fmaf(xr[c], wr[c], s);
+      os[threadIdx.x * cout + o] = bias ? s + bias[o] : s;
+    }
+  }
+  __syncthreads();
+  float* dst = y + v0 * cout;
+  for (int e = threadIdx.x; e < nv * cout; e += blockDim.x) dst[e] = os[e];
 }
 
 }  // namespace
@@ -830,6 +914,9 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
   a.bz = box.z;
   a.by = box.y;
   a.bx = box.x;
+  require((box.x & (box.x - 1)) == 0 && (box.y & (box.y - 1)) == 0, "box dims must be powers of two");
+  a.lbx = __builtin_ctz(box.x);
+  a.lbxy = __builtin_ctz(box.x * box.y);
   a.hz = box.hz;
   a.hy = box.hy;
   a.hx = box.hx;
@@ -866,14 +953,17 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
   const int64_t nvox = (int64_t)batch * size[0] * size[1] * size[2];
   require(nvox >= 1, "empty convolution input");
   ProfScope prof("conv3d_direct_cin1", 2.0 * 27 * cout * (double)nvox, 4.0 * (double)nvox * (1 + cout), st);
-  hipLaunchKernelGGL(direct_cin1_kernel, dim3((unsigned)ceil_div(nvox, 256)), dim3(256), 0, st,
-                     x, w, bias, y, nvox, size[0], size[1], size[2], cout);
+  hipLaunchKernelGGL(direct_cin1_kernel, dim3((unsigned)ceil_div(nvox, 256)), dim3(256),
+                     (size_t)256 * (cout + 1) * sizeof(float), st, x, w, bias, y, nvox, size[0],
+                     size[1], size[2], cout);
   launch_check("conv3d_direct_small_cin");
 }
 
+int tconv_packed_nblk(int64_t ncols) { return (int)(ceil_div(ceil_div(ncols, 16), kBlockGroup) * kBlockGroup); }
+
 int64_t tconv_packed_floats(int cout, const int* ksize, int cin) {
   const int64_t koff = (int64_t)ksize[0] * ksize[1] * ksize[2];
-  return ceil_div(cin, kChunk) * ceil_div(koff * cout, 16) * 64 * 2;
+  return ceil_div(cin, kChunk) * tconv_packed_nblk(koff * cout) * 64 * 2;
 }
 
 void tconv_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float* d_packed,
@@ -881,7 +971,7 @@ void tconv_pack_weight(const float* d_w, int cout, const int* ksize, int cin, fl
   require(cout >= 1 && cin >= 1, "invalid transposed-convolution channel counts");
   const int koff = ksize[0] * ksize[1] * ksize[2];
   const int chunks = (int)ceil_div(cin, kChunk);
-  const int nblk = (int)ceil_div((int64_t)koff * cout, 16);
+  const int nblk = tconv_packed_nblk((int64_t)koff * cout);
   const int64_t total = (int64_t)chunks * nblk * 64;
   const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 65536);
   hipLaunchKernelGGL(pack_tconv_weight_kernel, dim3(blocks), dim3(256), 0, st, d_w,
@@ -901,7 +991,7 @@ void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bia
   a.w = reinterpret_cast<const f2*>(packed);
   a.chunks = (int)ceil_div(cin, kChunk);
   const int ncols = ksize[0] * ksize[1] * ksize[2] * cout;
-  a.nblk = (int)ceil_div(ncols, 16);
+  a.nblk = tconv_packed_nblk(ncols);
   a.bias = bias;
   a.y = y;
   a.cout = cout;
@@ -912,6 +1002,7 @@ void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bia
   a.ih = in_size[1];
   a.iw = in_size[2];
   constexpr int MB = 4, NB = 4, WM = 2, WN = 2;
+  require(a.M < (1LL << 31) - 64, "transposed-convolution input too large");
   a.ntn = (int)ceil_div(ncols, 16 * NB * WN);
   const int64_t nwg = ceil_div(a.M, 16 * MB * WM) * a.ntn;
   require(nwg < (1LL << 31), "transposed-convolution grid too large");
@@ -929,8 +1020,13 @@ void conv1x1(const float* x, int cin, const float* w, const float* bias, float* 
           "1x1 convolution weight too large for the head kernel");
   require(voxels >= 1, "empty 1x1 convolution input");
   ProfScope prof("conv1x1_head", 2.0 * (double)voxels * cin * cout, 4.0 * (double)voxels * (cin + cout), st);
-  hipLaunchKernelGGL(conv1x1_kernel, dim3((unsigned)ceil_div(voxels, 256)), dim3(256),
-                     (size_t)cin * cout * sizeof(float), st, x, w, bias, y, voxels, cin, cout);
+  const size_t staged = ((size_t)cin * cout + 256 * (cin + 1) + 256 * cout) * sizeof(float);
+  if (cin % 4 == 0 && staged <= 64 * 1024)
+    hipLaunchKernelGGL(conv1x1_staged_kernel, dim3((unsigned)ceil_div(voxels, 256)), dim3(256),
+                       staged, st, x, w, bias, y, voxels, cin, cout);
+  else
+    hipLaunchKernelGGL(conv1x1_kernel, dim3((unsigned)ceil_div(voxels, 256)), dim3(256),
+                       (size_t)cin * cout * sizeof(float), st, x, w, bias, y, voxels, cin, cout);
   launch_check("conv1x1");
 }
 
