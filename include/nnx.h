@@ -46,6 +46,11 @@ const char* nnx_version(void);
 #define NNX_ARCH_PLAIN 0
 #define NNX_ARCH_RESIDUAL 1
 #define NNX_PRECISION_FP32 0
+/* Float32 semantics (float32 inputs, weights, accumulation and outputs) with the 3-D
+ * convolutions after the first one computed as three fp16 MFMA products of split operands
+ * (x = hi + lo), see nnx_conv3d_split.  Meets the float32 logits tolerance; activations
+ * must stay below 65504 in magnitude (they are normalised, so they do). */
+#define NNX_PRECISION_FP32_SPLIT 1
 
 typedef struct nnx_spec {
   int arch;              /* NNX_ARCH_PLAIN or NNX_ARCH_RESIDUAL */
@@ -65,7 +70,7 @@ typedef struct nnx_spec {
   int stem_channels; /* residual only; 0 means features[0] */
   const int* bottleneck_channels; /* residual only: n_stages entries for BottleneckD, or NULL
                                      for BasicBlockD */
-  int precision;     /* NNX_PRECISION_FP32 */
+  int precision;     /* NNX_PRECISION_FP32 or NNX_PRECISION_FP32_SPLIT */
 } nnx_spec;
 
 typedef struct nnx_model nnx_model;
@@ -178,6 +183,21 @@ int nnx_conv3d_igemm(const float* d_x1, int c1, const float* d_x2, int c2,
                      const float* d_packed, const float* d_bias, float* d_y, int batch,
                      const int* in_size, int cout, const int* ksize, const int* stride,
                      void* stream);
+
+/* The same convolution with float32 operands split into fp16 halves (hi = fp16(v),
+ * lo = fp16(v - hi)) and summed as hi*hi + hi*lo + lo*hi on fp16 MFMA with float32
+ * accumulation (relative error ~2^-21 per product).  Weights are multiplied by `scale`,
+ * a power of two from nnx_split_weight_scale(max |w|), before the split (so their low
+ * halves stay normal); outputs are multiplied by 1/scale (exact).  Packed size in bytes.
+ * Replaces the same reference calls as nnx_conv3d_igemm. */
+float nnx_split_weight_scale(float max_abs); /* 0 for a negative or non-finite argument */
+size_t nnx_conv3d_split_packed_bytes(int cout, const int* ksize, int c1, int c2);
+int nnx_conv3d_split_pack_weight(const float* d_weight /* (Cout,kD,kH,kW,c1+c2) */, int cout,
+                                 const int* ksize, int c1, int c2, float scale, void* d_packed,
+                                 void* stream);
+int nnx_conv3d_split(const float* d_x1, int c1, const float* d_x2, int c2, const void* d_packed,
+                     float scale, const float* d_bias, float* d_y, int batch, const int* in_size,
+                     int cout, const int* ksize, const int* stride, void* stream);
 
 /* One-input-channel 3x3x3 stride-1 pad-1 convolution, fma over taps in (kd,kh,kw) order.
  * Replaces single_channel_conv3d (src/nnunet_mlx/kernels/metal_single_channel_conv.py:32-97). */

@@ -14,6 +14,7 @@
 // K is walked in chunks of 8 input channels; inside a chunk and tap, lane slot s = l / 16
 // owns channels 2s and 2s+1, consumed by two MFMA k-steps, so every lane reads one
 // float2 of A from LDS and one float2 of B (weights) from global memory per tap.
+#include <cmath>
 #include <cstdlib>
 #include <string>
 
@@ -128,6 +129,9 @@ struct IgemmArgs {
   int tz, ty, tx;
   int ntn, nwg;
   float4* stats;  // optional per-tile InstanceNorm partials [b][tile][cout] (mean, M2, n, 0)
+  const uint4* w16;   // split-fp16 packed weights (x3 kernel)
+  int ntg;            // tap groups of 4 (x3 kernel)
+  float out_scale;    // 1 / weight scale (x3 kernel)
 };
 
 // A zeroed 16-byte line: padding voxels of an asynchronously loaded halo read from here.
@@ -159,6 +163,137 @@ __device__ __forceinline__ const float* halo_address(const IgemmArgs& a, const H
 __device__ __forceinline__ HaloSource halo_source(const IgemmArgs& a, int chunk) {
   if (chunk < a.chunks0) return HaloSource{a.x0, a.c0, chunk * kChunk};
   return HaloSource{a.x1, a.c1, (chunk - a.chunks0) * kChunk};
+}
+
+// Shared epilogue of the implicit-GEMM kernels.  acc holds D blocks: D[4*slot + r][row] of
+// block (mb, nb) is voxel 16*(wm*MB+mb) + 4*slot + r of the box and channel
+// (nbk0+nb)*16 + row.  Values are first multiplied by out_scale (a power of two undoing a
+// weight scale, exact; skipped when 1), then the bias is added as a separate float32
+// addition; optional fused InstanceNorm partials, then the stores.
+template <int MB, int NB, int WM, int WN>
+__device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB][NB], float* lds,
+                                               int wm, int wn, int slot, int row, int nbk0, int b,
+                                               int tzi, int tyi, int txi, int oz0, int oy0, int ox0,
+                                               float out_scale) {
+  if (out_scale != 1.0f) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = acc[mb][nb] * out_scale;
+  }
+  // The passes below stream over the accumulator blocks and recompute voxel validity, so the
+  // epilogue needs fewer registers than the main loop (which sets the occupancy).
+  float bias_n[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = (nbk0 + nb) * 16 + row;
+    bias_n[nb] = (a.bias && n < a.cout) ? a.bias[n] : 0.f;
+  }
+  const bool has_bias = a.bias != nullptr;
+  auto voxel_ok = [&](int mb, int r, int* z, int* yy, int* xx) {
+    const int v = 16 * (wm * MB + mb) + 4 * slot + r;
+    const int vx = v & (a.bx - 1);
+    const int vy = (v >> a.lbx) & (a.by - 1);
+    const int vz = v >> a.lbxy;
+    *z = oz0 + vz;
+    *yy = oy0 + vy;
+    *xx = ox0 + vx;
+    return *z < a.od && *yy < a.oh && *xx < a.ow;
+  };
+  if (a.stats) {
+    // InstanceNorm partials of this tile, two-pass over the registers: the tile mean of
+    // every channel (lane sums, xor-shuffles over the 4 row slots, then the WM waves
+    // through LDS), then the centred sum of squares about it.
+    constexpr int NWG = 16 * NB * WN;
+    float* red = lds;  // WM * NWG floats; the halo is no longer read
+    const float cnt = (float)((a.od - oz0 < a.bz ? a.od - oz0 : a.bz) *
+                              (a.oh - oy0 < a.by ? a.oh - oy0 : a.by) *
+                              (a.ow - ox0 < a.bx ? a.ow - ox0 : a.bx));
+    float part[NB], mean[NB];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) part[nb] = 0.f;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int z, yy, xx;
+        if (voxel_ok(mb, r, &z, &yy, &xx)) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            part[nb] += has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+        }
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      part[nb] += __shfl_xor(part[nb], 16);
+      part[nb] += __shfl_xor(part[nb], 32);
+    }
+    __syncthreads();
+    if (slot == 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      float t = 0.f;
+      for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
+      mean[nb] = t / cnt;
+      part[nb] = 0.f;
+    }
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        int z, yy, xx;
+        if (voxel_ok(mb, r, &z, &yy, &xx)) {
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb) {
+            const float v = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+            const float d = v - mean[nb];
+            part[nb] = fmaf(d, d, part[nb]);
+          }
+        }
+      }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      part[nb] += __shfl_xor(part[nb], 16);
+      part[nb] += __shfl_xor(part[nb], 32);
+    }
+    __syncthreads();
+    if (slot == 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
+    }
+    __syncthreads();
+    if (wm == 0 && slot == 0) {
+      const int tile_s = (tzi * a.ty + tyi) * a.tx + txi;
+      const int spt = a.tz * a.ty * a.tx;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int n = (nbk0 + nb) * 16 + row;
+        float t = 0.f;
+        for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
+        if (n < a.cout)
+          a.stats[((int64_t)b * spt + tile_s) * a.cout + n] = make_float4(mean[nb], t, cnt, 0.f);
+      }
+    }
+  }
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      int z, yy, xx;
+      if (voxel_ok(mb, r, &z, &yy, &xx)) {
+        float* yrow = a.y + ((((int64_t)b * a.od + z) * a.oh + yy) * a.ow + xx) * a.cout;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int n = (nbk0 + nb) * 16 + row;
+          if (n < a.cout) yrow[n] = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+        }
+      }
+    }
+  }
 }
 
 // ASYNC: both inputs have channel counts that are multiples of 8, so every halo float4 is
@@ -320,120 +455,236 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
     }
   }
 
-  // Epilogue: D[4*slot + r][row] of block (mb, nb) -> voxel 16*(wm*MB+mb) + 4*slot + r,
-  // channel (nbk0+nb)*16 + row; the bias is added as a separate float32 addition.  The
-  // passes below stream over the accumulator blocks and recompute voxel validity, so the
-  // epilogue needs fewer registers than the main loop (which sets the occupancy).
-  float bias_n[NB];
+  igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
+                                 ox0, 1.0f);
+}
+
+
+// ---------------------------------------------------------------------------------
+// "fp32-class" implicit GEMM on v_mfma_f32_16x16x32_f16.  Every float32 operand is split
+// into fp16 halves x = hi + lo (hi = fp16(x), lo = fp16(x - hi), the difference being
+// exact in float32); each product uses hi*hi + hi*lo + lo*hi (the lo*lo term, ~2^-22
+// relative, is dropped) with float32 accumulation.  Weights are scaled by a power of two
+// before splitting so their low halves stay normal; the epilogue multiplies by the
+// inverse (exact).  One MFMA's K = 32 spans 4 taps x 8 channels: lane slot s = lane/16
+// takes tap 4g + s of tap group g and channels 0..7 of the chunk, i.e. one 16-byte read
+// from each of the two LDS planes (hi, lo: [halo voxel][8 halves]).  Taps beyond the
+// kernel (the last group of 27 taps) read voxel 0 and meet zero weights.
+// ---------------------------------------------------------------------------------
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4 mfma16x16x32h(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ void split_half(float v, _Float16& hi, _Float16& lo) {
+  hi = (_Float16)v;
+  lo = (_Float16)(v - (float)hi);
+}
+
+template <int MB, int NB, int WM, int WN>
+__global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  constexpr int NT = 64 * WM * WN;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+  const int logical = xcd_remap(blockIdx.x, a.nwg);
+  const int nt = logical % a.ntn;
+  int tile = logical / a.ntn;
+  const int txi = tile % a.tx;
+  tile /= a.tx;
+  const int tyi = tile % a.ty;
+  tile /= a.ty;
+  const int tzi = tile % a.tz;
+  const int b = tile / a.tz;
+  const int oz0 = tzi * a.bz, oy0 = tyi * a.by, ox0 = txi * a.bx;
+  const int iz0 = oz0 * a.sd - a.pd, iy0 = oy0 * a.sh - a.ph, ix0 = ox0 * a.sw - a.pw;
+
+  const int row = lane & 15;
+  const int slot = lane >> 4;
+  int hbase[MB];
 #pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int n = (nbk0 + nb) * 16 + row;
-    bias_n[nb] = (a.bias && n < a.cout) ? a.bias[n] : 0.f;
-  }
-  const bool has_bias = a.bias != nullptr;
-  auto voxel_ok = [&](int mb, int r, int* z, int* yy, int* xx) {
-    const int v = 16 * (wm * MB + mb) + 4 * slot + r;
+  for (int mb = 0; mb < MB; ++mb) {
+    const int v = 16 * (wm * MB + mb) + row;
     const int vx = v & (a.bx - 1);
     const int vy = (v >> a.lbx) & (a.by - 1);
     const int vz = v >> a.lbxy;
-    *z = oz0 + vz;
-    *yy = oy0 + vy;
-    *xx = ox0 + vx;
-    return *z < a.od && *yy < a.oh && *xx < a.ow;
+    hbase[mb] = ((vz * a.sd) * a.hy + vy * a.sh) * a.hx + vx * a.sw;
+  }
+  const int nbk0 = nt * (WN * NB) + wn * NB;
+
+  f4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int hyx = a.hy * a.hx;
+  const int hvox = a.hz * hyx;
+  _Float16* hi_plane = reinterpret_cast<_Float16*>(lds);
+  _Float16* lo_plane = hi_plane + (size_t)hvox * kChunk;
+  const h8* hi8 = reinterpret_cast<const h8*>(hi_plane);
+  const h8* lo8 = reinterpret_cast<const h8*>(lo_plane);
+
+  // tap offset (in halo voxels) of this lane's tap in group g; padding taps read voxel 0
+  auto tap_offset = [&](int g) {
+    const int t = 4 * g + slot;
+    if (t >= a.taps) return -1;
+    const int kx = t % a.kw;
+    const int rest = t / a.kw;
+    const int ky = rest % a.kh;
+    const int kz = rest / a.kh;
+    return (kz * a.hy + ky) * a.hx + kx;
   };
-  if (a.stats) {
-    // InstanceNorm partials of this tile, two-pass over the registers: the tile mean of
-    // every channel (lane sums, xor-shuffles over the 4 row slots, then the WM waves
-    // through LDS), then the centred sum of squares about it.
-    constexpr int NWG = 16 * NB * WN;
-    float* red = lds;  // WM * NWG floats; the halo is no longer read
-    const float cnt = (float)((a.od - oz0 < a.bz ? a.od - oz0 : a.bz) *
-                              (a.oh - oy0 < a.by ? a.oh - oy0 : a.by) *
-                              (a.ow - ox0 < a.bx ? a.ow - ox0 : a.bx));
-    float part[NB], mean[NB];
+
+  for (int chunk = 0; chunk < a.chunks; ++chunk) {
+    const float* src;
+    int C, cb;
+    if (chunk < a.chunks0) {
+      src = a.x0;
+      C = a.c0;
+      cb = chunk * kChunk;
+    } else {
+      src = a.x1;
+      C = a.c1;
+      cb = (chunk - a.chunks0) * kChunk;
+    }
+    __syncthreads();
+    for (int i = tid; i < hvox * 2; i += NT) {
+      const int v = i >> 1, h = i & 1;
+      const int hz_ = v / hyx;
+      const int rem = v - hz_ * hyx;
+      const int hy_ = rem / a.hx;
+      const int hx_ = rem - hy_ * a.hx;
+      const int z = iz0 + hz_, yy = iy0 + hy_, xx = ix0 + hx_;
+      f4 val = {0.f, 0.f, 0.f, 0.f};
+      if ((unsigned)z < (unsigned)a.id && (unsigned)yy < (unsigned)a.ih &&
+          (unsigned)xx < (unsigned)a.iw) {
+        const int c = cb + h * 4;
+        const int64_t off = ((((int64_t)b * a.id + z) * a.ih + yy) * a.iw + xx) * C + c;
+        if ((C & 3) == 0) {
+          if (c < C) val = *reinterpret_cast<const f4*>(src + off);
+        } else {
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) part[nb] = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int z, yy, xx;
-        if (voxel_ok(mb, r, &z, &yy, &xx)) {
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-            part[nb] += has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+          for (int q = 0; q < 4; ++q)
+            if (c + q < C) val[q] = src[off + q];
         }
       }
+      h4 hv, lv;
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      part[nb] += __shfl_xor(part[nb], 16);
-      part[nb] += __shfl_xor(part[nb], 32);
-    }
-    __syncthreads();
-    if (slot == 0) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      float t = 0.f;
-      for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
-      mean[nb] = t / cnt;
-      part[nb] = 0.f;
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int z, yy, xx;
-        if (voxel_ok(mb, r, &z, &yy, &xx)) {
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            const float v = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
-            const float d = v - mean[nb];
-            part[nb] = fmaf(d, d, part[nb]);
-          }
-        }
+      for (int q = 0; q < 4; ++q) {
+        _Float16 hh, ll;
+        split_half(val[q], hh, ll);
+        hv[q] = hh;
+        lv[q] = ll;
       }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      part[nb] += __shfl_xor(part[nb], 16);
-      part[nb] += __shfl_xor(part[nb], 32);
+      *reinterpret_cast<h4*>(hi_plane + v * kChunk + h * 4) = hv;
+      *reinterpret_cast<h4*>(lo_plane + v * kChunk + h * 4) = lv;
     }
     __syncthreads();
-    if (slot == 0) {
+    // packed weights: [chunk][group][nblk][lane] x {hi h8, lo h8}
+    const uint4* wc = a.w16 + ((int64_t)chunk * a.ntg * a.nblk + nbk0) * 128 + lane * 2;
+    const int group_stride = a.nblk * 128;
+    h8 ah[MB], al[MB], bh[NB], bl[NB];
+    {
+      const int toff = tap_offset(0);
+      const int o = toff < 0 ? 0 : toff;
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
-    }
-    __syncthreads();
-    if (wm == 0 && slot == 0) {
-      const int tile_s = (tzi * a.ty + tyi) * a.tx + txi;
-      const int spt = a.tz * a.ty * a.tx;
+      for (int mb = 0; mb < MB; ++mb) {
+        ah[mb] = hi8[hbase[mb] + o];
+        al[mb] = lo8[hbase[mb] + o];
+      }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const int n = (nbk0 + nb) * 16 + row;
-        float t = 0.f;
-        for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
-        if (n < a.cout)
-          a.stats[((int64_t)b * spt + tile_s) * a.cout + n] = make_float4(mean[nb], t, cnt, 0.f);
+        const uint4 wh = wc[nb * 128], wl = wc[nb * 128 + 1];
+        bh[nb] = *reinterpret_cast<const h8*>(&wh);
+        bl[nb] = *reinterpret_cast<const h8*>(&wl);
+      }
+    }
+    for (int g = 0; g < a.ntg; ++g) {
+      const int ng = g + 1 < a.ntg ? g + 1 : g;
+      const int ntoff = tap_offset(ng);
+      const int no = ntoff < 0 ? 0 : ntoff;
+      h8 nah[MB], nal[MB], nbh[NB], nbl[NB];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        nah[mb] = hi8[hbase[mb] + no];
+        nal[mb] = lo8[hbase[mb] + no];
+      }
+      const uint4* wg = wc + (int64_t)ng * group_stride;
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint4 wh = wg[nb * 128], wl = wg[nb * 128 + 1];
+        nbh[nb] = *reinterpret_cast<const h8*>(&wh);
+        nbl[nb] = *reinterpret_cast<const h8*>(&wl);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          acc[mb][nb] = mfma16x16x32h(ah[mb], bh[nb], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(ah[mb], bl[nb], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(al[mb], bh[nb], acc[mb][nb]);
+        }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        ah[mb] = nah[mb];
+        al[mb] = nal[mb];
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        bh[nb] = nbh[nb];
+        bl[nb] = nbl[nb];
       }
     }
   }
+  igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
+                                 ox0, a.out_scale);
+}
+
+// Split-fp16 weight packing: packed[((chunk * groups + g) * nblk + nb) * 64 + lane] =
+// { hi h8, lo h8 } of scale * W[n][tap 4g + lane/16][cin(chunk, q)], q = 0..7.
+__global__ void pack_conv_weight_x3_kernel(const float* __restrict__ w, uint4* __restrict__ out,
+                                           int cout, int taps, int c1, int c2, int chunks1,
+                                           int chunks, int groups, int nblk, float scale) {
+  const int64_t total = (int64_t)chunks * groups * nblk * 64;
+  const int ctot = c1 + c2;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(i % 64);
+    int64_t r = i / 64;
+    const int nb = (int)(r % nblk);
+    r /= nblk;
+    const int g = (int)(r % groups);
+    const int chunk = (int)(r / groups);
+    const int n = nb * 16 + (lane & 15);
+    const int tap = 4 * g + (lane >> 4);
+    h8 hv, lv;
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      int z, yy, xx;
-      if (voxel_ok(mb, r, &z, &yy, &xx)) {
-        float* yrow = a.y + ((((int64_t)b * a.od + z) * a.oh + yy) * a.ow + xx) * a.cout;
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const int n = (nbk0 + nb) * 16 + row;
-          if (n < a.cout) yrow[n] = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
-        }
+    for (int q = 0; q < 8; ++q) {
+      int cin;
+      bool ok;
+      if (chunk < chunks1) {
+        cin = chunk * kChunk + q;
+        ok = cin < c1;
+      } else {
+        const int local = (chunk - chunks1) * kChunk + q;
+        ok = local < c2;
+        cin = c1 + local;
       }
+      float v = 0.f;
+      if (ok && n < cout && tap < taps) v = w[((int64_t)n * taps + tap) * ctot + cin] * scale;
+      _Float16 hh, ll;
+      split_half(v, hh, ll);
+      hv[q] = hh;
+      lv[q] = ll;
     }
+    out[i * 2] = *reinterpret_cast<const uint4*>(&hv);
+    out[i * 2 + 1] = *reinterpret_cast<const uint4*>(&lv);
   }
 }
 
@@ -515,6 +766,21 @@ void launch_igemm(const IgemmArgs& a, int nwg, bool async, hipStream_t st, doubl
     hipLaunchKernelGGL((igemm_kernel<MB, NB, WM, WN, false>), dim3(nwg), dim3(nt), buf_bytes, st,
                        a);
   launch_check("conv3d_igemm");
+}
+
+template <int MB, int NB, int WM, int WN>
+void launch_x3(const IgemmArgs& a, hipStream_t st, double flops, double bytes) {
+  static const std::string name = "conv3d_x3_m" + std::to_string(16 * MB * WM) + "n" +
+                                  std::to_string(16 * NB * WN);
+  constexpr int nt = 64 * WM * WN;
+  // two fp16 planes of [halo voxel][8] = 32 bytes per halo voxel; the epilogue reuses
+  // the first WM * 16 * NB * WN floats
+  const size_t halo_bytes = (size_t)a.hz * a.hy * a.hx * 32;
+  const size_t red_bytes = (size_t)WM * 16 * NB * WN * sizeof(float);
+  const size_t lds_bytes = halo_bytes > red_bytes ? halo_bytes : red_bytes;
+  ProfScope prof(name.c_str(), flops, bytes, st);
+  hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
+  launch_check("conv3d_x3");
 }
 
 // ---------------------------------------------------------------------------------
@@ -873,16 +1139,12 @@ int conv_stats_tiles(const ConvGeom& g, int cout, int c1, int c2) {
   return (int)(ceil_div(g.out[0], box.z) * ceil_div(g.out[1], box.y) * ceil_div(g.out[2], box.x));
 }
 
-void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
-                  const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st,
-                  float4* stats) {
-  require(x1 && y && packed, "convolution pointers must not be null");
-  require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
-  const IgemmPlan plan = plan_igemm(g, cout, c1, c2);
-  const Variant v = plan.v;
-  const Box box = plan.box;
-  const bool async = plan.async;
-  const int64_t vox = (int64_t)g.out[0] * g.out[1] * g.out[2];
+namespace {
+
+// Geometry, box and grid fields shared by both implicit-GEMM kernels.
+IgemmArgs igemm_args(const float* x1, int c1, const float* x2, int c2, const float* bias,
+                     float* y, const ConvGeom& g, int cout, const Variant& v, const Box& box,
+                     float4* stats) {
   IgemmArgs a{};
   a.x0 = x1;
   a.x1 = x2;
@@ -890,7 +1152,6 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
   a.c1 = c2;
   a.chunks0 = (int)ceil_div(c1, kChunk);
   a.chunks = a.chunks0 + (int)ceil_div(c2, kChunk);
-  a.w = reinterpret_cast<const f2*>(packed);
   a.bias = bias;
   a.y = y;
   a.id = g.in[0];
@@ -928,11 +1189,33 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
   require(nwg < (1LL << 31), "convolution grid too large");
   a.nwg = (int)nwg;
   a.stats = stats;
-  // Algorithmic work: 2*C_in*C_out*taps per output voxel; bytes: input, output, weights once.
-  const double out_vox = (double)g.batch * vox;
+  a.out_scale = 1.0f;
+  return a;
+}
+
+// Algorithmic work: 2*C_in*C_out*taps per output voxel; bytes: input, output, weights once.
+void igemm_work(const ConvGeom& g, int c1, int c2, int cout, double* flops, double* bytes) {
+  const double out_vox = (double)g.batch * g.out[0] * g.out[1] * g.out[2];
   const double in_vox = (double)g.batch * g.in[0] * g.in[1] * g.in[2];
-  const double flops = 2.0 * (c1 + c2) * cout * a.taps * out_vox;
-  const double bytes = 4.0 * (in_vox * (c1 + c2) + out_vox * cout + (double)a.taps * (c1 + c2) * cout);
+  const double taps = (double)g.k[0] * g.k[1] * g.k[2];
+  *flops = 2.0 * (c1 + c2) * cout * taps * out_vox;
+  *bytes = 4.0 * (in_vox * (c1 + c2) + out_vox * cout + taps * (c1 + c2) * cout);
+}
+
+}  // namespace
+
+void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
+                  const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st,
+                  float4* stats) {
+  require(x1 && y && packed, "convolution pointers must not be null");
+  require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
+  const IgemmPlan plan = plan_igemm(g, cout, c1, c2);
+  const Variant v = plan.v;
+  const bool async = plan.async;
+  IgemmArgs a = igemm_args(x1, c1, x2, c2, bias, y, g, cout, v, plan.box, stats);
+  a.w = reinterpret_cast<const f2*>(packed);
+  double flops, bytes;
+  igemm_work(g, c1, c2, cout, &flops, &bytes);
   if (v.MB == 8)
     launch_igemm<8, 2, 4, 1>(a, a.nwg, async, st, flops, bytes);
   else if (v.MB == 4 && v.WN == 1)
@@ -943,6 +1226,107 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
     launch_igemm<2, 4, 4, 1>(a, a.nwg, async, st, flops, bytes);
   else
     launch_igemm<2, 4, 2, 2>(a, a.nwg, async, st, flops, bytes);
+}
+
+// ---- split-fp16 ("x3") implicit GEMM ----------------------------------------------
+
+float split_weight_scale(float max_abs) {
+  require(std::isfinite(max_abs) && max_abs >= 0.f, "weight magnitude must be finite");
+  if (max_abs == 0.f) return 1.0f;
+  // the power of two that brings max |w| into [2^14, 2^15): high halves stay below the
+  // fp16 maximum (65504) and low halves of all but tiny weights stay normal
+  int e;
+  std::frexp(max_abs, &e);  // max_abs = m * 2^e, m in [0.5, 1)
+  return std::ldexp(1.0f, 15 - e);
+}
+
+int conv_x3_groups(const int* ksize) { return (ksize[0] * ksize[1] * ksize[2] + 3) / 4; }
+
+int64_t conv_x3_packed_bytes(int cout, const int* ksize, int c1, int c2) {
+  const int64_t chunks = ceil_div(c1, kChunk) + ceil_div(c2, kChunk);
+  return chunks * conv_x3_groups(ksize) * conv_packed_nblk(cout) * 64 * 32;
+}
+
+void conv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int c2,
+                         float scale, void* d_packed, hipStream_t st) {
+  require(cout >= 1 && c1 >= 1 && c2 >= 0, "invalid convolution channel counts");
+  require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+  const int taps = ksize[0] * ksize[1] * ksize[2];
+  const int chunks1 = (int)ceil_div(c1, kChunk);
+  const int chunks = chunks1 + (int)ceil_div(c2, kChunk);
+  const int groups = conv_x3_groups(ksize);
+  const int nblk = conv_packed_nblk(cout);
+  const int64_t total = (int64_t)chunks * groups * nblk * 64;
+  const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 65536);
+  hipLaunchKernelGGL(pack_conv_weight_x3_kernel, dim3(blocks), dim3(256), 0, st, d_w,
+                     reinterpret_cast<uint4*>(d_packed), cout, taps, c1, c2, chunks1, chunks,
+                     groups, nblk, scale);
+  launch_check("conv3d_x3_pack_weight");
+}
+
+namespace {
+
+constexpr Variant kX3A{4, 2, 4, 1};  // M 256, N 32
+constexpr Variant kX3B{2, 4, 4, 1};  // M 128, N 64
+constexpr Variant kX3C{2, 4, 2, 2};  // M 64,  N 128
+constexpr Variant kX3D{4, 4, 2, 2};  // M 128, N 128
+constexpr Variant kX3E{4, 4, 4, 1};  // M 256, N 64
+constexpr Variant kX3Table[] = {kX3A, kX3B, kX3C, kX3D, kX3E};
+
+struct X3Plan {
+  Variant v;
+  Box box;
+};
+
+X3Plan plan_x3(const ConvGeom& g, int cout) {
+  X3Plan p{};
+  static const char* forced = std::getenv("NNX_X3_VARIANT");  // tuning override: table index
+  if (forced && *forced) {
+    const int i = std::atoi(forced);
+    require(i >= 0 && i < (int)(sizeof(kX3Table) / sizeof(kX3Table[0])), "bad NNX_X3_VARIANT");
+    p.v = kX3Table[i];
+  } else if (cout <= 32) {
+    p.v = kX3A;
+  } else if (cout <= 64) {
+    p.v = kX3B;
+  } else {
+    p.v = kX3C;
+  }
+  p.box = choose_box(p.v, g, false);
+  return p;
+}
+
+}  // namespace
+
+int conv_x3_stats_tiles(const ConvGeom& g, int cout) {
+  const Box box = plan_x3(g, cout).box;
+  return (int)(ceil_div(g.out[0], box.z) * ceil_div(g.out[1], box.y) * ceil_div(g.out[2], box.x));
+}
+
+void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* packed,
+               float scale, const float* bias, float* y, const ConvGeom& g, int cout,
+               hipStream_t st, float4* stats) {
+  require(x1 && y && packed, "convolution pointers must not be null");
+  require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
+  require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+  const X3Plan plan = plan_x3(g, cout);
+  const Variant v = plan.v;
+  IgemmArgs a = igemm_args(x1, c1, x2, c2, bias, y, g, cout, v, plan.box, stats);
+  a.w16 = reinterpret_cast<const uint4*>(packed);
+  a.ntg = conv_x3_groups(g.k);
+  a.out_scale = 1.0f / scale;
+  double flops, bytes;
+  igemm_work(g, c1, c2, cout, &flops, &bytes);
+  if (v.MB == 4 && v.NB == 2)
+    launch_x3<4, 2, 4, 1>(a, st, flops, bytes);
+  else if (v.MB == 2 && v.WN == 1)
+    launch_x3<2, 4, 4, 1>(a, st, flops, bytes);
+  else if (v.MB == 2)
+    launch_x3<2, 4, 2, 2>(a, st, flops, bytes);
+  else if (v.WN == 2)
+    launch_x3<4, 4, 2, 2>(a, st, flops, bytes);
+  else
+    launch_x3<4, 4, 4, 1>(a, st, flops, bytes);
 }
 
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,

@@ -119,6 +119,19 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
                   const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st,
                   float4* stats = nullptr);
 int conv_stats_tiles(const ConvGeom& g, int cout, int c1, int c2);
+
+// Split-fp16 implicit GEMM: float32 operands split into fp16 high/low halves, three MFMA
+// products per term, float32 accumulation.  `scale` (a power of two from
+// split_weight_scale) multiplies the weights before the split and is undone in the
+// epilogue.  Activations must stay below the fp16 maximum (65504) in magnitude.
+float split_weight_scale(float max_abs);
+int64_t conv_x3_packed_bytes(int cout, const int* ksize, int c1, int c2);
+void conv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int c2,
+                         float scale, void* d_packed, hipStream_t st);
+void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* packed,
+               float scale, const float* bias, float* y, const ConvGeom& g, int cout,
+               hipStream_t st, float4* stats = nullptr);
+int conv_x3_stats_tiles(const ConvGeom& g, int cout);
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
                         const int* size, int cout, hipStream_t st);
 

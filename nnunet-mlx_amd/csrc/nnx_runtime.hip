@@ -122,6 +122,7 @@ struct Param {
   std::vector<int64_t> shape;
   std::vector<float> host;
   bool loaded = false;
+  float max_abs = 0.f;  // max |value|, taken before the host copy is released
   DevBuf dev;  // reference layout on device
   int64_t numel() const {
     int64_t n = 1;
@@ -143,6 +144,9 @@ struct ConvNorm {
   bool act = true;
   int pw = -1, pb = -1, pg = -1, pbeta = -1;
   bool direct = false;
+  bool first = false;   // reads the network input (kept in exact float32 products)
+  bool split = false;   // packed for the split-fp16 kernel
+  float scale = 1.f;    // power-of-two weight scale of the split packing
   DevBuf packed;
 };
 
@@ -191,6 +195,7 @@ struct nnx_model {
   bool conv_bias = true, norm_affine = true;
   float eps = 1e-5f, slope = 0.01f;
   int stem_channels = 0;
+  int precision = NNX_PRECISION_FP32;
   // params
   std::vector<nnx::Param> params;
   std::map<std::string, int> index;
@@ -331,6 +336,17 @@ const float* pdev(const nnx_model* m, int id) {
 
 void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
   if (c.direct) return;  // the direct kernel reads the reference layout
+  // Split-fp16 products for the hidden convolutions with >= 8 taps (a tap group holds 4
+  // taps; 1x1x1 convolutions would waste 3/4 of it).  The first convolution reads the
+  // raw network input, whose range is not normalised, so it keeps float32 products.
+  const int taps = c.k[0] * c.k[1] * c.k[2];
+  c.split = m->precision == NNX_PRECISION_FP32_SPLIT && !c.first && taps >= 8;
+  if (c.split) {
+    c.scale = split_weight_scale(m->params[c.pw].max_abs);
+    c.packed.ensure((size_t)conv_x3_packed_bytes(c.cout, c.k, c.cin1, c.cin2));
+    conv_x3_pack_weight(pdev(m, c.pw), c.cout, c.k, c.cin1, c.cin2, c.scale, c.packed.ptr, st);
+    return;
+  }
   const int64_t n = conv_packed_floats(c.cout, c.k, c.cin1, c.cin2);
   c.packed.ensure((size_t)n * sizeof(float));
   conv_pack_weight(pdev(m, c.pw), c.cout, c.k, c.cin1, c.cin2, c.packed.as<float>(), st);
@@ -390,7 +406,8 @@ struct Runner {
     // Implicit GEMM: the epilogue writes per-tile statistics, so the norm reads the
     // tensor once (apply) instead of twice.
     const ConvGeom g = make_conv_geom(n, in.d, c.k, c.s);
-    const int tiles = conv_stats_tiles(g, c.cout, c.cin1, c.cin2);
+    const int tiles = c.split ? conv_x3_stats_tiles(g, c.cout)
+                              : conv_stats_tiles(g, c.cout, c.cin1, c.cin2);
     if (plan->planning) {
       plan->stats = std::max(plan->stats, (size_t)n * tiles * c.cout * sizeof(float4));
       plan->params = std::max(plan->params, (size_t)n * c.cout * sizeof(float2));
@@ -398,8 +415,12 @@ struct Runner {
     }
     float4* stats = plan->ws->stats.as<float4>();
     float2* params = plan->ws->params.as<float2>();
-    conv3d_igemm(x1, c.cin1, x2, c.cin2, c.packed.as<float>(), pdev(m, c.pb), out, g, c.cout, st,
-                 stats);
+    if (c.split)
+      conv3d_x3(x1, c.cin1, x2, c.cin2, c.packed.ptr, c.scale, pdev(m, c.pb), out, g, c.cout, st,
+                stats);
+    else
+      conv3d_igemm(x1, c.cin1, x2, c.cin2, c.packed.as<float>(), pdev(m, c.pb), out, g, c.cout,
+                   st, stats);
     instnorm_merge_partials(stats, tiles, n, vox, c.cout, pdev(m, c.pg), m->eps, params, st);
     instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, pdev(m, c.pbeta), act,
                           m->slope, residual, st);
@@ -693,7 +714,8 @@ int nnx_model_create(const nnx_spec* spec, nnx_model** out) {
     require(spec->spatial_dims == 3, "only three-dimensional networks run on the HIP path");
     require(spec->arch == NNX_ARCH_PLAIN || spec->arch == NNX_ARCH_RESIDUAL,
             "unsupported network architecture");
-    require(spec->precision == NNX_PRECISION_FP32, "unsupported precision");
+    require(spec->precision == NNX_PRECISION_FP32 || spec->precision == NNX_PRECISION_FP32_SPLIT,
+            "unsupported precision");
     require(spec->input_channels >= 1 && spec->num_classes >= 1,
             "network needs input channels and at least one output");
     require(spec->n_stages >= 2, "network needs at least two stages");
@@ -727,7 +749,12 @@ int nnx_model_create(const nnx_spec* spec, nnx_model** out) {
     m->eps = spec->norm_eps;
     m->slope = spec->leaky_slope;
     m->stem_channels = spec->stem_channels;
+    m->precision = spec->precision;
     build_graph(m.get());
+    if (m->arch == NNX_ARCH_PLAIN)
+      m->enc[0][0].first = true;
+    else
+      m->stem.first = true;
     *out = m.release();
   });
 }
@@ -784,6 +811,7 @@ int nnx_model_finalize(nnx_model* model) {
       if (!p.loaded) missing += (missing.empty() ? "" : ", ") + p.name;
     if (!missing.empty()) fail(NNX_ERR_STATE, "missing parameters: " + missing);
     for (Param& p : model->params) {
+      for (float v : p.host) p.max_abs = std::max(p.max_abs, std::fabs(v));
       p.dev.ensure((size_t)p.numel() * sizeof(float));
       hip_check(hipMemcpy(p.dev.ptr, p.host.data(), (size_t)p.numel() * sizeof(float),
                           hipMemcpyHostToDevice),
@@ -915,6 +943,35 @@ int nnx_conv3d_igemm(const float* d_x1, int c1, const float* d_x2, int c2,
     require(cout >= 1, "convolution needs at least one output channel");
     const ConvGeom g = make_conv_geom(batch, in_size, ksize, stride);
     conv3d_igemm(d_x1, c1, d_x2, c2, d_packed, d_bias, d_y, g, cout, as_stream(stream));
+  });
+}
+
+float nnx_split_weight_scale(float max_abs) {
+  if (!(max_abs >= 0.f) || !std::isfinite(max_abs)) return 0.f;
+  return split_weight_scale(max_abs);
+}
+
+size_t nnx_conv3d_split_packed_bytes(int cout, const int* ksize, int c1, int c2) {
+  if (!ksize || cout < 1 || c1 < 1 || c2 < 0) return 0;
+  return (size_t)conv_x3_packed_bytes(cout, ksize, c1, c2);
+}
+
+int nnx_conv3d_split_pack_weight(const float* d_weight, int cout, const int* ksize, int c1,
+                                 int c2, float scale, void* d_packed, void* stream) {
+  return guarded([&] {
+    require(d_weight && ksize && d_packed, "null argument");
+    conv_x3_pack_weight(d_weight, cout, ksize, c1, c2, scale, d_packed, as_stream(stream));
+  });
+}
+
+int nnx_conv3d_split(const float* d_x1, int c1, const float* d_x2, int c2, const void* d_packed,
+                     float scale, const float* d_bias, float* d_y, int batch, const int* in_size,
+                     int cout, const int* ksize, const int* stride, void* stream) {
+  return guarded([&] {
+    require(in_size && ksize && stride, "null argument");
+    require(cout >= 1, "convolution needs at least one output channel");
+    const ConvGeom g = make_conv_geom(batch, in_size, ksize, stride);
+    conv3d_x3(d_x1, c1, d_x2, c2, d_packed, scale, d_bias, d_y, g, cout, as_stream(stream));
   });
 }
 

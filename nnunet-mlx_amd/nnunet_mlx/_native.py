@@ -31,6 +31,7 @@ NNX_ERR_NOMEM = -5
 NNX_ARCH_PLAIN = 0
 NNX_ARCH_RESIDUAL = 1
 NNX_PRECISION_FP32 = 0
+NNX_PRECISION_FP32_SPLIT = 1
 NNX_ACCUM_F32 = 0
 NNX_ACCUM_NNUNET_F16 = 1
 
@@ -127,6 +128,17 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int,
         [c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_int,
          c_int_p, ctypes.c_int, c_int_p, c_int_p, c_void_p],
+    ),
+    "nnx_split_weight_scale": (ctypes.c_float, [ctypes.c_float]),
+    "nnx_conv3d_split_packed_bytes": (ctypes.c_size_t, [ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_int]),
+    "nnx_conv3d_split_pack_weight": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p],
+    ),
+    "nnx_conv3d_split": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p,
+         ctypes.c_int, c_int_p, ctypes.c_int, c_int_p, c_int_p, c_void_p],
     ),
     "nnx_conv3d_direct_small_cin": (
         ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, c_void_p]

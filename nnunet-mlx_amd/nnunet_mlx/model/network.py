@@ -23,7 +23,14 @@ from nnunet_mlx.errors import ContractError
 from nnunet_mlx.model.topology import NetworkSpec, PlainConvUNetSpec, ResidualEncoderUNetSpec
 
 
-def _spec_struct(spec: NetworkSpec, keep: list) -> _native.NnxSpec:
+# Convolution arithmetic of the HIP network.  Both meet the float32 logits tolerance:
+# "fp32" multiplies in float32 on fp32 MFMA; "fp32-split" computes the convolutions after
+# the first as hi*hi + hi*lo + lo*hi of fp16-split operands with float32 accumulation.
+PRECISIONS = {"fp32": _native.NNX_PRECISION_FP32, "fp32-split": _native.NNX_PRECISION_FP32_SPLIT}
+DEFAULT_PRECISION = "fp32"
+
+
+def _spec_struct(spec: NetworkSpec, keep: list, precision: str = DEFAULT_PRECISION) -> _native.NnxSpec:
     residual = isinstance(spec, ResidualEncoderUNetSpec)
     if spec.spatial_dims != 3:
         raise ContractError("only three-dimensional networks run on the HIP path")
@@ -54,20 +61,23 @@ def _spec_struct(spec: NetworkSpec, keep: list) -> _native.NnxSpec:
     s.leaky_slope = float(spec.leaky_slope)
     s.stem_channels = int(spec.stem_channels or 0) if residual else 0
     s.bottleneck_channels = ctypes.cast(bottleneck, _native.c_int_p) if bottleneck is not None else None
-    s.precision = _native.NNX_PRECISION_FP32
+    if precision not in PRECISIONS:
+        raise ContractError(f"unsupported precision {precision!r}; expected one of {sorted(PRECISIONS)}")
+    s.precision = PRECISIONS[precision]
     return s
 
 
 class NativeNetwork:
     """Shared implementation of the two architectures (one ``nnx_model`` each)."""
 
-    def __init__(self, spec: NetworkSpec) -> None:
+    def __init__(self, spec: NetworkSpec, *, precision: str = DEFAULT_PRECISION) -> None:
         self.spec = spec
         self.training = False
         self.inference_arithmetic = "native"
+        self.precision = precision
         self._lib = _native.load()
         keep: list = []
-        struct = _spec_struct(spec, keep)
+        struct = _spec_struct(spec, keep, precision)
         handle = ctypes.c_void_p()
         _native.check(self._lib.nnx_model_create(ctypes.byref(struct), ctypes.byref(handle)),
                       "nnx_model_create")
@@ -177,22 +187,22 @@ class NativeNetwork:
 class PlainConvUNet(NativeNetwork):
     """Plan-driven PlainConvUNet (dynamic-network-architectures v0.4.4 semantics)."""
 
-    def __init__(self, spec: PlainConvUNetSpec) -> None:
+    def __init__(self, spec: PlainConvUNetSpec, *, precision: str = DEFAULT_PRECISION) -> None:
         if not isinstance(spec, PlainConvUNetSpec):
             raise ContractError("PlainConvUNet needs a PlainConvUNetSpec")
-        super().__init__(spec)
+        super().__init__(spec, precision=precision)
 
 
 class ResidualEncoderUNet(NativeNetwork):
     """nnU-Net ResidualEncoderUNet: residual stem and stages, plain decoder."""
 
-    def __init__(self, spec: ResidualEncoderUNetSpec) -> None:
+    def __init__(self, spec: ResidualEncoderUNetSpec, *, precision: str = DEFAULT_PRECISION) -> None:
         if not isinstance(spec, ResidualEncoderUNetSpec):
             raise ContractError("ResidualEncoderUNet needs a ResidualEncoderUNetSpec")
-        super().__init__(spec)
+        super().__init__(spec, precision=precision)
 
 
-def build_network(spec: NetworkSpec) -> NativeNetwork:
+def build_network(spec: NetworkSpec, *, precision: str = DEFAULT_PRECISION) -> NativeNetwork:
     if isinstance(spec, ResidualEncoderUNetSpec):
-        return ResidualEncoderUNet(spec)
-    return PlainConvUNet(spec)
+        return ResidualEncoderUNet(spec, precision=precision)
+    return PlainConvUNet(spec, precision=precision)

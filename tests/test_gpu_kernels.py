@@ -79,6 +79,45 @@ def test_conv3d_igemm_matches_float64(lib, case):
     assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
 
 
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}-k{c[5]}-s{c[6]}")
+def test_conv3d_split_matches_float64(lib, case):
+    """Split-fp16 products (hi*hi + hi*lo + lo*hi) hold the same float32 bar as the fp32 kernel."""
+    batch, size, c1, c2, cout, kernel, stride = case
+    print(f"split conv case {case}", flush=True)
+    rng = np.random.default_rng((hash(case) + 7) % 2**32)
+    x1 = rng.standard_normal((batch, *size, c1)).astype(np.float32)
+    x2 = rng.standard_normal((batch, *size, c2)).astype(np.float32) if c2 else None
+    w = (rng.standard_normal((cout, *kernel, c1 + c2)) / np.sqrt((c1 + c2) * np.prod(kernel))).astype(np.float32)
+    # a few weights three decades below the rest exercise the low halves of small values
+    w.reshape(-1)[:: 7] *= 1e-3
+    bias = rng.standard_normal(cout).astype(np.float32)
+    out_size = [(s + 2 * (k // 2) - k) // st + 1 for s, k, st in zip(size, kernel, stride)]
+    k_c = _native.ints(kernel)
+    scale = lib.nnx_split_weight_scale(float(np.abs(w).max()))
+    assert scale > 0 and np.log2(scale) == int(np.log2(scale))
+    assert 2.0**14 <= np.abs(w).max() * scale < 2.0**15
+    nbytes = lib.nnx_conv3d_split_packed_bytes(cout, k_c, c1, c2)
+    packed = torch.empty(nbytes, dtype=torch.uint8, device="cuda")
+    dw = dev(w)
+    _native.check(lib.nnx_conv3d_split_pack_weight(dw.data_ptr(), cout, k_c, c1, c2, scale,
+                                                   packed.data_ptr(), stream()))
+    dx1 = dev(x1)
+    dx2 = dev(x2) if c2 else None
+    db = dev(bias)
+    y = torch.full((batch, *out_size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_conv3d_split(
+        dx1.data_ptr(), c1, dx2.data_ptr() if c2 else None, c2, packed.data_ptr(), scale,
+        db.data_ptr(), y.data_ptr(), batch, _native.ints(size), cout, k_c, _native.ints(stride),
+        stream()))
+    got = host(y)
+    full = np.concatenate([x1, x2], axis=-1) if c2 else x1
+    ref = _conv_ref64(full, w, stride) + bias.astype(np.float64)
+    msg = report("split conv", got, ref)
+    assert np.isfinite(got).all(), msg
+    assert rel_l2(got, ref) <= 1e-5, msg
+    assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
+
+
 @pytest.mark.parametrize("size,cout", [((16, 16, 16), 32), ((5, 7, 9), 8)])
 def test_direct_single_channel_conv(lib, size, cout):
     print(f"direct conv {size} {cout}", flush=True)

@@ -53,29 +53,33 @@ CASES = {
                                                 (1, 2, 2), (1, 1), bottleneck_channels=(2, 4, 8)),
                         (8, 8, 8), 1, True),
     "resenc-L": (resenc_spec(), (128, 64, 64), 1, True),
+    "liver-128": (liver_spec(), (128, 128, 128), 1, True),
 }
 
 
 @pytest.mark.parametrize("name", list(CASES))
 def test_forward_matches_oracle(device, name):
+    """Both convolution arithmetics ("fp32" products and "fp32-split" fp16-split products)
+    against one oracle run."""
     spec, patch, batch, affine = CASES[name]
-    print(f"network case {name} patch={patch} batch={batch}", flush=True)
     weights = random_weights(spec, seed=1, random_affine=affine)
-    net = build_network(spec)
-    net.load_weights(weights)
     rng = np.random.default_rng(0)
     x = rng.standard_normal((batch, *patch, spec.input_channels)).astype(np.float32)
-    got = net(torch.from_numpy(x).to(device)).cpu().numpy()
     residual = isinstance(spec, ResidualEncoderUNetSpec)
     ref = OracleNetwork(spec, weights, residual=residual)(x)
-    msg = report(name, got, ref)
-    print(msg, flush=True)
-    assert got.shape == ref.shape
-    assert np.abs(got - ref).max() <= 1e-3, msg
-    assert rel_l2(got, ref) <= 1e-5, msg
-    agree = (got.argmax(-1) == ref.argmax(-1)).mean()
-    assert agree >= 0.9999, f"{msg} label agreement {agree}"
-    net.close()
+    for precision in ("fp32", "fp32-split"):
+        print(f"network case {name} patch={patch} batch={batch} precision={precision}", flush=True)
+        net = build_network(spec, precision=precision)
+        net.load_weights(weights)
+        got = net(torch.from_numpy(x).to(device)).cpu().numpy()
+        msg = report(f"{name} {precision}", got, ref)
+        print(msg, flush=True)
+        assert got.shape == ref.shape
+        assert np.abs(got - ref).max() <= 1e-3, msg
+        assert rel_l2(got, ref) <= 1e-5, msg
+        agree = (got.argmax(-1) == ref.argmax(-1)).mean()
+        assert agree >= 0.9999, f"{msg} label agreement {agree}"
+        net.close()
 
 
 def test_forward_rejects_bad_input(device):

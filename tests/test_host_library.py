@@ -44,3 +44,21 @@ def test_error_path_without_gpu():
     assert b"odd" in lib.nnx_last_error()
     with pytest.raises(ContractError):
         _native.check(rc)
+
+
+def test_split_weight_scale_rules():
+    """The split-fp16 weight scale is the power of two that puts max |w| in [2^14, 2^15)."""
+    from nnunet_mlx import _native
+
+    lib = _native.load()
+    assert lib.nnx_split_weight_scale(0.0) == 1.0
+    assert lib.nnx_split_weight_scale(1.0) == 2.0**14
+    assert lib.nnx_split_weight_scale(0.75) == 2.0**15
+    assert lib.nnx_split_weight_scale(6e4) == 0.5
+    assert lib.nnx_split_weight_scale(2.0**-30) == 2.0**44
+    assert lib.nnx_split_weight_scale(float("nan")) == 0.0
+    assert lib.nnx_split_weight_scale(float("inf")) == 0.0
+    assert lib.nnx_split_weight_scale(-1.0) == 0.0
+    for m in (1e-4, 0.0123, 0.5, 3.0, 1000.0):
+        s = lib.nnx_split_weight_scale(m)
+        assert 2.0**14 <= m * s < 2.0**15
