@@ -80,13 +80,17 @@ def _short_kernel(name: str) -> str:
 
 
 def kernel_class_of(short: str) -> str | None:
-    """Map a rocprof kernel name to the profiling class bench.py reports."""
-    variants = {"igemm_kernel<8, 2, 4, 1>": "conv3d_igemm_m512n32",
-                "igemm_kernel<4, 4, 4, 1>": "conv3d_igemm_m256n64",
-                "igemm_kernel<4, 4, 2, 2>": "conv3d_igemm_m128n128",
-                "igemm_kernel<2, 4, 4, 1>": "conv3d_igemm_m128n64",
-                "igemm_kernel<2, 4, 2, 2>": "conv3d_igemm_m64n128"}
-    return variants.get(short)
+    """Map a rocprof kernel name to the profiling class bench.py reports
+    (igemm_kernel<MB, NB, WM, WN, ...> -> conv3d_igemm_m{16*MB*WM}n{16*NB*WN}, and the
+    split-fp16 kernels igemm_x3s_kernel / igemm_x3_kernel -> conv3d_x3s_* / conv3d_x3_*)."""
+    import re
+
+    m = re.match(r"igemm(_x3s|_x3)?_kernel<(\d+), (\d+), (\d+), (\d+)", short)
+    if not m:
+        return None
+    prefix = {None: "conv3d_igemm", "_x3s": "conv3d_x3s", "_x3": "conv3d_x3"}[m.group(1)]
+    mb, nb, wm, wn = (int(g) for g in m.groups()[1:])
+    return f"{prefix}_m{16 * mb * wm}n{16 * nb * wn}"
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_liver_tile.md"
@@ -109,7 +113,7 @@ def summarize_profiles(directory: str) -> None:
         "Command (repo root on the MI355X box):",
         "",
         "    rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/prof_trace -o liver -- \\",
-        "        python -u bench.py --warmup 1 --steps 1 --no-cpu-baseline --no-pcie",
+        "        python -u bench.py --warmup 1 --steps 1 --no-cpu-baseline --no-pcie --no-alt",
         "",
         "Calls count the warmup and the timed case (2 cases). Average = per launch.",
         "",
@@ -144,9 +148,9 @@ def summarize_profiles(directory: str) -> None:
         "Commands (repo root on the MI355X box), one counter per run:",
         "",
         "    rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/prof_fetch -o fetch -- \\",
-        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --copy-calibration",
+        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt --copy-calibration",
         "    rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/prof_write -o write -- \\",
-        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --copy-calibration",
+        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt --copy-calibration",
         "",
         f"Calibration: torch.neg over 1 GiB (reads 1 GiB, writes 1 GiB) reads FETCH_SIZE = "
         f"{neg['FETCH_SIZE']:.0f} KiB and WRITE_SIZE = {neg['WRITE_SIZE']:.0f} KiB, so FETCH_SIZE is "
@@ -239,9 +243,12 @@ def main() -> int:
                              "(torch.neg) whose HBM counters calibrate FETCH_SIZE/WRITE_SIZE")
     parser.add_argument("--summarize-profiles", metavar="DIR",
                         help="write the profiles/ summaries from rocprofv3 CSV output in DIR and exit")
-    parser.add_argument("--precision", choices=("fp32", "fp32-split"), default="fp32",
-                        help="convolution arithmetic: float32 products on fp32 MFMA, or "
-                             "fp16-split products (3 per term) on fp16 MFMA; both float32 I/O")
+    parser.add_argument("--precision", choices=("fp32", "fp32-split"), default="fp32-split",
+                        help="convolution arithmetic: fp16-split products (3 per term) on fp16 "
+                             "MFMA (default), or float32 products on fp32 MFMA; both float32 I/O "
+                             "and accumulation, both within the float32 logits tolerance")
+    parser.add_argument("--no-alt", action="store_true",
+                        help="skip the one-step measurement of the other precision")
     parser.add_argument("--shape", type=int, nargs=3, default=VOLUME_SHAPE[1:],
                         help="volume size (Z Y X); the default is the liver case")
     args = parser.parse_args()
@@ -339,6 +346,25 @@ def main() -> int:
     conv_peak = PEAK_FP32_MFMA_TFLOPS if args.precision == "fp32" else PEAK_FP16_MFMA_TFLOPS / SPLIT_PRODUCTS
     conv_frac = conv_flops / (conv_ms * 1e-3) / 1e12 / conv_peak if conv_ms else None
 
+    alt = None
+    if not args.no_alt:
+        other = "fp32" if args.precision == "fp32-split" else "fp32-split"
+        print(f"[bench] one step with precision {other}", file=sys.stderr, flush=True)
+        alt_net = build_network(spec, precision=other)
+        alt_net.load_weights(weights)
+        alt_net.share_workspace(net)
+        sw.average_fold_labels((alt_net,), volume, return_device=True, **kwargs)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        alt_labels = sw.average_fold_labels((alt_net,), volume, return_device=True, **kwargs)
+        torch.cuda.synchronize()
+        alt_s = time.perf_counter() - t0
+        agree = float((alt_labels == labels).float().mean())
+        alt = {"precision": other, "value": round(voxels / alt_s, 1),
+               "ms_per_step": round(alt_s * 1e3, 2), "label_agreement": round(agree, 7)}
+        alt_net.close()
+        del alt_labels
+
     pcie = None
     if not args.no_pcie:
         torch.cuda.synchronize()
@@ -381,6 +407,7 @@ def main() -> int:
         "ms_per_tile": round(step_s * 1e3 / ntiles, 2),
         "conv3d_mfma_frac": round(conv_frac, 4) if conv_frac else None,
         "pcie_inclusive_voxels_per_s": round(pcie, 1) if pcie else None,
+        "other_precision": alt,
         "roofline": roofline,
         "cpu_baseline": baseline,
         "kernels": kernels,

@@ -483,10 +483,16 @@ __device__ __forceinline__ void split_half(float v, _Float16& hi, _Float16& lo) 
   lo = (_Float16)(v - (float)hi);
 }
 
-template <int MB, int NB, int WM, int WN>
+// Halo lines (8-byte halves of a voxel's 8-channel chunk, 4 floats) per thread: the
+// split kernel stages the next chunk's halo in registers while the current chunk computes.
+constexpr int kX3MaxLines = 6;  // halo lines per thread in flight (register staging)
+constexpr int kX3Threads = 256;
+
+template <int MB, int NB, int WM, int WN, int NTG>
 __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
   extern __shared__ __align__(16) float lds[];
   constexpr int NT = 64 * WM * WN;
+  static_assert(NT == kX3Threads, "split kernel variants use 256 threads");
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
@@ -517,6 +523,21 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
   }
   const int nbk0 = nt * (WN * NB) + wn * NB;
 
+  // halo offset of this lane's tap 4g + slot; padding taps (beyond the kernel) read voxel
+  // 0 of the halo against zero weights
+  int toff[NTG];
+#pragma unroll
+  for (int g = 0; g < NTG; ++g) {
+    const int t = 4 * g + slot;
+    int o = 0;
+    if (t < a.taps) {
+      const int kx = t % a.kw;
+      const int r = t / a.kw;
+      o = ((r / a.kh) * a.hy + r % a.kh) * a.hx + kx;
+    }
+    toff[g] = o;
+  }
+
   f4 acc[MB][NB];
 #pragma unroll
   for (int mb = 0; mb < MB; ++mb)
@@ -525,129 +546,313 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
 
   const int hyx = a.hy * a.hx;
   const int hvox = a.hz * hyx;
+  const int nlines = hvox * 2;
   _Float16* hi_plane = reinterpret_cast<_Float16*>(lds);
   _Float16* lo_plane = hi_plane + (size_t)hvox * kChunk;
   const h8* hi8 = reinterpret_cast<const h8*>(hi_plane);
   const h8* lo8 = reinterpret_cast<const h8*>(lo_plane);
 
-  // tap offset (in halo voxels) of this lane's tap in group g; padding taps read voxel 0
-  auto tap_offset = [&](int g) {
-    const int t = 4 * g + slot;
-    if (t >= a.taps) return -1;
-    const int kx = t % a.kw;
-    const int rest = t / a.kw;
-    const int ky = rest % a.kh;
-    const int kz = rest / a.kh;
-    return (kz * a.hy + ky) * a.hx + kx;
-  };
-
-  for (int chunk = 0; chunk < a.chunks; ++chunk) {
-    const float* src;
-    int C, cb;
-    if (chunk < a.chunks0) {
-      src = a.x0;
-      C = a.c0;
-      cb = chunk * kChunk;
-    } else {
-      src = a.x1;
-      C = a.c1;
-      cb = (chunk - a.chunks0) * kChunk;
-    }
-    __syncthreads();
-    for (int i = tid; i < hvox * 2; i += NT) {
-      const int v = i >> 1, h = i & 1;
+  // This thread's halo lines j*NT + tid: all share the half h = tid & 1 (NT is even); the
+  // voxel index within the batch item is fixed across chunks (-1 outside the volume).
+  const int h = tid & 1;
+  int vofs[kX3MaxLines];
+#pragma unroll
+  for (int j = 0; j < kX3MaxLines; ++j) {
+    const int line = j * NT + tid;
+    int o = -1;
+    if (line < nlines) {
+      const int v = line >> 1;
       const int hz_ = v / hyx;
       const int rem = v - hz_ * hyx;
       const int hy_ = rem / a.hx;
-      const int hx_ = rem - hy_ * a.hx;
-      const int z = iz0 + hz_, yy = iy0 + hy_, xx = ix0 + hx_;
-      f4 val = {0.f, 0.f, 0.f, 0.f};
+      const int z = iz0 + hz_, yy = iy0 + hy_, xx = ix0 + (rem - hy_ * a.hx);
       if ((unsigned)z < (unsigned)a.id && (unsigned)yy < (unsigned)a.ih &&
-          (unsigned)xx < (unsigned)a.iw) {
-        const int c = cb + h * 4;
-        const int64_t off = ((((int64_t)b * a.id + z) * a.ih + yy) * a.iw + xx) * C + c;
-        if ((C & 3) == 0) {
-          if (c < C) val = *reinterpret_cast<const f4*>(src + off);
+          (unsigned)xx < (unsigned)a.iw)
+        o = (z * a.ih + yy) * a.iw + xx;
+    }
+    vofs[j] = o;
+  }
+  const int64_t bvox = (int64_t)b * a.id * a.ih * a.iw;
+
+  f4 stage[kX3MaxLines];
+  auto fetch = [&](int chunk) {
+    const HaloSource hs = halo_source(a, chunk);
+    const int c = hs.cb + h * 4;
+#pragma unroll
+    for (int j = 0; j < kX3MaxLines; ++j) {
+      f4 val = {0.f, 0.f, 0.f, 0.f};
+      if (vofs[j] >= 0) {
+        const int64_t off = (bvox + vofs[j]) * hs.C + c;
+        if ((hs.C & 3) == 0) {
+          if (c < hs.C) val = *reinterpret_cast<const f4*>(hs.src + off);
         } else {
 #pragma unroll
           for (int q = 0; q < 4; ++q)
-            if (c + q < C) val[q] = src[off + q];
+            if (c + q < hs.C) val[q] = hs.src[off + q];
         }
       }
-      h4 hv, lv;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        _Float16 hh, ll;
-        split_half(val[q], hh, ll);
-        hv[q] = hh;
-        lv[q] = ll;
-      }
-      *reinterpret_cast<h4*>(hi_plane + v * kChunk + h * 4) = hv;
-      *reinterpret_cast<h4*>(lo_plane + v * kChunk + h * 4) = lv;
+      stage[j] = val;
     }
+  };
+  auto publish = [&]() {
+#pragma unroll
+    for (int j = 0; j < kX3MaxLines; ++j) {
+      const int line = j * NT + tid;
+      if (line < nlines) {
+        h4 hv, lv;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          _Float16 hh, ll;
+          split_half(stage[j][q], hh, ll);
+          hv[q] = hh;
+          lv[q] = ll;
+        }
+        *reinterpret_cast<h4*>(hi_plane + line * 4) = hv;
+        *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
+      }
+    }
+  };
+
+  fetch(0);
+  const int group_stride = a.nblk * 128;
+  for (int chunk = 0; chunk < a.chunks; ++chunk) {
+    // packed weights: [chunk][group][nblk] x {hi h8 of 64 lanes, lo h8 of 64 lanes}
+    const uint4* wc = a.w16 + ((int64_t)chunk * NTG * a.nblk + nbk0) * 128 + lane;
+    h8 A[2][MB][2], B[2][NB][2];
+    auto load_b = [&](int p, int g) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint4 wh = wc[g * group_stride + nb * 128];
+        const uint4 wl = wc[g * group_stride + nb * 128 + 64];
+        B[p][nb][0] = *reinterpret_cast<const h8*>(&wh);
+        B[p][nb][1] = *reinterpret_cast<const h8*>(&wl);
+      }
+    };
+    auto load_a = [&](int p, int g) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        A[p][mb][0] = hi8[hbase[mb] + toff[g]];
+        A[p][mb][1] = lo8[hbase[mb] + toff[g]];
+      }
+    };
+    load_b(0, 0);  // in flight across the barriers below
+    __syncthreads();  // the previous chunk's fragments have been read
+    publish();
     __syncthreads();
-    // packed weights: [chunk][group][nblk][lane] x {hi h8, lo h8}
-    const uint4* wc = a.w16 + ((int64_t)chunk * a.ntg * a.nblk + nbk0) * 128 + lane * 2;
-    const int group_stride = a.nblk * 128;
-    h8 ah[MB], al[MB], bh[NB], bl[NB];
-    {
-      const int toff = tap_offset(0);
-      const int o = toff < 0 ? 0 : toff;
+    if (chunk + 1 < a.chunks) fetch(chunk + 1);  // lands while this chunk computes
+    load_a(0, 0);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        ah[mb] = hi8[hbase[mb] + o];
-        al[mb] = lo8[hbase[mb] + o];
+    for (int g = 0; g < NTG; ++g) {
+      const int cur = g & 1;
+      if (g + 1 < NTG) {
+        load_a(cur ^ 1, g + 1);
+        load_b(cur ^ 1, g + 1);
       }
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint4 wh = wc[nb * 128], wl = wc[nb * 128 + 1];
-        bh[nb] = *reinterpret_cast<const h8*>(&wh);
-        bl[nb] = *reinterpret_cast<const h8*>(&wl);
-      }
-    }
-    for (int g = 0; g < a.ntg; ++g) {
-      const int ng = g + 1 < a.ntg ? g + 1 : g;
-      const int ntoff = tap_offset(ng);
-      const int no = ntoff < 0 ? 0 : ntoff;
-      h8 nah[MB], nal[MB], nbh[NB], nbl[NB];
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        nah[mb] = hi8[hbase[mb] + no];
-        nal[mb] = lo8[hbase[mb] + no];
-      }
-      const uint4* wg = wc + (int64_t)ng * group_stride;
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint4 wh = wg[nb * 128], wl = wg[nb * 128 + 1];
-        nbh[nb] = *reinterpret_cast<const h8*>(&wh);
-        nbl[nb] = *reinterpret_cast<const h8*>(&wl);
-      }
+      // hi*hi, hi*lo, lo*hi: the three passes touch MB*NB independent accumulators in turn
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          acc[mb][nb] = mfma16x16x32h(ah[mb], bh[nb], acc[mb][nb]);
-          acc[mb][nb] = mfma16x16x32h(ah[mb], bl[nb], acc[mb][nb]);
-          acc[mb][nb] = mfma16x16x32h(al[mb], bh[nb], acc[mb][nb]);
-        }
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][0], acc[mb][nb]);
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        ah[mb] = nah[mb];
-        al[mb] = nal[mb];
-      }
+      for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        bh[nb] = nbh[nb];
-        bl[nb] = nbl[nb];
-      }
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][1], acc[mb][nb]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = mfma16x16x32h(A[cur][mb][1], B[cur][nb][0], acc[mb][nb]);
     }
   }
   igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
                                  ox0, a.out_scale);
 }
 
-// Split-fp16 weight packing: packed[((chunk * groups + g) * nblk + nb) * 64 + lane] =
-// { hi h8, lo h8 } of scale * W[n][tap 4g + lane/16][cin(chunk, q)], q = 0..7.
+// Weight-staged split kernel: per chunk, the workgroup copies its halo (split into the
+// two planes) and its weights (all NTG tap groups of its WN*NB column blocks) into LDS,
+// then computes from LDS only.  The main loop issues no global loads, so its LDS waits
+// never queue behind memory traffic; the chunk-boundary load latency is covered by the
+// other resident workgroups.  LDS: 32 bytes per halo voxel + NTG * WN*NB * 2 KB.
+template <int MB, int NB, int WM, int WN, int NTG, bool VEC>
+__global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) {
+  extern __shared__ __align__(16) float lds[];
+  constexpr int NT = 64 * WM * WN;
+  constexpr int WBLK = WN * NB;  // column blocks of the workgroup
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave % WM;
+  const int wn = wave / WM;
+  const int logical = xcd_remap(blockIdx.x, a.nwg);
+  const int nt = logical % a.ntn;
+  int tile = logical / a.ntn;
+  const int txi = tile % a.tx;
+  tile /= a.tx;
+  const int tyi = tile % a.ty;
+  tile /= a.ty;
+  const int tzi = tile % a.tz;
+  const int b = tile / a.tz;
+  const int oz0 = tzi * a.bz, oy0 = tyi * a.by, ox0 = txi * a.bx;
+  const int iz0 = oz0 * a.sd - a.pd, iy0 = oy0 * a.sh - a.ph, ix0 = ox0 * a.sw - a.pw;
+
+  const int row = lane & 15;
+  const int slot = lane >> 4;
+  int hbase[MB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb) {
+    const int v = 16 * (wm * MB + mb) + row;
+    const int vx = v & (a.bx - 1);
+    const int vy = (v >> a.lbx) & (a.by - 1);
+    const int vz = v >> a.lbxy;
+    hbase[mb] = ((vz * a.sd) * a.hy + vy * a.sh) * a.hx + vx * a.sw;
+  }
+  const int nbk0 = nt * WBLK + wn * NB;
+
+  int toff[NTG];
+#pragma unroll
+  for (int g = 0; g < NTG; ++g) {
+    const int t = 4 * g + slot;
+    int o = 0;
+    if (t < a.taps) {
+      const int kx = t % a.kw;
+      const int r = t / a.kw;
+      o = ((r / a.kh) * a.hy + r % a.kh) * a.hx + kx;
+    }
+    toff[g] = o;
+  }
+
+  f4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+
+  const int hyx = a.hy * a.hx;
+  const int hvox = a.hz * hyx;
+  const int nlines = hvox * 2;
+  _Float16* hi_plane = reinterpret_cast<_Float16*>(lds);
+  _Float16* lo_plane = hi_plane + (size_t)hvox * kChunk;
+  const h8* hi8 = reinterpret_cast<const h8*>(hi_plane);
+  const h8* lo8 = reinterpret_cast<const h8*>(lo_plane);
+  // weights: [group][block][hi 64 lanes | lo 64 lanes] of 16 bytes
+  uint4* wl = reinterpret_cast<uint4*>(lds + (size_t)hvox * 8);
+  const h8* wl8 = reinterpret_cast<const h8*>(wl);
+
+  const int h = tid & 1;  // every line j*NT + tid of this thread is half h of its voxel
+  const int64_t bvox = (int64_t)b * a.id * a.ih * a.iw;
+  const float* zero = g_zero_line;
+
+  for (int chunk = 0; chunk < a.chunks; ++chunk) {
+    const HaloSource hs = halo_source(a, chunk);
+    const int c = hs.cb + h * 4;
+    __syncthreads();  // the previous chunk's fragments have been read
+    // halo: batches of kX3MaxLines loads in flight, then split + store
+    for (int base = 0; base < nlines; base += kX3MaxLines * NT) {
+      f4 val[kX3MaxLines];
+#pragma unroll
+      for (int j = 0; j < kX3MaxLines; ++j) {
+        const int line = base + j * NT + tid;
+        const float* src = zero;
+        bool inside = false;
+        if (line < nlines) {
+          const int v = line >> 1;
+          const int hz_ = v / hyx;
+          const int rem = v - hz_ * hyx;
+          const int hy_ = rem / a.hx;
+          const int z = iz0 + hz_, yy = iy0 + hy_, xx = ix0 + (rem - hy_ * a.hx);
+          inside = (unsigned)z < (unsigned)a.id && (unsigned)yy < (unsigned)a.ih &&
+                   (unsigned)xx < (unsigned)a.iw;
+          if (inside) src = hs.src + (bvox + (int64_t)(z * a.ih + yy) * a.iw + xx) * hs.C + c;
+        }
+        if constexpr (VEC) {
+          val[j] = *reinterpret_cast<const f4*>(src);
+        } else {
+          val[j] = f4{0.f, 0.f, 0.f, 0.f};
+          if (inside) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (c + q < hs.C) val[j][q] = src[q];
+          }
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < kX3MaxLines; ++j) {
+        const int line = base + j * NT + tid;
+        if (line < nlines) {
+          h4 hv, lv;
+#pragma unroll
+          for (int q = 0; q < 4; ++q) {
+            _Float16 hh, ll;
+            split_half(val[j][q], hh, ll);
+            hv[q] = hh;
+            lv[q] = ll;
+          }
+          *reinterpret_cast<h4*>(hi_plane + line * 4) = hv;
+          *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
+        }
+      }
+    }
+    // weights of this chunk and column range: NTG runs of WBLK*128 16-byte words
+    {
+      const uint4* wsrc = a.w16 + ((int64_t)chunk * NTG * a.nblk + nt * WBLK) * 128;
+      constexpr int run = WBLK * 128;
+      constexpr int total = NTG * run;
+#pragma unroll
+      for (int i0 = 0; i0 < total; i0 += NT) {
+        const int i = i0 + tid;
+        if (i < total) {
+          const int g = i / run;
+          wl[i] = wsrc[(int64_t)g * a.nblk * 128 + (i - g * run)];
+        }
+      }
+    }
+    __syncthreads();
+
+    h8 A[2][MB][2], B[2][NB][2];
+    auto load = [&](int p, int g) {
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        A[p][mb][0] = hi8[hbase[mb] + toff[g]];
+        A[p][mb][1] = lo8[hbase[mb] + toff[g]];
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int wb = (g * WBLK + wn * NB + nb) * 128 + lane;
+        B[p][nb][0] = wl8[wb];
+        B[p][nb][1] = wl8[wb + 64];
+      }
+    };
+    load(0, 0);
+#pragma unroll
+    for (int g = 0; g < NTG; ++g) {
+      const int cur = g & 1;
+      if (g + 1 < NTG) load(cur ^ 1, g + 1);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][0], acc[mb][nb]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][1], acc[mb][nb]);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          acc[mb][nb] = mfma16x16x32h(A[cur][mb][1], B[cur][nb][0], acc[mb][nb]);
+    }
+  }
+  igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
+                                 ox0, a.out_scale);
+}
+
+// Split-fp16 weight packing: 16-byte words packed[((chunk * groups + g) * nblk + nb) * 128 +
+// part * 64 + lane] = part 0: hi h8, part 1: lo h8 of scale * W[n][tap 4g + lane/16][cin(chunk,
+// q)], q = 0..7, n = nb * 16 + lane % 16.
 __global__ void pack_conv_weight_x3_kernel(const float* __restrict__ w, uint4* __restrict__ out,
                                            int cout, int taps, int c1, int c2, int chunks1,
                                            int chunks, int groups, int nblk, float scale) {
@@ -683,8 +888,9 @@ __global__ void pack_conv_weight_x3_kernel(const float* __restrict__ w, uint4* _
       hv[q] = hh;
       lv[q] = ll;
     }
-    out[i * 2] = *reinterpret_cast<const uint4*>(&hv);
-    out[i * 2 + 1] = *reinterpret_cast<const uint4*>(&lv);
+    const int64_t word = (i - lane) * 2 + lane;  // block * 128 + lane
+    out[word] = *reinterpret_cast<const uint4*>(&hv);
+    out[word + 64] = *reinterpret_cast<const uint4*>(&lv);
   }
 }
 
@@ -716,7 +922,7 @@ int64_t halo_buffer_bytes(int64_t halo_voxels) {
   return ceil_div(halo_voxels * 2, kThreads) * kThreads * 16;
 }
 
-Box choose_box(const Variant& v, const ConvGeom& g, bool double_buffer) {
+Box choose_box(const Variant& v, const ConvGeom& g, bool double_buffer, int64_t max_halo = -1) {
   const int m = v.m();
   Box best{};
   bool have = false;
@@ -736,6 +942,7 @@ Box choose_box(const Variant& v, const ConvGeom& g, bool double_buffer) {
       c.hx = (bx - 1) * g.s[2] + g.k[2];
       const int64_t halo = (int64_t)c.hz * c.hy * c.hx;
       if (halo_buffer_bytes(halo) * (double_buffer ? 2 : 1) > kMaxLdsBytes) continue;
+      if (max_halo >= 0 && halo > max_halo) continue;
       c.tiles = ceil_div(g.out[0], bz) * ceil_div(g.out[1], by) * ceil_div(g.out[2], bx);
       // MFMA rows actually computed (padding waste) dominate; halo traffic breaks ties.
       const double score = (double)c.tiles * m + 0.25 * (double)c.tiles * halo;
@@ -779,8 +986,45 @@ void launch_x3(const IgemmArgs& a, hipStream_t st, double flops, double bytes) {
   const size_t red_bytes = (size_t)WM * 16 * NB * WN * sizeof(float);
   const size_t lds_bytes = halo_bytes > red_bytes ? halo_bytes : red_bytes;
   ProfScope prof(name.c_str(), flops, bytes, st);
-  hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
+  if (a.ntg == 7)
+    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, 7>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
+  else if (a.ntg == 3)
+    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, 3>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, 1>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
   launch_check("conv3d_x3");
+}
+
+template <int MB, int NB, int WM, int WN, int NTG>
+void launch_x3s_ntg(const IgemmArgs& a, bool vec, size_t lds_bytes, hipStream_t st) {
+  constexpr int nt = 64 * WM * WN;
+  if (vec)
+    hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, true>), dim3(a.nwg), dim3(nt),
+                       lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, false>), dim3(a.nwg), dim3(nt),
+                       lds_bytes, st, a);
+}
+
+size_t x3s_lds_bytes(int64_t halo_voxels, int ntg, int wblk) {
+  return (size_t)halo_voxels * 32 + (size_t)ntg * wblk * 128 * 16;
+}
+
+template <int MB, int NB, int WM, int WN>
+void launch_x3s(const IgemmArgs& a, bool vec, hipStream_t st, double flops, double bytes) {
+  static const std::string name = "conv3d_x3s_m" + std::to_string(16 * MB * WM) + "n" +
+                                  std::to_string(16 * NB * WN);
+  const size_t red_bytes = (size_t)WM * 16 * NB * WN * sizeof(float);
+  size_t lds_bytes = x3s_lds_bytes((int64_t)a.hz * a.hy * a.hx, a.ntg, WN * NB);
+  if (lds_bytes < red_bytes) lds_bytes = red_bytes;
+  ProfScope prof(name.c_str(), flops, bytes, st);
+  if (a.ntg == 7)
+    launch_x3s_ntg<MB, NB, WM, WN, 7>(a, vec, lds_bytes, st);
+  else if (a.ntg == 3)
+    launch_x3s_ntg<MB, NB, WM, WN, 3>(a, vec, lds_bytes, st);
+  else
+    launch_x3s_ntg<MB, NB, WM, WN, 1>(a, vec, lds_bytes, st);
+  launch_check("conv3d_x3s");
 }
 
 // ---------------------------------------------------------------------------------
@@ -1241,7 +1485,6 @@ float split_weight_scale(float max_abs) {
 }
 
 int conv_x3_groups(const int* ksize) { return (ksize[0] * ksize[1] * ksize[2] + 3) / 4; }
-
 int64_t conv_x3_packed_bytes(int cout, const int* ksize, int c1, int c2) {
   const int64_t chunks = ceil_div(c1, kChunk) + ceil_div(c2, kChunk);
   return chunks * conv_x3_groups(ksize) * conv_packed_nblk(cout) * 64 * 32;
@@ -1266,37 +1509,57 @@ void conv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int c1, i
 
 namespace {
 
-constexpr Variant kX3A{4, 2, 4, 1};  // M 256, N 32
-constexpr Variant kX3B{2, 4, 4, 1};  // M 128, N 64
+// register-staged kernels (strided convolutions, whose halos exceed the staged budget)
 constexpr Variant kX3C{2, 4, 2, 2};  // M 64,  N 128
-constexpr Variant kX3D{4, 4, 2, 2};  // M 128, N 128
-constexpr Variant kX3E{4, 4, 4, 1};  // M 256, N 64
-constexpr Variant kX3Table[] = {kX3A, kX3B, kX3C, kX3D, kX3E};
+constexpr Variant kX3F{2, 2, 2, 2};  // M 64,  N 64
+// halo voxels one workgroup can stage in registers (2 lines per voxel)
+constexpr int64_t kX3MaxHalo = (int64_t)kX3MaxLines * kX3Threads / 2;
+
+// LDS per workgroup of the weight-staged kernel that keeps 3 workgroups on a CU
+constexpr int64_t kX3sLdsBytes = 53 * 1024;
+constexpr Variant kX3S{4, 2, 4, 1};  // weight-staged: M 256, N 32
 
 struct X3Plan {
   Variant v;
   Box box;
+  bool staged;  // igemm_x3s_kernel
 };
 
+bool x3_groups_supported(int ntg) { return ntg == 1 || ntg == 3 || ntg == 7; }
+
+// Stride-1 convolutions use the weight-staged kernel (M 256, N 32 per workgroup) when a box
+// fits its LDS budget; the others (strided) use the register-staged kernel.
 X3Plan plan_x3(const ConvGeom& g, int cout) {
+  require(x3_groups_supported(conv_x3_groups(g.k)),
+          "split convolution supports 1-4, 9-12 or 25-28 kernel taps");
   X3Plan p{};
-  static const char* forced = std::getenv("NNX_X3_VARIANT");  // tuning override: table index
-  if (forced && *forced) {
-    const int i = std::atoi(forced);
-    require(i >= 0 && i < (int)(sizeof(kX3Table) / sizeof(kX3Table[0])), "bad NNX_X3_VARIANT");
-    p.v = kX3Table[i];
-  } else if (cout <= 32) {
-    p.v = kX3A;
-  } else if (cout <= 64) {
-    p.v = kX3B;
-  } else {
-    p.v = kX3C;
+  const int ntg = conv_x3_groups(g.k);
+  const int64_t wbytes = (int64_t)x3s_lds_bytes(0, ntg, kX3S.NB * kX3S.WN);
+  try {
+    p.box = choose_box(kX3S, g, false, (kX3sLdsBytes - wbytes) / 32);
+    p.v = kX3S;
+    p.staged = true;
+    return p;
+  } catch (const Error&) {
   }
-  p.box = choose_box(p.v, g, false);
+  p.v = cout <= 64 ? kX3F : kX3C;
+  p.box = choose_box(p.v, g, false, kX3MaxHalo);
+  p.staged = false;
   return p;
 }
 
 }  // namespace
+
+bool conv_x3_supported(const int* ksize, const int* stride, int cout) {
+  // the halo box depends on kernel and stride only; probe with a large volume
+  const int big[3] = {256, 256, 256};
+  try {
+    plan_x3(make_conv_geom(1, big, ksize, stride), cout);
+    return true;
+  } catch (const Error&) {
+    return false;
+  }
+}
 
 int conv_x3_stats_tiles(const ConvGeom& g, int cout) {
   const Box box = plan_x3(g, cout).box;
@@ -1315,18 +1578,19 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
   a.w16 = reinterpret_cast<const uint4*>(packed);
   a.ntg = conv_x3_groups(g.k);
   a.out_scale = 1.0f / scale;
+  require(plan.staged || (int64_t)a.hz * a.hy * a.hx <= kX3MaxHalo,
+          "split convolution halo exceeds the staging");
   double flops, bytes;
   igemm_work(g, c1, c2, cout, &flops, &bytes);
-  if (v.MB == 4 && v.NB == 2)
-    launch_x3<4, 2, 4, 1>(a, st, flops, bytes);
-  else if (v.MB == 2 && v.WN == 1)
-    launch_x3<2, 4, 4, 1>(a, st, flops, bytes);
-  else if (v.MB == 2)
+  if (plan.staged) {
+    const bool vec = c1 % kChunk == 0 && c2 % kChunk == 0;
+    launch_x3s<4, 2, 4, 1>(a, vec, st, flops, bytes);
+    return;
+  }
+  if (v.NB == 4)
     launch_x3<2, 4, 2, 2>(a, st, flops, bytes);
-  else if (v.WN == 2)
-    launch_x3<4, 4, 2, 2>(a, st, flops, bytes);
   else
-    launch_x3<4, 4, 4, 1>(a, st, flops, bytes);
+    launch_x3<2, 2, 2, 2>(a, st, flops, bytes);
 }
 
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,

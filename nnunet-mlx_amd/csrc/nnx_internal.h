@@ -132,6 +132,8 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
                float scale, const float* bias, float* y, const ConvGeom& g, int cout,
                hipStream_t st, float4* stats = nullptr);
 int conv_x3_stats_tiles(const ConvGeom& g, int cout);
+// Whether the split kernel handles this kernel size / stride (tap count and halo size).
+bool conv_x3_supported(const int* ksize, const int* stride, int cout);
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
                         const int* size, int cout, hipStream_t st);
 

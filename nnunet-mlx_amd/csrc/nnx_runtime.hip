@@ -340,7 +340,8 @@ void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
   // taps; 1x1x1 convolutions would waste 3/4 of it).  The first convolution reads the
   // raw network input, whose range is not normalised, so it keeps float32 products.
   const int taps = c.k[0] * c.k[1] * c.k[2];
-  c.split = m->precision == NNX_PRECISION_FP32_SPLIT && !c.first && taps >= 8;
+  c.split = m->precision == NNX_PRECISION_FP32_SPLIT && !c.first && taps >= 8 &&
+            conv_x3_supported(c.k, c.s, c.cout);
   if (c.split) {
     c.scale = split_weight_scale(m->params[c.pw].max_abs);
     c.packed.ensure((size_t)conv_x3_packed_bytes(c.cout, c.k, c.cin1, c.cin2));
