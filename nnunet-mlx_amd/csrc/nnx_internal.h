@@ -161,6 +161,10 @@ void instnorm_apply_params(const float* x, float* y, int batch, int64_t spatial,
 void avgpool3d(const float* x, float* y, int batch, const int* in_size, int channels,
                const int* kernel, hipStream_t st);
 
+// Centred crop / zero pad of an NDHWC tensor to out_size (the decoder's _match_spatial).
+void match_spatial(const float* x, const int* in_size, float* y, const int* out_size, int batch,
+                   int channels, hipStream_t st);
+
 void count_nonfinite(const float* x, int64_t n, unsigned int* count, hipStream_t st);
 
 void sw_gather_flip(const float* vol, int channels, const int64_t* size, const int* pad_before,

@@ -289,6 +289,34 @@ __global__ __launch_bounds__(256) void avgpool_kernel(const float* __restrict__ 
   }
 }
 
+// Centred crop / zero pad of an NDHWC tensor: out[b, z, y, x, c] = in[b, z + oz, y + oy,
+// x + ox, c] inside the input, 0 outside; offsets o = (in - out) / 2 truncated toward
+// zero (crop start delta // 2, or pad before (-delta) // 2).  VW channels per thread.
+template <int VW>
+__global__ __launch_bounds__(256) void match_spatial_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y, int64_t nout,
+                                                            int ID, int IH, int IW, int OD,
+                                                            int OH, int OW, int C, int oz,
+                                                            int oy, int ox) {
+  typedef float V __attribute__((ext_vector_type(VW)));
+  const int cv = C / VW;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nout;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(i % cv) * VW;
+    int64_t v = i / cv;
+    const int xx = (int)(v % OW) + ox;
+    v /= OW;
+    const int yy = (int)(v % OH) + oy;
+    v /= OH;
+    const int zz = (int)(v % OD) + oz;
+    const int64_t b = v / OD;
+    V r = {};
+    if ((unsigned)zz < (unsigned)ID && (unsigned)yy < (unsigned)IH && (unsigned)xx < (unsigned)IW)
+      r = *reinterpret_cast<const V*>(x + (((b * ID + zz) * IH + yy) * (int64_t)IW + xx) * C + c);
+    *reinterpret_cast<V*>(y + i * VW) = r;
+  }
+}
+
 __global__ __launch_bounds__(256) void nonfinite_kernel(const float* __restrict__ x, int64_t n,
                                                         unsigned int* count) {
   __shared__ unsigned int total;
@@ -424,6 +452,29 @@ void avgpool3d(const float* x, float* y, int batch, const int* in_size, int chan
   hipLaunchKernelGGL(avgpool_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, y, nout,
                      in_size[0], in_size[1], in_size[2], channels, kernel[0], kernel[1], kernel[2]);
   launch_check("avgpool3d");
+}
+
+void match_spatial(const float* x, const int* in_size, float* y, const int* out_size, int batch,
+                   int channels, hipStream_t st) {
+  require(x && y && x != y, "crop/pad needs distinct input and output buffers");
+  int off[3];
+  for (int i = 0; i < 3; ++i) {
+    require(in_size[i] >= 1 && out_size[i] >= 1, "crop/pad sizes must be positive");
+    off[i] = (in_size[i] - out_size[i]) / 2;
+  }
+  const int vw = channels % 4 == 0 ? 4 : 1;
+  const int64_t nout = (int64_t)batch * out_size[0] * out_size[1] * out_size[2] * (channels / vw);
+  const int64_t blocks = std::min<int64_t>(ceil_div(nout, 256), 65536);
+  ProfScope prof("match_spatial", 0.0, 8.0 * (double)nout * vw, st);
+  if (vw == 4)
+    hipLaunchKernelGGL(match_spatial_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, st, x, y,
+                       nout, in_size[0], in_size[1], in_size[2], out_size[0], out_size[1],
+                       out_size[2], channels, off[0], off[1], off[2]);
+  else
+    hipLaunchKernelGGL(match_spatial_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, st, x, y,
+                       nout, in_size[0], in_size[1], in_size[2], out_size[0], out_size[1],
+                       out_size[2], channels, off[0], off[1], off[2]);
+  launch_check("match_spatial");
 }
 
 void count_nonfinite(const float* x, int64_t n, unsigned int* count, hipStream_t st) {

@@ -446,14 +446,18 @@ struct Runner {
       Shape3 us;
       for (int i = 0; i < 3; ++i) us.d[i] = hs.d[i] * u.k[i];
       const Shape3& ss = skip_shapes[src - 1];
-      require(us == ss,
-              "decoder upsample does not match its skip connection; the patch size must be "
-              "divisible by the total stride of every axis");
       float* upbuf = plan->take((size_t)n * us.vox() * u.cout);
       if (!plan->planning)
         tconv3d_gemm(hidden, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d, u.cout,
                      u.k, st);
-      Shape3 cur = us;
+      if (!(us == ss)) {
+        // patch not divisible by the total stride: centre crop / zero pad the upsampled
+        // tensor to the skip's size (_match_spatial, src/nnunet_mlx/model/network.py:898-916)
+        float* matched = plan->take((size_t)n * ss.vox() * u.cout);
+        if (!plan->planning) match_spatial(upbuf, us.d, matched, ss.d, n, u.cout, st);
+        upbuf = matched;
+      }
+      Shape3 cur = ss;
       const float* a = upbuf;
       const float* b = skips[src - 1];
       float* h = nullptr;

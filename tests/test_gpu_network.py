@@ -54,6 +54,10 @@ CASES = {
                         (8, 8, 8), 1, True),
     "resenc-L": (resenc_spec(), (128, 64, 64), 1, True),
     "liver-128": (liver_spec(), (128, 128, 128), 1, True),
+    # patch not divisible by the total stride: the decoder centre-crops each upsample
+    "plain-nondivisible": (PlainConvUNetSpec(1, 3, (8, 16, 32), K3 * 3,
+                                             ((1, 1, 1), (2, 2, 2), (2, 2, 2)), (2, 2, 2), (2, 2)),
+                           (13, 18, 21), 2, True),
 }
 
 
@@ -92,5 +96,9 @@ def test_forward_rejects_bad_input(device):
     net.load_weights(random_weights(spec, seed=0))
     with pytest.raises(ContractError):
         net(torch.zeros((1, 8, 8, 8, 2), device=device))  # wrong channel count
+    res_spec = CASES["tiny-residual"][0]
+    res = build_network(res_spec)
+    res.load_weights(random_weights(res_spec, seed=0))
     with pytest.raises(ContractError):
-        net(torch.zeros((1, 9, 8, 8, 1), device=device))  # not divisible by the stride
+        # odd sizes: the stride-2 conv rounds up, the shortcut's average pool rounds down
+        res(torch.zeros((1, 9, 8, 8, 1), device=device))
