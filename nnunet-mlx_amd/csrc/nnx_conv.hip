@@ -132,7 +132,49 @@ struct IgemmArgs {
   const uint4* w16;   // split-fp16 packed weights (x3 kernel)
   int ntg;            // tap groups of 4 (x3 kernel)
   float out_scale;    // 1 / weight scale (x3 kernel)
+  // pending InstanceNorm (+ LeakyReLU) of input 0 / 1: (mean, scale, beta, 0) per (b, c)
+  const float4* nrm0;
+  const float4* nrm1;
+  int act0, act1;
+  float slope;
 };
+
+// The pending normalisation of one halo line (4 channels c..c+3 of the chunk's source):
+// parameters of missing channels (c + q >= C) are zero, so their zero loads stay zero.
+struct NormLine {
+  float m[4], s[4], b[4];
+  bool on, act;
+};
+
+__device__ __forceinline__ NormLine norm_line(const IgemmArgs& a, int chunk, int b, int C, int c) {
+  NormLine nl;
+  const bool first = chunk < a.chunks0;
+  const float4* p = first ? a.nrm0 : a.nrm1;
+  nl.on = p != nullptr;
+  nl.act = (first ? a.act0 : a.act1) != 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (nl.on && c + q < C) v = p[(int64_t)b * C + c + q];
+    nl.m[q] = v.x;
+    nl.s[q] = v.y;
+    nl.b[q] = v.z;
+  }
+  return nl;
+}
+
+// r = fma(x - mean, scale, beta), then max(slope * r, r): the operations of the InstanceNorm
+// apply pass, so a fused load produces the same bits.
+__device__ __forceinline__ f4 norm_apply4(f4 v, const NormLine& nl, float slope) {
+  f4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float t = fmaf(v[q] - nl.m[q], nl.s[q], nl.b[q]);
+    if (nl.act) t = fmaxf(slope * t, t);
+    r[q] = t;
+  }
+  return r;
+}
 
 // A zeroed 16-byte line: padding voxels of an asynchronously loaded halo read from here.
 __device__ __align__(16) float g_zero_line[4];
@@ -365,6 +407,8 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
       __syncthreads();                // ... and everyone's; the other buffer is free
     } else {
       const HaloSource hs = halo_source(a, chunk);
+      // every line i = tid + k*NT of this thread is half (tid & 1) of its voxel
+      const NormLine nl = norm_line(a, chunk, b, hs.C, hs.cb + (tid & 1) * 4);
       __syncthreads();
       for (int i = tid; i < nf4; i += NT) {
         const int v = i >> 1, h = i & 1;
@@ -385,6 +429,7 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
             for (int q = 0; q < 4; ++q)
               if (c + q < hs.C) val[q] = hs.src[off + q];
           }
+          if (nl.on) val = norm_apply4(val, nl, a.slope);
         }
         *reinterpret_cast<f4*>(lds + v * kChunk + h * 4) = val;
       }
@@ -578,6 +623,7 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
   auto fetch = [&](int chunk) {
     const HaloSource hs = halo_source(a, chunk);
     const int c = hs.cb + h * 4;
+    const NormLine nl = norm_line(a, chunk, b, hs.C, c);
 #pragma unroll
     for (int j = 0; j < kX3MaxLines; ++j) {
       f4 val = {0.f, 0.f, 0.f, 0.f};
@@ -590,6 +636,7 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
           for (int q = 0; q < 4; ++q)
             if (c + q < hs.C) val[q] = hs.src[off + q];
         }
+        if (nl.on) val = norm_apply4(val, nl, a.slope);
       }
       stage[j] = val;
     }
@@ -747,10 +794,12 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
   for (int chunk = 0; chunk < a.chunks; ++chunk) {
     const HaloSource hs = halo_source(a, chunk);
     const int c = hs.cb + h * 4;
+    const NormLine nl = norm_line(a, chunk, b, hs.C, c);
     __syncthreads();  // the previous chunk's fragments have been read
     // halo: batches of kX3MaxLines loads in flight, then split + store
     for (int base = 0; base < nlines; base += kX3MaxLines * NT) {
       f4 val[kX3MaxLines];
+      bool in[kX3MaxLines];
 #pragma unroll
       for (int j = 0; j < kX3MaxLines; ++j) {
         const int line = base + j * NT + tid;
@@ -766,6 +815,7 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
                    (unsigned)xx < (unsigned)a.iw;
           if (inside) src = hs.src + (bvox + (int64_t)(z * a.ih + yy) * a.iw + xx) * hs.C + c;
         }
+        in[j] = inside;
         if constexpr (VEC) {
           val[j] = *reinterpret_cast<const f4*>(src);
         } else {
@@ -781,6 +831,7 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
       for (int j = 0; j < kX3MaxLines; ++j) {
         const int line = base + j * NT + tid;
         if (line < nlines) {
+          if (nl.on && in[j]) val[j] = norm_apply4(val[j], nl, a.slope);
           h4 hv, lv;
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
@@ -1230,21 +1281,33 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void pw_gemm_kernel(PwArgs a) {
 // 1x1x1 convolution with few outputs (segmentation head): one thread per voxel, the
 // weights in LDS; s = fma chain over input channels, then + bias.
 // ---------------------------------------------------------------------------------
+// Pending InstanceNorm (+ LeakyReLU) of one input element (the apply pass's operations).
+__device__ __forceinline__ float norm_apply1(float v, float4 p, int act, float slope) {
+  float t = fmaf(v - p.x, p.y, p.z);
+  return act ? fmaxf(slope * t, t) : t;
+}
+
 __global__ __launch_bounds__(256) void conv1x1_kernel(const float* __restrict__ x,
                                                       const float* __restrict__ w,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int64_t nvox,
-                                                      int cin, int cout) {
+                                                      int cin, int cout,
+                                                      const float4* __restrict__ nrm, int act,
+                                                      float slope, int64_t item_vox) {
   extern __shared__ float ws[];  // cout * cin
   for (int i = threadIdx.x; i < cout * cin; i += blockDim.x) ws[i] = w[i];
   __syncthreads();
   const int64_t vox = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (vox >= nvox) return;
   const float* xr = x + vox * cin;
+  const float4* pr = nrm ? nrm + (vox / item_vox) * cin : nullptr;
   for (int o = 0; o < cout; ++o) {
     float s = 0.f;
     const float* wr = ws + o * cin;
-    for (int c = 0; c < cin; ++c) s = fmaf(xr[c], wr[c], s);
+    for (int c = 0; c < cin; ++c) {
+      const float xv = pr ? norm_apply1(xr[c], pr[c], act, slope) : xr[c];
+      s = fmaf(xv, wr[c], s);
+    }
     y[vox * cout + o] = bias ? s + bias[o] : s;
   }
 }
@@ -1256,7 +1319,10 @@ __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __rest
                                                              const float* __restrict__ w,
                                                              const float* __restrict__ bias,
                                                              float* __restrict__ y, int64_t nvox,
-                                                             int cin, int cout) {
+                                                             int cin, int cout,
+                                                             const float4* __restrict__ nrm,
+                                                             int act, float slope,
+                                                             int64_t item_vox) {
   extern __shared__ float smem[];
   float* ws = smem;                          // cout * cin
   float* xs = smem + cout * cin;             // 256 * (cin + 1)
@@ -1267,9 +1333,16 @@ __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __rest
   const float4* src = reinterpret_cast<const float4*>(x + v0 * cin);
   const int total4 = nv * cin / 4;
   for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
-    const float4 v = src[e4];
+    float4 v = src[e4];
     const int e = e4 * 4;
     const int r = e / cin, c = e - r * cin;
+    if (nrm) {
+      const float4* pr = nrm + ((v0 + r) / item_vox) * cin + c;
+      v.x = norm_apply1(v.x, pr[0], act, slope);
+      v.y = norm_apply1(v.y, pr[1], act, slope);
+      v.z = norm_apply1(v.z, pr[2], act, slope);
+      v.w = norm_apply1(v.w, pr[3], act, slope);
+    }
     float* d = xs + r * (cin + 1) + c;
     d[0] = v.x;
     d[1] = v.y;
@@ -1388,8 +1461,15 @@ namespace {
 // Geometry, box and grid fields shared by both implicit-GEMM kernels.
 IgemmArgs igemm_args(const float* x1, int c1, const float* x2, int c2, const float* bias,
                      float* y, const ConvGeom& g, int cout, const Variant& v, const Box& box,
-                     float4* stats) {
+                     float4* stats, const PendingNorm& n1, const PendingNorm& n2) {
+  require(!(n1.params && n2.params) || n1.slope == n2.slope,
+          "pending normalisations of one convolution must share the LeakyReLU slope");
   IgemmArgs a{};
+  a.nrm0 = n1.params;
+  a.nrm1 = n2.params;
+  a.act0 = n1.act ? 1 : 0;
+  a.act1 = n2.act ? 1 : 0;
+  a.slope = n1.params ? n1.slope : n2.slope;
   a.x0 = x1;
   a.x1 = x2;
   a.c0 = c1;
@@ -1450,13 +1530,14 @@ void igemm_work(const ConvGeom& g, int c1, int c2, int cout, double* flops, doub
 
 void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
                   const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st,
-                  float4* stats) {
+                  float4* stats, const PendingNorm& n1, const PendingNorm& n2) {
   require(x1 && y && packed, "convolution pointers must not be null");
   require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
   const IgemmPlan plan = plan_igemm(g, cout, c1, c2);
   const Variant v = plan.v;
-  const bool async = plan.async;
-  IgemmArgs a = igemm_args(x1, c1, x2, c2, bias, y, g, cout, v, plan.box, stats);
+  // the DMA halo path copies lines unchanged: pending normalisations need the register path
+  const bool async = plan.async && !n1.params && !n2.params;
+  IgemmArgs a = igemm_args(x1, c1, x2, c2, bias, y, g, cout, v, plan.box, stats, n1, n2);
   a.w = reinterpret_cast<const f2*>(packed);
   double flops, bytes;
   igemm_work(g, c1, c2, cout, &flops, &bytes);
@@ -1568,13 +1649,13 @@ int conv_x3_stats_tiles(const ConvGeom& g, int cout) {
 
 void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* packed,
                float scale, const float* bias, float* y, const ConvGeom& g, int cout,
-               hipStream_t st, float4* stats) {
+               hipStream_t st, float4* stats, const PendingNorm& n1, const PendingNorm& n2) {
   require(x1 && y && packed, "convolution pointers must not be null");
   require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
   require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
   const X3Plan plan = plan_x3(g, cout);
   const Variant v = plan.v;
-  IgemmArgs a = igemm_args(x1, c1, x2, c2, bias, y, g, cout, v, plan.box, stats);
+  IgemmArgs a = igemm_args(x1, c1, x2, c2, bias, y, g, cout, v, plan.box, stats, n1, n2);
   a.w16 = reinterpret_cast<const uint4*>(packed);
   a.ntg = conv_x3_groups(g.k);
   a.out_scale = 1.0f / scale;
@@ -1662,8 +1743,12 @@ void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bia
 }
 
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y, int64_t voxels,
-             int cout, hipStream_t st) {
+             int cout, hipStream_t st, const PendingNorm& nx, int64_t item_voxels) {
   require(x && w && y, "1x1 convolution pointers must not be null");
+  require(!nx.params || (item_voxels >= 1 && voxels % item_voxels == 0),
+          "a pending normalisation needs the voxels per batch item");
+  const int64_t item = nx.params ? item_voxels : 1;
+  const int act = nx.act ? 1 : 0;
   require(cin >= 1 && cout >= 1 && (int64_t)cin * cout <= 16384,
           "1x1 convolution weight too large for the head kernel");
   require(voxels >= 1, "empty 1x1 convolution input");
@@ -1671,10 +1756,12 @@ void conv1x1(const float* x, int cin, const float* w, const float* bias, float* 
   const size_t staged = ((size_t)cin * cout + 256 * (cin + 1) + 256 * cout) * sizeof(float);
   if (cin % 4 == 0 && staged <= 64 * 1024)
     hipLaunchKernelGGL(conv1x1_staged_kernel, dim3((unsigned)ceil_div(voxels, 256)), dim3(256),
-                       staged, st, x, w, bias, y, voxels, cin, cout);
+                       staged, st, x, w, bias, y, voxels, cin, cout, nx.params, act, nx.slope,
+                       item);
   else
     hipLaunchKernelGGL(conv1x1_kernel, dim3((unsigned)ceil_div(voxels, 256)), dim3(256),
-                       (size_t)cin * cout * sizeof(float), st, x, w, bias, y, voxels, cin, cout);
+                       (size_t)cin * cout * sizeof(float), st, x, w, bias, y, voxels, cin, cout,
+                       nx.params, act, nx.slope, item);
   launch_check("conv1x1");
 }
 

@@ -112,12 +112,23 @@ ConvGeom make_conv_geom(int batch, const int* in_size, const int* ksize, const i
 int64_t conv_packed_floats(int cout, const int* ksize, int c1, int c2);
 void conv_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int c2,
                       float* d_packed, hipStream_t st);
+// A convolution input may carry a pending InstanceNorm (+ LeakyReLU): its consumer applies
+// r = fma(x - mean, scale, beta), then max(slope * r, r) when `act`, to every in-volume
+// element it loads, with the same float32 operations as instnorm_apply_params (the zero
+// padding stays zero).  `params` = (mean, scale, beta, 0) per (batch item, channel).
+struct PendingNorm {
+  const float4* params = nullptr;  // null: the tensor is already final
+  bool act = false;
+  float slope = 0.f;
+};
+
 // When `stats` is given, the epilogue also writes InstanceNorm partials
 // stats[(b * tiles + tile) * cout + c] = (tile mean, tile M2, tile voxel count, 0) of
 // (conv + bias); `tiles` = conv_stats_tiles(...) per batch item.
 void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float* packed,
                   const float* bias, float* y, const ConvGeom& g, int cout, hipStream_t st,
-                  float4* stats = nullptr);
+                  float4* stats = nullptr, const PendingNorm& n1 = {},
+                  const PendingNorm& n2 = {});
 int conv_stats_tiles(const ConvGeom& g, int cout, int c1, int c2);
 
 // Split-fp16 implicit GEMM: float32 operands split into fp16 high/low halves, three MFMA
@@ -130,7 +141,8 @@ void conv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int c1, i
                          float scale, void* d_packed, hipStream_t st);
 void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* packed,
                float scale, const float* bias, float* y, const ConvGeom& g, int cout,
-               hipStream_t st, float4* stats = nullptr);
+               hipStream_t st, float4* stats = nullptr, const PendingNorm& n1 = {},
+               const PendingNorm& n2 = {});
 int conv_x3_stats_tiles(const ConvGeom& g, int cout);
 // Whether the split kernel handles this kernel size / stride (tap count and halo size).
 bool conv_x3_supported(const int* ksize, const int* stride, int cout);
@@ -142,22 +154,30 @@ void tconv_pack_weight(const float* d_w, int cout, const int* ksize, int cin, fl
                        hipStream_t st);
 void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bias, float* y,
                   int batch, const int* in_size, int cout, const int* ksize, hipStream_t st);
+// `item_voxels` = voxels per batch item (to index the pending norm's parameters).
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y,
-             int64_t voxels, int cout, hipStream_t st);
+             int64_t voxels, int cout, hipStream_t st, const PendingNorm& nx = {},
+             int64_t item_voxels = 0);
 
 size_t instnorm_workspace_bytes(int batch, int64_t spatial, int channels);
 void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int channels,
                     const float* input_bias, const float* gamma, const float* beta, float eps,
                     bool act, float slope, const float* residual, void* ws, size_t ws_bytes,
                     hipStream_t st);
-// InstanceNorm from precomputed partials: merge (mean, M2, n) partials of each (b, c)
-// into (mean, gamma*rsqrt(var+eps)) params, then apply; `params` holds batch*channels float2.
+// InstanceNorm parameters only: params[b * channels + c] = (mean, gamma*rsqrt(var+eps), beta,
+// 0) of (x + input_bias); written to `params`, or into the workspace when params is null.
+void instnorm_params(const float* x, int batch, int64_t spatial, int channels,
+                     const float* input_bias, const float* gamma, const float* beta, float eps,
+                     void* ws, size_t ws_bytes, float4* params, hipStream_t st);
+// The same parameters from per-tile partials (mean, M2, n, 0) written by a convolution
+// epilogue.
 void instnorm_merge_partials(const float4* partials, int nparts, int batch, int64_t spatial,
-                             int channels, const float* gamma, float eps, float2* params,
-                             hipStream_t st);
+                             int channels, const float* gamma, const float* beta, float eps,
+                             float4* params, hipStream_t st);
+// y = LeakyReLU?(fma(x + input_bias - mean, scale, beta) (+ residual)), elementwise.
 void instnorm_apply_params(const float* x, float* y, int batch, int64_t spatial, int channels,
-                           const float2* params, const float* input_bias, const float* beta,
-                           bool act, float slope, const float* residual, hipStream_t st);
+                           const float4* params, const float* input_bias, bool act, float slope,
+                           const float* residual, hipStream_t st);
 void avgpool3d(const float* x, float* y, int batch, const int* in_size, int channels,
                const int* kernel, hipStream_t st);
 

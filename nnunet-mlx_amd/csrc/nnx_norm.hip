@@ -140,7 +140,8 @@ __device__ __forceinline__ void chan_merge(double& na, double& ma, double& m2a, 
 }
 
 __global__ __launch_bounds__(256) void norm_merge_kernel(const float2* __restrict__ partial,
-                                                         float2* __restrict__ params,
+                                                         float4* __restrict__ params,
+                                                         const float* __restrict__ beta,
                                                          const float* __restrict__ gamma,
                                                          int64_t S, int C, int nchunks,
                                                          int chunk_vox, float eps) {
@@ -174,14 +175,15 @@ __global__ __launch_bounds__(256) void norm_merge_kernel(const float2* __restric
     float varf = (float)(var > 0.0 ? var : 0.0);
     float scale = 1.0f / sqrtf(varf + eps);
     if (gamma) scale = gamma[c] * scale;
-    params[(int64_t)b * C + c] = make_float2((float)sm[0], scale);
+    params[(int64_t)b * C + c] = make_float4((float)sm[0], scale, beta ? beta[c] : 0.f, 0.f);
   }
 }
 
 // Same merge for partials that carry their own counts (per-tile partials written by the
 // convolution epilogue: (mean, M2, n, 0)).
 __global__ __launch_bounds__(256) void norm_merge_counted_kernel(const float4* __restrict__ partial,
-                                                                 float2* __restrict__ params,
+                                                                 float4* __restrict__ params,
+                                                                 const float* __restrict__ beta,
                                                                  const float* __restrict__ gamma,
                                                                  int64_t S, int C, int nparts,
                                                                  float eps) {
@@ -213,15 +215,14 @@ __global__ __launch_bounds__(256) void norm_merge_counted_kernel(const float4* _
     float varf = (float)(var > 0.0 ? var : 0.0);
     float scale = 1.0f / sqrtf(varf + eps);
     if (gamma) scale = gamma[c] * scale;
-    params[(int64_t)b * C + c] = make_float2((float)sm[0], scale);
+    params[(int64_t)b * C + c] = make_float4((float)sm[0], scale, beta ? beta[c] : 0.f, 0.f);
   }
 }
 
 template <int VW>
 __global__ __launch_bounds__(256) void norm_apply_kernel(
-    const float* x, float* y, const float2* __restrict__ params, const float* __restrict__ in_bias,
-    const float* __restrict__ beta, const float* residual, int64_t SC, int C, int act,
-    float slope) {
+    const float* x, float* y, const float4* __restrict__ params, const float* __restrict__ in_bias,
+    const float* residual, int64_t SC, int C, int act, float slope) {
   typedef typename Vec<VW>::type V;
   extern __shared__ float smem[];  // C * 4: mean, scale, beta, input bias
   float* s_mean = smem;
@@ -230,10 +231,10 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(
   float* s_bias = smem + 3 * C;
   const int b = blockIdx.y;
   for (int i = threadIdx.x; i < C; i += blockDim.x) {
-    const float2 p = params[(int64_t)b * C + i];
+    const float4 p = params[(int64_t)b * C + i];
     s_mean[i] = p.x;
     s_scale[i] = p.y;
-    s_beta[i] = beta ? beta[i] : 0.f;
+    s_beta[i] = p.z;
     s_bias[i] = in_bias ? in_bias[i] : 0.f;
   }
   __syncthreads();
@@ -364,15 +365,14 @@ StatsLayout stats_layout(int64_t spatial, int channels) {
 size_t instnorm_workspace_bytes(int batch, int64_t spatial, int channels) {
   const StatsLayout l = stats_layout(spatial, channels);
   const size_t partial = (size_t)batch * l.nchunks * channels * sizeof(float2);
-  const size_t params = (size_t)batch * channels * sizeof(float2);
+  const size_t params = (size_t)batch * channels * sizeof(float4);
   return ((partial + 255) / 256) * 256 + params;
 }
 
-void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int channels,
-                    const float* input_bias, const float* gamma, const float* beta, float eps,
-                    bool act, float slope, const float* residual, void* ws, size_t ws_bytes,
-                    hipStream_t st) {
-  require(x && y, "instance normalisation pointers must not be null");
+void instnorm_params(const float* x, int batch, int64_t spatial, int channels,
+                     const float* input_bias, const float* gamma, const float* beta, float eps,
+                     void* ws, size_t ws_bytes, float4* params, hipStream_t st) {
+  require(x != nullptr, "instance normalisation pointers must not be null");
   require(batch >= 1 && spatial >= 1 && channels >= 1, "instance normalisation needs a non-empty tensor");
   require(eps > 0.f, "instance-normalization epsilon must be positive");
   require(batch <= 65535, "instance normalisation batch too large");
@@ -382,8 +382,9 @@ void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int ch
           "instance normalisation workspace too small");
   float2* partial = reinterpret_cast<float2*>(ws);
   const size_t partial_bytes = (size_t)batch * l.nchunks * channels * sizeof(float2);
-  float2* params = reinterpret_cast<float2*>(reinterpret_cast<char*>(ws) +
-                                             ((partial_bytes + 255) / 256) * 256);
+  if (!params)
+    params = reinterpret_cast<float4*>(reinterpret_cast<char*>(ws) +
+                                       ((partial_bytes + 255) / 256) * 256);
   const dim3 sgrid((unsigned)l.nchunks, (unsigned)batch);
   const double nelem = (double)batch * spatial * channels;
   {
@@ -399,27 +400,40 @@ void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int ch
   {
   ProfScope prof("instnorm_merge", 0.0, 8.0 * (double)batch * l.nchunks * channels, st);
   hipLaunchKernelGGL(norm_merge_kernel, dim3(channels, batch), dim3(256), 0, st, partial, params,
-                     gamma, spatial, channels, (int)l.nchunks, l.chunk_vox, eps);
+                     beta, gamma, spatial, channels, (int)l.nchunks, l.chunk_vox, eps);
   launch_check("instnorm merge");
   }
-  instnorm_apply_params(x, y, batch, spatial, channels, params, input_bias, beta, act, slope,
-                        residual, st);
+}
+
+void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int channels,
+                    const float* input_bias, const float* gamma, const float* beta, float eps,
+                    bool act, float slope, const float* residual, void* ws, size_t ws_bytes,
+                    hipStream_t st) {
+  require(x && y, "instance normalisation pointers must not be null");
+  instnorm_params(x, batch, spatial, channels, input_bias, gamma, beta, eps, ws, ws_bytes,
+                  nullptr, st);
+  const StatsLayout l = stats_layout(spatial, channels);
+  const size_t partial_bytes = (size_t)batch * l.nchunks * channels * sizeof(float2);
+  const float4* params = reinterpret_cast<const float4*>(reinterpret_cast<char*>(ws) +
+                                                         ((partial_bytes + 255) / 256) * 256);
+  instnorm_apply_params(x, y, batch, spatial, channels, params, input_bias, act, slope, residual,
+                        st);
 }
 
 void instnorm_merge_partials(const float4* partials, int nparts, int batch, int64_t spatial,
-                             int channels, const float* gamma, float eps, float2* params,
-                             hipStream_t st) {
+                             int channels, const float* gamma, const float* beta, float eps,
+                             float4* params, hipStream_t st) {
   require(partials && params, "instance normalisation partials must not be null");
   require(nparts >= 1 && batch >= 1 && batch <= 65535 && channels >= 1, "invalid partial layout");
   ProfScope prof("instnorm_merge", 0.0, 16.0 * (double)batch * nparts * channels, st);
   hipLaunchKernelGGL(norm_merge_counted_kernel, dim3(channels, batch), dim3(256), 0, st, partials,
-                     params, gamma, spatial, channels, nparts, eps);
+                     params, beta, gamma, spatial, channels, nparts, eps);
   launch_check("instnorm merge partials");
 }
 
 void instnorm_apply_params(const float* x, float* y, int batch, int64_t spatial, int channels,
-                           const float2* params, const float* input_bias, const float* beta,
-                           bool act, float slope, const float* residual, hipStream_t st) {
+                           const float4* params, const float* input_bias, bool act, float slope,
+                           const float* residual, hipStream_t st) {
   require(x && y && params, "instance normalisation pointers must not be null");
   require(channels <= 1024, "instance normalisation supports at most 1024 channels");
   const int vw = channels % 4 == 0 ? 4 : 1;
@@ -431,12 +445,12 @@ void instnorm_apply_params(const float* x, float* y, int batch, int64_t spatial,
   const size_t smem = (size_t)channels * 4 * sizeof(float);
   if (vw == 4)
     hipLaunchKernelGGL(norm_apply_kernel<4>, dim3((unsigned)std::max<int64_t>(blocks, 1), batch),
-                       dim3(256), smem, st, x, y, params, input_bias, beta, residual, sc,
-                       channels, act ? 1 : 0, slope);
+                       dim3(256), smem, st, x, y, params, input_bias, residual, sc, channels,
+                       act ? 1 : 0, slope);
   else
     hipLaunchKernelGGL(norm_apply_kernel<1>, dim3((unsigned)std::max<int64_t>(blocks, 1), batch),
-                       dim3(256), smem, st, x, y, params, input_bias, beta, residual, sc,
-                       channels, act ? 1 : 0, slope);
+                       dim3(256), smem, st, x, y, params, input_bias, residual, sc, channels,
+                       act ? 1 : 0, slope);
   launch_check("instnorm apply");
 }
 

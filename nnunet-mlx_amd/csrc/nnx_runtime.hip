@@ -179,8 +179,6 @@ struct Workspace {
   size_t norm_ws_bytes = 0;
   DevBuf stats;   // per-tile InstanceNorm partials written by the conv epilogue
   size_t stats_bytes = 0;
-  DevBuf params;  // (mean, scale) per (b, c)
-  size_t params_bytes = 0;
   float* get(size_t i) { return bufs[i]->as<float>(); }
 };
 
@@ -367,7 +365,6 @@ struct Planner {
   std::vector<size_t> sizes;
   size_t norm_ws = 0;
   size_t stats = 0;
-  size_t params = 0;
   size_t next = 0;
   bool planning = true;
   Workspace* ws = nullptr;
@@ -381,75 +378,98 @@ struct Planner {
   }
 };
 
+// An activation as its consumer sees it: the buffer, plus the InstanceNorm (+ LeakyReLU)
+// still to be applied to it when the producer deferred its apply pass to the consumer.
+struct Act {
+  const float* data = nullptr;
+  PendingNorm norm;
+};
+
 struct Runner {
   nnx_model* m;
   Planner* plan;
   hipStream_t st;
   int n;
 
-  void convnorm(const ConvNorm& c, const float* x1, const float* x2, const Shape3& in, float* out,
-                const Shape3& outs, const float* residual) {
+  // Conv + InstanceNorm (+ LeakyReLU).  With `defer` (every consumer of the output is a
+  // convolution or the segmentation head, which normalise on load) the apply pass is
+  // skipped and the output carries its parameters; otherwise it is applied in place
+  // (with the residual addition for a residual block's last convolution).
+  Act convnorm(const ConvNorm& c, const Act& x1, const Act& x2, const Shape3& in, float* out,
+               const Shape3& outs, const float* residual, bool defer) {
     const int64_t vox = outs.vox();
     // A residual block's last ConvNorm has no activation of its own; LeakyReLU follows the
     // residual addition (ResidualBlock.__call__), fused into the same apply pass.
     const bool act = c.act || residual != nullptr;
+    require(!(defer && residual), "a residual sum cannot be deferred");
+    float4* params = reinterpret_cast<float4*>(plan->take((size_t)n * c.cout * 4));
+    Act result;
+    result.data = out;
+    if (defer) result.norm = PendingNorm{params, act, m->slope};
     if (c.direct) {
+      require(!x1.norm.params, "the one-channel convolution reads the network input");
       const size_t nbytes = instnorm_workspace_bytes(n, vox, c.cout);
       if (plan->planning) {
         plan->norm_ws = std::max(plan->norm_ws, nbytes);
-        return;
+        return result;
       }
-      conv3d_direct_cin1(x1, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st);
-      instnorm_lrelu(out, out, n, vox, c.cout, nullptr, pdev(m, c.pg), pdev(m, c.pbeta), m->eps,
-                     act, m->slope, residual, plan->ws->norm_ws.ptr, plan->ws->norm_ws_bytes, st);
-      return;
+      conv3d_direct_cin1(x1.data, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st);
+      instnorm_params(out, n, vox, c.cout, nullptr, pdev(m, c.pg), pdev(m, c.pbeta), m->eps,
+                      plan->ws->norm_ws.ptr, plan->ws->norm_ws_bytes, params, st);
+      if (!defer)
+        instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, act, m->slope, residual,
+                              st);
+      return result;
     }
-    // Implicit GEMM: the epilogue writes per-tile statistics, so the norm reads the
-    // tensor once (apply) instead of twice.
+    // Implicit GEMM: the epilogue writes per-tile statistics, so the norm never re-reads the
+    // tensor for them.
     const ConvGeom g = make_conv_geom(n, in.d, c.k, c.s);
     const int tiles = c.split ? conv_x3_stats_tiles(g, c.cout)
                               : conv_stats_tiles(g, c.cout, c.cin1, c.cin2);
     if (plan->planning) {
       plan->stats = std::max(plan->stats, (size_t)n * tiles * c.cout * sizeof(float4));
-      plan->params = std::max(plan->params, (size_t)n * c.cout * sizeof(float2));
-      return;
+      return result;
     }
     float4* stats = plan->ws->stats.as<float4>();
-    float2* params = plan->ws->params.as<float2>();
     if (c.split)
-      conv3d_x3(x1, c.cin1, x2, c.cin2, c.packed.ptr, c.scale, pdev(m, c.pb), out, g, c.cout, st,
-                stats);
+      conv3d_x3(x1.data, c.cin1, x2.data, c.cin2, c.packed.ptr, c.scale, pdev(m, c.pb), out, g,
+                c.cout, st, stats, x1.norm, x2.norm);
     else
-      conv3d_igemm(x1, c.cin1, x2, c.cin2, c.packed.as<float>(), pdev(m, c.pb), out, g, c.cout,
-                   st, stats);
-    instnorm_merge_partials(stats, tiles, n, vox, c.cout, pdev(m, c.pg), m->eps, params, st);
-    instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, pdev(m, c.pbeta), act,
-                          m->slope, residual, st);
+      conv3d_igemm(x1.data, c.cin1, x2.data, c.cin2, c.packed.as<float>(), pdev(m, c.pb), out, g,
+                   c.cout, st, stats, x1.norm, x2.norm);
+    instnorm_merge_partials(stats, tiles, n, vox, c.cout, pdev(m, c.pg), pdev(m, c.pbeta), m->eps,
+                            params, st);
+    if (!defer)
+      instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, act, m->slope, residual,
+                            st);
+    return result;
   }
 
-  // Returns the output buffer; *outs receives its spatial shape.
-  float* run_convnorm(const ConvNorm& c, const float* x1, const float* x2, const Shape3& in,
-                      Shape3* outs, const float* residual = nullptr) {
+  // *outs receives the output's spatial shape.
+  Act run_convnorm(const ConvNorm& c, const Act& x1, const Act& x2, const Shape3& in,
+                   Shape3* outs, bool defer, const float* residual = nullptr) {
     *outs = conv_out(in, c);
     float* out = plan->take((size_t)n * outs->vox() * c.cout);
-    convnorm(c, x1, x2, in, out, *outs, residual);
-    return out;
+    return convnorm(c, x1, x2, in, out, *outs, residual, defer);
   }
 
-  float* decode(std::vector<float*>& skips, std::vector<Shape3>& skip_shapes, float* d_out) {
+  // The decoder.  Its last stage feeds the segmentation head, which normalises on load;
+  // every other stage's last output feeds a transposed convolution and is applied.
+  void decode(std::vector<Act>& skips, std::vector<Shape3>& skip_shapes, float* d_out) {
     const int S = m->stages;
-    float* hidden = skips[S - 1];
+    Act hidden = skips[S - 1];
     Shape3 hs = skip_shapes[S - 1];
     for (int d = 0; d < S - 1; ++d) {
       const int src = S - 1 - d;
       const Upsample& u = m->up[d];
+      require(!hidden.norm.params, "transposed convolution inputs are applied tensors");
       Shape3 us;
       for (int i = 0; i < 3; ++i) us.d[i] = hs.d[i] * u.k[i];
       const Shape3& ss = skip_shapes[src - 1];
       float* upbuf = plan->take((size_t)n * us.vox() * u.cout);
       if (!plan->planning)
-        tconv3d_gemm(hidden, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d, u.cout,
-                     u.k, st);
+        tconv3d_gemm(hidden.data, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d,
+                     u.cout, u.k, st);
       if (!(us == ss)) {
         // patch not divisible by the total stride: centre crop / zero pad the upsampled
         // tensor to the skip's size (_match_spatial, src/nnunet_mlx/model/network.py:898-916)
@@ -458,55 +478,60 @@ struct Runner {
         upbuf = matched;
       }
       Shape3 cur = ss;
-      const float* a = upbuf;
-      const float* b = skips[src - 1];
-      float* h = nullptr;
-      for (size_t j = 0; j < m->dec[d].size(); ++j) {
+      Act a;
+      a.data = upbuf;
+      const size_t nb = m->dec[d].size();
+      for (size_t j = 0; j < nb; ++j) {
         Shape3 o;
-        h = run_convnorm(m->dec[d][j], a, j == 0 ? b : nullptr, cur, &o);
-        a = h;
+        const bool defer = j + 1 < nb || d == S - 2;
+        a = run_convnorm(m->dec[d][j], a, j == 0 ? skips[src - 1] : Act{}, cur, &o, defer);
         cur = o;
       }
-      hidden = h;
+      hidden = a;
       hs = cur;
     }
     const SegHead& sh = m->seg[S - 2];
     if (!plan->planning)
-      conv1x1(hidden, sh.cin, pdev(m, sh.pw), pdev(m, sh.pb), d_out, (int64_t)n * hs.vox(),
-              sh.cout, st);
-    return d_out;
+      conv1x1(hidden.data, sh.cin, pdev(m, sh.pw), pdev(m, sh.pb), d_out, (int64_t)n * hs.vox(),
+              sh.cout, st, hidden.norm, hs.vox());
   }
 
   void forward_plain(const float* x, const Shape3& in, float* d_out) {
     const int S = m->stages;
-    std::vector<float*> skips(S);
+    std::vector<Act> skips(S);
     std::vector<Shape3> shapes(S);
-    const float* h = x;
+    Act h;
+    h.data = x;
     Shape3 cur = in;
     for (int s = 0; s < S; ++s) {
-      float* out = nullptr;
-      for (size_t j = 0; j < m->enc[s].size(); ++j) {
+      const size_t nb = m->enc[s].size();
+      for (size_t j = 0; j < nb; ++j) {
         Shape3 o;
-        out = run_convnorm(m->enc[s][j], h, nullptr, cur, &o);
-        h = out;
+        // the bottleneck's output feeds the first transposed convolution
+        const bool defer = !(s == S - 1 && j + 1 == nb);
+        h = run_convnorm(m->enc[s][j], h, Act{}, cur, &o, defer);
         cur = o;
       }
-      skips[s] = out;
+      skips[s] = h;
       shapes[s] = cur;
     }
     decode(skips, shapes, d_out);
   }
 
+  // Residual encoder: block outputs (residual sums) and the stem are applied tensors; the
+  // inner convolutions of a block defer to the next convolution of the block.
   void forward_residual(const float* x, const Shape3& in, float* d_out) {
     const int S = m->stages;
-    std::vector<float*> skips(S);
+    std::vector<Act> skips(S);
     std::vector<Shape3> shapes(S);
     Shape3 cur;
-    float* h = run_convnorm(m->stem, x, nullptr, in, &cur);
+    Act xin;
+    xin.data = x;
+    Act h = run_convnorm(m->stem, xin, Act{}, in, &cur, false);
     for (int s = 0; s < S; ++s) {
       for (auto& rb : m->res[s]) {
         // skip path: pool (stride) then 1x1 projection (channel change)
-        const float* residual = h;
+        const float* residual = h.data;
         Shape3 rs = cur;
         const int cin = rb.convs[0].cin1;
         if (rb.pool) {
@@ -516,17 +541,18 @@ struct Runner {
             rs.d[i] = cur.d[i] / rb.pool_k[i];
           }
           float* pooled = plan->take((size_t)n * rs.vox() * cin);
-          if (!plan->planning) avgpool3d(h, pooled, n, cur.d, cin, rb.pool_k, st);
+          if (!plan->planning) avgpool3d(h.data, pooled, n, cur.d, cin, rb.pool_k, st);
           residual = pooled;
         }
         if (rb.proj) {
           Shape3 ps;
-          residual = run_convnorm(rb.projc, residual, nullptr, rs, &ps);
+          Act r;
+          r.data = residual;
+          residual = run_convnorm(rb.projc, r, Act{}, rs, &ps, false).data;
           rs = ps;
         }
-        const float* a = h;
+        Act a = h;
         Shape3 as = cur;
-        float* out = nullptr;
         for (size_t j = 0; j < rb.convs.size(); ++j) {
           Shape3 o;
           const bool last = j + 1 == rb.convs.size();
@@ -534,12 +560,11 @@ struct Runner {
             o = conv_out(as, rb.convs[j]);
             require(o == rs, "residual branch and shortcut shapes differ");
           }
-          out = run_convnorm(rb.convs[j], a, nullptr, as, &o, last ? residual : nullptr);
-          a = out;
+          // the last conv has no activation of its own: LeakyReLU follows the residual add
+          a = run_convnorm(rb.convs[j], a, Act{}, as, &o, !last, last ? residual : nullptr);
           as = o;
         }
-        // last conv has no activation of its own: apply LeakyReLU after the residual add
-        h = out;
+        h = a;
         cur = as;
       }
       skips[s] = h;
@@ -577,10 +602,6 @@ void ensure_workspace(nnx_model* m, int n, const Shape3& in) {
   if (plan.stats > ws.stats_bytes) {
     ws.stats.ensure(plan.stats);
     ws.stats_bytes = plan.stats;
-  }
-  if (plan.params > ws.params_bytes) {
-    ws.params.ensure(plan.params);
-    ws.params_bytes = plan.params;
   }
   ws.n = n;
   ws.in = in;
