@@ -215,6 +215,18 @@ int nnx_tconv3d_gemm(const float* d_x, int cin, const float* d_packed, const flo
                      float* d_y, int batch, const int* in_size, int cout, const int* ksize,
                      void* stream);
 
+/* The same transposed convolution with split-fp16 products (hi*hi + hi*lo + lo*hi, float32
+ * accumulation), weights multiplied by `scale` (nnx_split_weight_scale) before the split;
+ * the tile is staged in LDS and written as contiguous channel runs.  Packed size in bytes.
+ * Replaces the same reference call as nnx_tconv3d_gemm. */
+size_t nnx_tconv3d_split_packed_bytes(int cout, const int* ksize, int cin);
+int nnx_tconv3d_split_pack_weight(const float* d_weight /* (Cout,kD,kH,kW,Cin) */, int cout,
+                                  const int* ksize, int cin, float scale, void* d_packed,
+                                  void* stream);
+int nnx_tconv3d_split(const float* d_x, int cin, const void* d_packed, float scale,
+                      const float* d_bias, float* d_y, int batch, const int* in_size, int cout,
+                      const int* ksize, void* stream);
+
 /* 1x1x1 convolution with bias (segmentation head), NDHWC.
  * Replaces seg{n-1} (src/nnunet_mlx/model/network.py:804-808,875-876). */
 int nnx_conv1x1(const float* d_x, int cin, const float* d_weight /* (Cout,1,1,1,Cin) */,

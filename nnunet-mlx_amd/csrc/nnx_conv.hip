@@ -1083,19 +1083,26 @@ void launch_x3s(const IgemmArgs& a, bool vec, hipStream_t st, double flops, doub
 // in registers (zeros in the padding) and starts every output channel from 0 with
 // fma over the taps in (kd, kh, kw) order.  The optional bias is a separate addition.
 // ---------------------------------------------------------------------------------
+// Grid: (blocks of 256 voxels per batch item, batch).  With `stats`, the block also writes
+// the InstanceNorm partials of its voxels, stats[(b * gridDim.x + block) * cout + c] =
+// (mean, M2, n, 0) of conv + bias, two-pass over the block's outputs in LDS.
 __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ bias,
-                                                          float* __restrict__ y, int64_t nvox,
-                                                          int D, int H, int W, int cout) {
+                                                          float* __restrict__ y, int64_t S,
+                                                          int D, int H, int W, int cout,
+                                                          float4* __restrict__ stats) {
   __shared__ float ws[27 * 64];
   __shared__ float bs[64];
+  __shared__ float red[256];
   extern __shared__ float out_s[];  // 256 voxels x (cout + 1): padded rows, no bank conflicts
   for (int i = threadIdx.x; i < 27 * cout; i += blockDim.x) ws[i] = w[i];
   for (int i = threadIdx.x; i < cout; i += blockDim.x) bs[i] = bias ? bias[i] : 0.f;
   __syncthreads();
-  const int64_t v0 = blockIdx.x * (int64_t)blockDim.x;
+  const int64_t s0 = blockIdx.x * (int64_t)blockDim.x;
+  const int64_t v0 = (int64_t)blockIdx.y * S + s0;  // first voxel of the block in the batch
   const int64_t vox = v0 + threadIdx.x;
+  const int64_t nvox = (int64_t)blockIdx.y * S + S;  // end of this batch item
   const int stride = cout + 1;
   if (vox < nvox) {
     const int xx = (int)(vox % W);
@@ -1126,8 +1133,8 @@ __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restric
     }
   }
   __syncthreads();
-  // the block's voxels are contiguous in NDHWC: write them as one coalesced run
   const int64_t nv = nvox - v0 < (int64_t)blockDim.x ? nvox - v0 : (int64_t)blockDim.x;
+  // the block's voxels are contiguous in NDHWC: write them as one coalesced run
   const int total4 = (int)(nv * cout / 4);
   f4* dst = reinterpret_cast<f4*>(y + v0 * cout);
   for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
@@ -1135,6 +1142,38 @@ __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restric
     const int v = e / cout, c = e - v * cout;
     const float* src = out_s + v * stride + c;
     dst[e4] = f4{src[0], src[1], src[2], src[3]};
+  }
+  // statistics after the stores are issued, so they overlap the write-back
+  if (stats) {
+    // channel c = tid % cout, rows part, part + parts, ...: block mean, then centred M2
+    const int parts = blockDim.x / cout;
+    const int c = threadIdx.x % cout, part = threadIdx.x / cout;
+    const bool active = part < parts;
+    float t = 0.f;
+    if (active)
+      for (int r = part; r < nv; r += parts) t += out_s[r * stride + c];
+    red[threadIdx.x] = t;
+    __syncthreads();
+    float mean = 0.f;
+    if (active) {
+      for (int q = 0; q < parts; ++q) mean += red[q * cout + c];
+      mean = mean / (float)nv;
+    }
+    __syncthreads();
+    t = 0.f;
+    if (active)
+      for (int r = part; r < nv; r += parts) {
+        const float d = out_s[r * stride + c] - mean;
+        t = fmaf(d, d, t);
+      }
+    red[threadIdx.x] = t;
+    __syncthreads();
+    if (part == 0) {
+      float m2 = 0.f;
+      for (int q = 0; q < parts; ++q) m2 += red[q * cout + c];
+      stats[((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * cout + c] =
+          make_float4(mean, m2, (float)nv, 0.f);
+    }
   }
 }
 
@@ -1274,6 +1313,203 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void pw_gemm_kernel(PwArgs a) {
         }
       }
     }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Split-fp16 transposed convolution (stride == kernel): the pointwise GEMM above on
+// v_mfma_f32_16x16x32_f16 with hi*hi + hi*lo + lo*hi products.  A workgroup computes 64
+// input voxels x 128 columns (4 waves x 64 x 32).  Per 64-channel block the rows are read
+// as contiguous float4 lines, split into fp16 planes in LDS ([row][channel], row stride
+// 72 halves); B fragments come from the packed weights (L2 resident).  The epilogue
+// stages the tile in LDS and writes each output voxel's channels as contiguous runs; the
+// output address is a per-row base (input voxel -> output voxel of offset 0) plus a
+// per-column offset (kernel offset and channel), both precomputed in LDS.
+// ---------------------------------------------------------------------------------
+struct TcArgs {
+  const float* x;
+  int cin;
+  int64_t M;
+  const uint4* w16;  // [k-step of 32 channels][16-column block][hi|lo][64 lanes] x 8 fp16
+  int nblk, ksteps;
+  const float* bias;
+  float* y;
+  int cout, ncols;
+  int kd, kh, kw;
+  int id, ih, iw;
+  int ntn, nwg;
+  float out_scale;
+};
+
+constexpr int kTcRows = 64, kTcCols = 128, kTcKBlock = 64, kTcRowHalves = kTcKBlock + 8;
+constexpr int kTcTileStride = kTcCols + 1;  // floats per staged output row
+
+__global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
+  constexpr int MB = 4, NB = 2;
+  extern __shared__ __align__(16) float lds[];
+  _Float16* hi = reinterpret_cast<_Float16*>(lds);
+  _Float16* lo = hi + kTcRows * kTcRowHalves;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int row = lane & 15;
+  const int slot = lane >> 4;
+  const int logical = xcd_remap(blockIdx.x, a.nwg);
+  const int nt = logical % a.ntn;
+  const int64_t m0 = (int64_t)(logical / a.ntn) * kTcRows;
+  const int blk0 = nt * (kTcCols / 16) + wave * NB;  // first 16-column block of this wave
+
+  f4 acc[MB][NB];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+
+  for (int kb = 0; kb < a.cin; kb += kTcKBlock) {
+    __syncthreads();  // the previous block's fragments have been read
+    // rows m0.., channels kb..kb+63: 16 float4 lines per row
+    for (int i = tid; i < kTcRows * (kTcKBlock / 4); i += 256) {
+      const int r = i >> 4, c4 = (i & 15) * 4;
+      const int64_t m = m0 + r;
+      const int c = kb + c4;
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (m < a.M) {
+        const float* src = a.x + m * a.cin + c;
+        if (c + 3 < a.cin) {
+          v = *reinterpret_cast<const f4*>(src);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (c + q < a.cin) v[q] = src[q];
+        }
+      }
+      h4 hv, lv;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        _Float16 hh, ll;
+        split_half(v[q], hh, ll);
+        hv[q] = hh;
+        lv[q] = ll;
+      }
+      *reinterpret_cast<h4*>(hi + r * kTcRowHalves + c4) = hv;
+      *reinterpret_cast<h4*>(lo + r * kTcRowHalves + c4) = lv;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < kTcKBlock / 32; ++ks) {
+      const int kstep = kb / 32 + ks;
+      if (kstep >= a.ksteps) break;
+      h8 bh[NB], bl[NB], ah[MB], al[MB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const uint4* w = a.w16 + (((int64_t)kstep * a.nblk + blk0 + nb) * 2) * 64 + lane;
+        const uint4 wh = w[0], wl = w[64];
+        bh[nb] = *reinterpret_cast<const h8*>(&wh);
+        bl[nb] = *reinterpret_cast<const h8*>(&wl);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        const int off = (mb * 16 + row) * kTcRowHalves + ks * 32 + slot * 8;
+        ah[mb] = *reinterpret_cast<const h8*>(hi + off);
+        al[mb] = *reinterpret_cast<const h8*>(lo + off);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          acc[mb][nb] = mfma16x16x32h(ah[mb], bh[nb], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(ah[mb], bl[nb], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(al[mb], bh[nb], acc[mb][nb]);
+        }
+    }
+  }
+
+  // epilogue: tile T[r][c] (scaled, + bias) in LDS, then runs of contiguous channels
+  float* tile = lds;
+  int64_t* row_base = reinterpret_cast<int64_t*>(lds + kTcRows * kTcTileStride);
+  int* col_off = reinterpret_cast<int*>(row_base + kTcRows);
+  const int od = a.id * a.kd, oh = a.ih * a.kh, ow = a.iw * a.kw;
+  __syncthreads();  // the A planes are no longer read
+  if (tid < kTcRows) {
+    const int64_t m = m0 + tid;
+    int64_t base = -1;
+    if (m < a.M) {
+      const int xx = (int)(m % a.iw);
+      int64_t t = m / a.iw;
+      const int yy = (int)(t % a.ih);
+      t /= a.ih;
+      const int zz = (int)(t % a.id);
+      const int64_t bb = t / a.id;
+      base = ((bb * od + (int64_t)zz * a.kd) * oh + (int64_t)yy * a.kh) * ow + (int64_t)xx * a.kw;
+    }
+    row_base[tid] = base;
+  } else if (tid < kTcRows + kTcCols) {
+    const int cl = tid - kTcRows;
+    const int n = nt * kTcCols + cl;
+    int off = -1;
+    if (n < a.ncols) {
+      const int j = n / a.cout, o = n - j * a.cout;
+      const int ax = j % a.kw, ay = (j / a.kw) % a.kh, az = j / (a.kw * a.kh);
+      off = ((az * oh + ay) * ow + ax) * a.cout + o;
+    }
+    col_off[cl] = off;
+  }
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int cl = (wave * NB + nb) * 16 + row;
+    const int n = nt * kTcCols + cl;
+    const float bias_n = (a.bias && n < a.ncols) ? a.bias[n % a.cout] : 0.f;
+    const bool has_bias = a.bias != nullptr;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float v = acc[mb][nb][r] * a.out_scale;
+        tile[(mb * 16 + 4 * slot + r) * kTcTileStride + cl] = has_bias ? v + bias_n : v;
+      }
+  }
+  __syncthreads();
+  for (int e = tid; e < kTcRows * kTcCols; e += 256) {
+    const int r = e >> 7, cl = e & (kTcCols - 1);
+    const int64_t base = row_base[r];
+    const int off = col_off[cl];
+    if (base >= 0 && off >= 0) a.y[base * a.cout + off] = tile[r * kTcTileStride + cl];
+  }
+}
+
+// Packing: words ((kstep * nblk + nb) * 2 + part) * 64 + lane = part 0: hi, part 1: lo h8 of
+// scale * W[k][n], k = 32 * kstep + 8 * (lane / 16) + q, n = 16 * nb + lane % 16, where
+// column n = ((az * KH + ay) * KW + ax) * C_out + o reads the reference weight
+// (C_out, kD, kH, kW, C_in) at (o, az, ay, ax, k).
+__global__ void pack_tconv_weight_x3_kernel(const float* __restrict__ w, uint4* __restrict__ out,
+                                            int cout, int koff, int cin, int ksteps, int nblk,
+                                            float scale) {
+  const int64_t total = (int64_t)ksteps * nblk * 64;
+  const int ncols = koff * cout;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(i % 64);
+    const int64_t r = i / 64;
+    const int nb = (int)(r % nblk);
+    const int kstep = (int)(r / nblk);
+    const int n = nb * 16 + (lane & 15);
+    h8 hv, lv;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int k = kstep * 32 + 8 * (lane >> 4) + q;
+      float v = 0.f;
+      if (n < ncols && k < cin) {
+        const int o = n % cout, off = n / cout;
+        v = w[((int64_t)o * koff + off) * cin + k] * scale;
+      }
+      _Float16 hh, ll;
+      split_half(v, hh, ll);
+      hv[q] = hh;
+      lv[q] = ll;
+    }
+    const int64_t word = (i - lane) * 2 + lane;
+    out[word] = *reinterpret_cast<const uint4*>(&hv);
+    out[word + 64] = *reinterpret_cast<const uint4*>(&lv);
   }
 }
 
@@ -1674,17 +1910,23 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
     launch_x3<2, 2, 2, 2>(a, st, flops, bytes);
 }
 
+int conv_direct_stats_tiles(const int* size) {
+  return (int)ceil_div((int64_t)size[0] * size[1] * size[2], 256);
+}
+
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
-                        const int* size, int cout, hipStream_t st) {
+                        const int* size, int cout, hipStream_t st, float4* stats) {
   require(x && w && y, "convolution pointers must not be null");
   require(cout >= 4 && cout <= 64 && cout % 4 == 0,
           "one-channel direct convolution supports 4..64 outputs in steps of 4");
-  const int64_t nvox = (int64_t)batch * size[0] * size[1] * size[2];
-  require(nvox >= 1, "empty convolution input");
+  require(batch >= 1 && batch <= 65535, "invalid convolution batch");
+  const int64_t S = (int64_t)size[0] * size[1] * size[2];
+  require(S >= 1, "empty convolution input");
+  const int64_t nvox = (int64_t)batch * S;
   ProfScope prof("conv3d_direct_cin1", 2.0 * 27 * cout * (double)nvox, 4.0 * (double)nvox * (1 + cout), st);
-  hipLaunchKernelGGL(direct_cin1_kernel, dim3((unsigned)ceil_div(nvox, 256)), dim3(256),
-                     (size_t)256 * (cout + 1) * sizeof(float), st, x, w, bias, y, nvox, size[0],
-                     size[1], size[2], cout);
+  hipLaunchKernelGGL(direct_cin1_kernel, dim3((unsigned)ceil_div(S, 256), (unsigned)batch),
+                     dim3(256), (size_t)256 * (cout + 1) * sizeof(float), st, x, w, bias, y, S,
+                     size[0], size[1], size[2], cout, stats);
   launch_check("conv3d_direct_small_cin");
 }
 
@@ -1740,6 +1982,64 @@ void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bia
                  4.0 * ((double)a.M * (cin + ncols) + (double)cin * ncols), st);
   hipLaunchKernelGGL((pw_gemm_kernel<MB, NB, WM, WN>), dim3(a.nwg), dim3(64 * WM * WN), 0, st, a);
   launch_check("tconv3d_gemm");
+}
+
+int64_t tconv_x3_packed_bytes(int cout, const int* ksize, int cin) {
+  const int64_t koff = (int64_t)ksize[0] * ksize[1] * ksize[2];
+  return ceil_div(cin, 32) * tconv_packed_nblk(koff * cout) * 128 * 16;
+}
+
+void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float scale,
+                          void* d_packed, hipStream_t st) {
+  require(cout >= 1 && cin >= 1, "invalid transposed-convolution channel counts");
+  require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+  const int koff = ksize[0] * ksize[1] * ksize[2];
+  const int ksteps = (int)ceil_div(cin, 32);
+  const int nblk = tconv_packed_nblk((int64_t)koff * cout);
+  const int64_t total = (int64_t)ksteps * nblk * 64;
+  const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 65536);
+  hipLaunchKernelGGL(pack_tconv_weight_x3_kernel, dim3(blocks), dim3(256), 0, st, d_w,
+                     reinterpret_cast<uint4*>(d_packed), cout, koff, cin, ksteps, nblk, scale);
+  launch_check("tconv3d_split_pack_weight");
+}
+
+void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const float* bias,
+                float* y, int batch, const int* in_size, int cout, const int* ksize,
+                hipStream_t st) {
+  require(x && packed && y, "transposed-convolution pointers must not be null");
+  require(cin >= 1 && cout >= 1, "invalid transposed-convolution channel counts");
+  require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+  for (int i = 0; i < 3; ++i) require(ksize[i] >= 1 && in_size[i] >= 1, "invalid tconv geometry");
+  TcArgs a{};
+  a.x = x;
+  a.cin = cin;
+  a.M = (int64_t)batch * in_size[0] * in_size[1] * in_size[2];
+  a.w16 = reinterpret_cast<const uint4*>(packed);
+  a.ksteps = (int)ceil_div(cin, 32);
+  a.ncols = ksize[0] * ksize[1] * ksize[2] * cout;
+  a.nblk = tconv_packed_nblk(a.ncols);
+  a.bias = bias;
+  a.y = y;
+  a.cout = cout;
+  a.kd = ksize[0];
+  a.kh = ksize[1];
+  a.kw = ksize[2];
+  a.id = in_size[0];
+  a.ih = in_size[1];
+  a.iw = in_size[2];
+  a.out_scale = 1.0f / scale;
+  const int64_t ovox = (int64_t)in_size[0] * ksize[0] * in_size[1] * ksize[1] * in_size[2] * ksize[2];
+  require(ovox * cout < (1LL << 31), "transposed-convolution output item too large");
+  a.ntn = (int)ceil_div(a.ncols, kTcCols);
+  require(a.nblk >= a.ntn * (kTcCols / 16), "transposed-convolution packing too small");
+  const int64_t nwg = ceil_div(a.M, kTcRows) * a.ntn;
+  require(nwg < (1LL << 31), "transposed-convolution grid too large");
+  a.nwg = (int)nwg;
+  const size_t lds_bytes = (size_t)kTcRows * kTcTileStride * 4 + kTcRows * 8 + kTcCols * 4;
+  ProfScope prof("tconv3d_x3", 2.0 * (double)a.M * cin * a.ncols,
+                 4.0 * ((double)a.M * (cin + a.ncols) + (double)cin * a.ncols), st);
+  hipLaunchKernelGGL(tconv_x3_kernel, dim3(a.nwg), dim3(256), lds_bytes, st, a);
+  launch_check("tconv3d_split");
 }
 
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y, int64_t voxels,

@@ -146,14 +146,23 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
 int conv_x3_stats_tiles(const ConvGeom& g, int cout);
 // Whether the split kernel handles this kernel size / stride (tap count and halo size).
 bool conv_x3_supported(const int* ksize, const int* stride, int cout);
+// With `stats`: per-block InstanceNorm partials, conv_direct_stats_tiles(size) per item.
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
-                        const int* size, int cout, hipStream_t st);
+                        const int* size, int cout, hipStream_t st, float4* stats = nullptr);
+int conv_direct_stats_tiles(const int* size);
 
 int64_t tconv_packed_floats(int cout, const int* ksize, int cin);
 void tconv_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float* d_packed,
                        hipStream_t st);
 void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bias, float* y,
                   int batch, const int* in_size, int cout, const int* ksize, hipStream_t st);
+// Split-fp16 transposed convolution (stride == kernel), weights scaled like conv3d_x3.
+int64_t tconv_x3_packed_bytes(int cout, const int* ksize, int cin);
+void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float scale,
+                          void* d_packed, hipStream_t st);
+void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const float* bias,
+                float* y, int batch, const int* in_size, int cout, const int* ksize,
+                hipStream_t st);
 // `item_voxels` = voxels per batch item (to index the pending norm's parameters).
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y,
              int64_t voxels, int cout, hipStream_t st, const PendingNorm& nx = {},

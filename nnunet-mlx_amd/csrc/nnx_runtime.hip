@@ -154,6 +154,8 @@ struct Upsample {
   int cin = 0, cout = 0;
   int k[3] = {2, 2, 2};
   int pw = -1, pb = -1;
+  bool split = false;  // split-fp16 packing (fp32-split precision)
+  float scale = 1.f;
   DevBuf packed;
 };
 
@@ -175,8 +177,6 @@ struct Workspace {
   int n = 0;
   Shape3 in{};
   std::vector<std::unique_ptr<DevBuf>> bufs;
-  DevBuf norm_ws;
-  size_t norm_ws_bytes = 0;
   DevBuf stats;   // per-tile InstanceNorm partials written by the conv epilogue
   size_t stats_bytes = 0;
   float* get(size_t i) { return bufs[i]->as<float>(); }
@@ -363,7 +363,6 @@ Shape3 conv_out(const Shape3& in, const ConvNorm& c) {
 struct Planner {
   // During planning, records buffer sizes; during execution, hands out the same buffers.
   std::vector<size_t> sizes;
-  size_t norm_ws = 0;
   size_t stats = 0;
   size_t next = 0;
   bool planning = true;
@@ -407,15 +406,17 @@ struct Runner {
     result.data = out;
     if (defer) result.norm = PendingNorm{params, act, m->slope};
     if (c.direct) {
+      // the direct kernel writes per-block statistics of its output
       require(!x1.norm.params, "the one-channel convolution reads the network input");
-      const size_t nbytes = instnorm_workspace_bytes(n, vox, c.cout);
+      const int tiles = conv_direct_stats_tiles(in.d);
       if (plan->planning) {
-        plan->norm_ws = std::max(plan->norm_ws, nbytes);
+        plan->stats = std::max(plan->stats, (size_t)n * tiles * c.cout * sizeof(float4));
         return result;
       }
-      conv3d_direct_cin1(x1.data, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st);
-      instnorm_params(out, n, vox, c.cout, nullptr, pdev(m, c.pg), pdev(m, c.pbeta), m->eps,
-                      plan->ws->norm_ws.ptr, plan->ws->norm_ws_bytes, params, st);
+      float4* stats = plan->ws->stats.as<float4>();
+      conv3d_direct_cin1(x1.data, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st, stats);
+      instnorm_merge_partials(stats, tiles, n, vox, c.cout, pdev(m, c.pg), pdev(m, c.pbeta),
+                              m->eps, params, st);
       if (!defer)
         instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, act, m->slope, residual,
                               st);
@@ -467,9 +468,14 @@ struct Runner {
       for (int i = 0; i < 3; ++i) us.d[i] = hs.d[i] * u.k[i];
       const Shape3& ss = skip_shapes[src - 1];
       float* upbuf = plan->take((size_t)n * us.vox() * u.cout);
-      if (!plan->planning)
-        tconv3d_gemm(hidden.data, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d,
+      if (!plan->planning) {
+        if (u.split)
+          tconv3d_x3(hidden.data, u.cin, u.packed.ptr, u.scale, pdev(m, u.pb), upbuf, n, hs.d,
                      u.cout, u.k, st);
+        else
+          tconv3d_gemm(hidden.data, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d,
+                       u.cout, u.k, st);
+      }
       if (!(us == ss)) {
         // patch not divisible by the total stride: centre crop / zero pad the upsampled
         // tensor to the skip's size (_match_spatial, src/nnunet_mlx/model/network.py:898-916)
@@ -594,10 +600,6 @@ void ensure_workspace(nnx_model* m, int n, const Shape3& in) {
   for (size_t i = 0; i < plan.sizes.size(); ++i) {
     if (!ws.bufs[i]) ws.bufs[i] = std::make_unique<DevBuf>();
     ws.bufs[i]->ensure(plan.sizes[i]);
-  }
-  if (plan.norm_ws > ws.norm_ws_bytes) {
-    ws.norm_ws.ensure(plan.norm_ws);
-    ws.norm_ws_bytes = plan.norm_ws;
   }
   if (plan.stats > ws.stats_bytes) {
     ws.stats.ensure(plan.stats);
@@ -859,6 +861,13 @@ int nnx_model_finalize(nnx_model* model) {
     for (auto& stage : model->dec)
       for (auto& c : stage) pack_convnorm(model, c, st);
     for (auto& u : model->up) {
+      u.split = model->precision == NNX_PRECISION_FP32_SPLIT;
+      if (u.split) {
+        u.scale = split_weight_scale(model->params[u.pw].max_abs);
+        u.packed.ensure((size_t)tconv_x3_packed_bytes(u.cout, u.k, u.cin));
+        tconv_x3_pack_weight(pdev(model, u.pw), u.cout, u.k, u.cin, u.scale, u.packed.ptr, st);
+        continue;
+      }
       const int64_t n = tconv_packed_floats(u.cout, u.k, u.cin);
       u.packed.ensure((size_t)n * sizeof(float));
       tconv_pack_weight(pdev(model, u.pw), u.cout, u.k, u.cin, u.packed.as<float>(), st);
@@ -1029,6 +1038,30 @@ int nnx_tconv3d_gemm(const float* d_x, int cin, const float* d_packed, const flo
     require(in_size && ksize, "null argument");
     require(batch >= 1 && cout >= 1, "invalid transposed-convolution sizes");
     tconv3d_gemm(d_x, cin, d_packed, d_bias, d_y, batch, in_size, cout, ksize, as_stream(stream));
+  });
+}
+
+size_t nnx_tconv3d_split_packed_bytes(int cout, const int* ksize, int cin) {
+  if (!ksize || cout < 1 || cin < 1) return 0;
+  return (size_t)tconv_x3_packed_bytes(cout, ksize, cin);
+}
+
+int nnx_tconv3d_split_pack_weight(const float* d_weight, int cout, const int* ksize, int cin,
+                                  float scale, void* d_packed, void* stream) {
+  return guarded([&] {
+    require(d_weight && ksize && d_packed, "null argument");
+    tconv_x3_pack_weight(d_weight, cout, ksize, cin, scale, d_packed, as_stream(stream));
+  });
+}
+
+int nnx_tconv3d_split(const float* d_x, int cin, const void* d_packed, float scale,
+                      const float* d_bias, float* d_y, int batch, const int* in_size, int cout,
+                      const int* ksize, void* stream) {
+  return guarded([&] {
+    require(in_size && ksize, "null argument");
+    require(batch >= 1 && cout >= 1, "invalid transposed-convolution sizes");
+    tconv3d_x3(d_x, cin, d_packed, scale, d_bias, d_y, batch, in_size, cout, ksize,
+               as_stream(stream));
   });
 }
 

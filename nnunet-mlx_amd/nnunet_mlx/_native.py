@@ -147,6 +147,15 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "nnx_tconv3d_pack_weight": (
         ctypes.c_int, [c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, c_void_p, c_void_p]
     ),
+    "nnx_tconv3d_split_packed_bytes": (ctypes.c_size_t, [ctypes.c_int, c_int_p, ctypes.c_int]),
+    "nnx_tconv3d_split_pack_weight": (
+        ctypes.c_int, [c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p]
+    ),
+    "nnx_tconv3d_split": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p, ctypes.c_int, c_int_p,
+         ctypes.c_int, c_int_p, c_void_p],
+    ),
     "nnx_tconv3d_gemm": (
         ctypes.c_int,
         [c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_int, c_int_p, ctypes.c_int,

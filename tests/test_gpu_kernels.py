@@ -235,6 +235,43 @@ def test_tconv3d_gemm_matches_float64(lib, case):
     assert rel_l2(got, ref) <= 1e-6, report("tconv", got, ref)
 
 
+@pytest.mark.parametrize("case", [
+    (2, (4, 4, 4), 64, 32, (2, 2, 2)),
+    (1, (7, 5, 4), 320, 320, (1, 2, 2)),
+    (1, (8, 8, 8), 128, 64, (2, 2, 2)),
+    (1, (3, 5, 2), 6, 4, (2, 1, 2)),
+    (3, (5, 6, 7), 96, 24, (2, 2, 2)),
+], ids=str)
+def test_tconv3d_split_matches_float64(lib, case):
+    """Split-fp16 products hold the float32 bar (rel-L2 <= 1e-5) of the transposed conv."""
+    batch, size, cin, cout, k = case
+    print(f"split tconv case {case}", flush=True)
+    rng = np.random.default_rng(4)
+    x = rng.standard_normal((batch, *size, cin)).astype(np.float32)
+    w = (rng.standard_normal((cout, *k, cin)) / np.sqrt(cin)).astype(np.float32)
+    w.reshape(-1)[::5] *= 1e-3
+    b = rng.standard_normal(cout).astype(np.float32)
+    k_c = _native.ints(k)
+    scale = lib.nnx_split_weight_scale(float(np.abs(w).max()))
+    packed = torch.empty(lib.nnx_tconv3d_split_packed_bytes(cout, k_c, cin), dtype=torch.uint8, device="cuda")
+    dx, dw, db = dev(x), dev(w), dev(b)
+    _native.check(lib.nnx_tconv3d_split_pack_weight(dw.data_ptr(), cout, k_c, cin, scale,
+                                                    packed.data_ptr(), stream()))
+    out_size = [s * kk for s, kk in zip(size, k)]
+    y = torch.full((batch, *out_size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_tconv3d_split(dx.data_ptr(), cin, packed.data_ptr(), scale, db.data_ptr(),
+                                        y.data_ptr(), batch, _native.ints(size), cout, k_c, stream()))
+    got = host(y)
+    xt = torch.from_numpy(x.astype(np.float64)).permute(0, 4, 1, 2, 3)
+    wt = torch.from_numpy(w.astype(np.float64)).permute(4, 0, 1, 2, 3)
+    ref = F.conv_transpose3d(xt, wt, torch.from_numpy(b.astype(np.float64)), stride=k)
+    ref = ref.permute(0, 2, 3, 4, 1).numpy()
+    msg = report("split tconv", got, ref)
+    assert np.isfinite(got).all(), msg
+    assert rel_l2(got, ref) <= 1e-5, msg
+    assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
+
+
 def test_conv1x1_seg_head(lib):
     rng = np.random.default_rng(5)
     x = rng.standard_normal((2, 6, 7, 8, 32)).astype(np.float32)
