@@ -1086,19 +1086,21 @@ void launch_x3s(const IgemmArgs& a, bool vec, hipStream_t st, double flops, doub
 // Grid: (blocks of 256 voxels per batch item, batch).  With `stats`, the block also writes
 // the InstanceNorm partials of its voxels, stats[(b * gridDim.x + block) * cout + c] =
 // (mean, M2, n, 0) of conv + bias, two-pass over the block's outputs in LDS.
+// Weights and bias are read through the constant address space: the loads are uniform,
+// so they become scalar loads and every fma takes its weight from an SGPR (no LDS reads).
+template <int COUT>
 __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ bias,
                                                           float* __restrict__ y, int64_t S,
-                                                          int D, int H, int W, int cout,
+                                                          int D, int H, int W,
                                                           float4* __restrict__ stats) {
-  __shared__ float ws[27 * 64];
-  __shared__ float bs[64];
+  typedef const __attribute__((address_space(4))) float* cfloat_p;
+  constexpr int cout = COUT;
   __shared__ float red[256];
   extern __shared__ float out_s[];  // 256 voxels x (cout + 1): padded rows, no bank conflicts
-  for (int i = threadIdx.x; i < 27 * cout; i += blockDim.x) ws[i] = w[i];
-  for (int i = threadIdx.x; i < cout; i += blockDim.x) bs[i] = bias ? bias[i] : 0.f;
-  __syncthreads();
+  const cfloat_p wc = (cfloat_p)w;
+  const cfloat_p bc = (cfloat_p)bias;
   const int64_t s0 = blockIdx.x * (int64_t)blockDim.x;
   const int64_t v0 = (int64_t)blockIdx.y * S + s0;  // first voxel of the block in the batch
   const int64_t vox = v0 + threadIdx.x;
@@ -1125,11 +1127,12 @@ __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restric
       }
     }
     const bool has_bias = bias != nullptr;
+#pragma unroll
     for (int c = 0; c < cout; ++c) {
       float sum = 0.f;
 #pragma unroll
-      for (int t = 0; t < 27; ++t) sum = fmaf(taps[t], ws[c * 27 + t], sum);
-      out_s[threadIdx.x * stride + c] = has_bias ? sum + bs[c] : sum;
+      for (int t = 0; t < 27; ++t) sum = fmaf(taps[t], wc[c * 27 + t], sum);
+      out_s[threadIdx.x * stride + c] = has_bias ? sum + bc[c] : sum;
     }
   }
   __syncthreads();
@@ -1567,13 +1570,19 @@ __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __rest
   const int64_t v0 = blockIdx.x * (int64_t)blockDim.x;
   const int nv = (int)(nvox - v0 < 256 ? nvox - v0 : 256);
   const float4* src = reinterpret_cast<const float4*>(x + v0 * cin);
-  const int total4 = nv * cin / 4;
+  const int cin4 = cin / 4;
+  const int total4 = nv * cin4;
+  // batch item of the block's first voxel; rows from `split` on belong to the next item
+  const int64_t item0 = nrm ? v0 / item_vox : 0;
+  const int64_t split = nrm ? (item0 + 1) * item_vox - v0 : 0;
+  // (row, channel group) of element e4 = row * cin4 + group, advanced without divisions
+  const int step_r = (int)blockDim.x / cin4, step_g = (int)blockDim.x % cin4;
+  int r = (int)threadIdx.x / cin4, g = (int)threadIdx.x % cin4;
   for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
     float4 v = src[e4];
-    const int e = e4 * 4;
-    const int r = e / cin, c = e - r * cin;
+    const int c = g * 4;
     if (nrm) {
-      const float4* pr = nrm + ((v0 + r) / item_vox) * cin + c;
+      const float4* pr = nrm + (item0 + (r >= split ? 1 : 0)) * cin + c;
       v.x = norm_apply1(v.x, pr[0], act, slope);
       v.y = norm_apply1(v.y, pr[1], act, slope);
       v.z = norm_apply1(v.z, pr[2], act, slope);
@@ -1584,6 +1593,12 @@ __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __rest
     d[1] = v.y;
     d[2] = v.z;
     d[3] = v.w;
+    r += step_r;
+    g += step_g;
+    if (g >= cin4) {
+      g -= cin4;
+      ++r;
+    }
   }
   __syncthreads();
   if ((int)threadIdx.x < nv) {
@@ -1924,9 +1939,20 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
   require(S >= 1, "empty convolution input");
   const int64_t nvox = (int64_t)batch * S;
   ProfScope prof("conv3d_direct_cin1", 2.0 * 27 * cout * (double)nvox, 4.0 * (double)nvox * (1 + cout), st);
-  hipLaunchKernelGGL(direct_cin1_kernel, dim3((unsigned)ceil_div(S, 256), (unsigned)batch),
-                     dim3(256), (size_t)256 * (cout + 1) * sizeof(float), st, x, w, bias, y, S,
-                     size[0], size[1], size[2], cout, stats);
+  const dim3 grid((unsigned)ceil_div(S, 256), (unsigned)batch);
+  const size_t lds = (size_t)256 * (cout + 1) * sizeof(float);
+  switch (cout / 4) {
+#define NNX_DIRECT_CASE(Q)                                                                     \
+  case Q:                                                                                      \
+    hipLaunchKernelGGL(direct_cin1_kernel<4 * Q>, grid, dim3(256), lds, st, x, w, bias, y, S,  \
+                       size[0], size[1], size[2], stats);                                      \
+    break;
+    NNX_DIRECT_CASE(1) NNX_DIRECT_CASE(2) NNX_DIRECT_CASE(3) NNX_DIRECT_CASE(4)
+    NNX_DIRECT_CASE(5) NNX_DIRECT_CASE(6) NNX_DIRECT_CASE(7) NNX_DIRECT_CASE(8)
+    NNX_DIRECT_CASE(9) NNX_DIRECT_CASE(10) NNX_DIRECT_CASE(11) NNX_DIRECT_CASE(12)
+    NNX_DIRECT_CASE(13) NNX_DIRECT_CASE(14) NNX_DIRECT_CASE(15) NNX_DIRECT_CASE(16)
+#undef NNX_DIRECT_CASE
+  }
   launch_check("conv3d_direct_small_cin");
 }
 
