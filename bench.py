@@ -85,11 +85,13 @@ def kernel_class_of(short: str) -> str | None:
     split-fp16 kernels igemm_x3s_kernel / igemm_x3_kernel -> conv3d_x3s_* / conv3d_x3_*)."""
     import re
 
-    m = re.match(r"igemm(_x3s|_x3)?_kernel<(\d+), (\d+), (\d+), (\d+)", short)
+    m = re.match(r"igemm(_x3s|_x3)?_kernel<(\d+), (\d+), (\d+), (\d+)([^>]*)>", short)
     if not m:
         return None
     prefix = {None: "conv3d_igemm", "_x3s": "conv3d_x3s", "_x3": "conv3d_x3"}[m.group(1)]
-    mb, nb, wm, wn = (int(g) for g in m.groups()[1:])
+    if m.group(1) and m.group(6).split(",")[-1].strip() == "1":  # bf16 arithmetic
+        prefix += "_bf16"
+    mb, nb, wm, wn = (int(g) for g in m.groups()[1:5])
     return f"{prefix}_m{16 * mb * wm}n{16 * nb * wn}"
 
 
@@ -243,7 +245,7 @@ def main() -> int:
                              "(torch.neg) whose HBM counters calibrate FETCH_SIZE/WRITE_SIZE")
     parser.add_argument("--summarize-profiles", metavar="DIR",
                         help="write the profiles/ summaries from rocprofv3 CSV output in DIR and exit")
-    parser.add_argument("--precision", choices=("fp32", "fp32-split"), default="fp32-split",
+    parser.add_argument("--precision", choices=("fp32", "fp32-split", "bf16"), default="fp32-split",
                         help="convolution arithmetic: fp16-split products (3 per term) on fp16 "
                              "MFMA (default), or float32 products on fp32 MFMA; both float32 I/O "
                              "and accumulation, both within the float32 logits tolerance")
@@ -312,7 +314,11 @@ def main() -> int:
         entry = {"launches": c["launches"], "ms": round(c["ms"], 3)}
         if c["flops"]:
             entry["tflops"] = round(c["flops"] / (c["ms"] * 1e-3) / 1e12, 2)
-            if name.startswith("conv3d_x3"):
+            if name.startswith("conv3d_x3") and "_bf16" in name:
+                # issued bf16 MFMA work: 1 product per term, 4-tap groups (27 -> 28 taps)
+                entry["frac_bf16_mfma_issued"] = round(
+                    entry["tflops"] * 28 / 27 / PEAK_FP16_MFMA_TFLOPS, 4)
+            elif name.startswith("conv3d_x3"):
                 # issued fp16 MFMA work: 3 products per term, 4-tap groups (27 -> 28 taps)
                 entry["frac_fp16_mfma_issued"] = round(
                     entry["tflops"] * SPLIT_PRODUCTS * 28 / 27 / PEAK_FP16_MFMA_TFLOPS, 4)
@@ -333,7 +339,8 @@ def main() -> int:
                     "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                     "traffic": measured_traffic(dominant)}
         if dominant.startswith("conv3d_x3"):
-            roofline["issued_frac"] = kernels[dominant]["frac_fp16_mfma_issued"]
+            roofline["issued_frac"] = kernels[dominant].get(
+                "frac_bf16_mfma_issued", kernels[dominant].get("frac_fp16_mfma_issued"))
     else:
         achieved = d["bytes"] / (d["ms"] * 1e-3) / 1e9
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
@@ -343,12 +350,13 @@ def main() -> int:
     conv_flops = sum(c["flops"] for c in conv)
     conv_ms = sum(c["ms"] for c in conv)
     # 3x3x3 convolution rate against the float32-class MFMA peak of the arithmetic used
-    conv_peak = PEAK_FP32_MFMA_TFLOPS if args.precision == "fp32" else PEAK_FP16_MFMA_TFLOPS / SPLIT_PRODUCTS
+    conv_peak = {"fp32": PEAK_FP32_MFMA_TFLOPS, "fp32-split": PEAK_FP16_MFMA_TFLOPS / SPLIT_PRODUCTS,
+                 "bf16": PEAK_FP16_MFMA_TFLOPS}[args.precision]
     conv_frac = conv_flops / (conv_ms * 1e-3) / 1e12 / conv_peak if conv_ms else None
 
     alt = None
     if not args.no_alt:
-        other = "fp32" if args.precision == "fp32-split" else "fp32-split"
+        other = "fp32" if args.precision in ("fp32-split", "bf16") else "fp32-split"
         print(f"[bench] one step with precision {other}", file=sys.stderr, flush=True)
         alt_net = build_network(spec, precision=other)
         alt_net.load_weights(weights)
@@ -391,7 +399,8 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "f32" if args.precision == "fp32" else "f32 (fp16-split products, f32 accumulate)",
+        "dtype": {"fp32": "f32", "fp32-split": "f32 (fp16-split products, f32 accumulate)",
+                  "bf16": "bf16 products, f32 accumulate"}[args.precision],
         "precision": args.precision,
         "data": "synthetic",
         "config": {

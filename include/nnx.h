@@ -51,6 +51,12 @@ const char* nnx_version(void);
  * (x = hi + lo), see nnx_conv3d_split.  Meets the float32 logits tolerance; activations
  * must stay below 65504 in magnitude (they are normalised, so they do). */
 #define NNX_PRECISION_FP32_SPLIT 1
+/* bf16 operands with float32 accumulation (the pancreas config's bf16): the 3-D
+ * convolutions after the first one and the transposed convolutions round their weights
+ * and input activations to bf16 (nearest even) and multiply on bf16 MFMA, accumulating in
+ * float32; InstanceNorm statistics, the first convolution, 1x1x1 convolutions and the
+ * activations between layers stay float32.  Logits meet relative-L2 1e-2. */
+#define NNX_PRECISION_BF16 2
 
 typedef struct nnx_spec {
   int arch;              /* NNX_ARCH_PLAIN or NNX_ARCH_RESIDUAL */
@@ -70,7 +76,7 @@ typedef struct nnx_spec {
   int stem_channels; /* residual only; 0 means features[0] */
   const int* bottleneck_channels; /* residual only: n_stages entries for BottleneckD, or NULL
                                      for BasicBlockD */
-  int precision;     /* NNX_PRECISION_FP32 or NNX_PRECISION_FP32_SPLIT */
+  int precision;     /* NNX_PRECISION_FP32, NNX_PRECISION_FP32_SPLIT or NNX_PRECISION_BF16 */
 } nnx_spec;
 
 typedef struct nnx_model nnx_model;
@@ -226,6 +232,24 @@ int nnx_tconv3d_split_pack_weight(const float* d_weight /* (Cout,kD,kH,kW,Cin) *
 int nnx_tconv3d_split(const float* d_x, int cin, const void* d_packed, float scale,
                       const float* d_bias, float* d_y, int batch, const int* in_size, int cout,
                       const int* ksize, void* stream);
+
+/* The bf16 arithmetic (NNX_PRECISION_BF16) of the same two kernels: weights times `scale`
+ * and input activations rounded to bf16 (nearest even), one bf16 MFMA product, float32
+ * accumulation, outputs times 1/scale.  Packed sizes as nnx_conv3d_split_packed_bytes and
+ * nnx_tconv3d_split_packed_bytes.  Replace the same reference calls as the split entries
+ * (the reference has no bf16 path; these serve the bf16 config). */
+int nnx_conv3d_bf16_pack_weight(const float* d_weight /* (Cout,kD,kH,kW,c1+c2) */, int cout,
+                                const int* ksize, int c1, int c2, float scale, void* d_packed,
+                                void* stream);
+int nnx_conv3d_bf16(const float* d_x1, int c1, const float* d_x2, int c2, const void* d_packed,
+                    float scale, const float* d_bias, float* d_y, int batch, const int* in_size,
+                    int cout, const int* ksize, const int* stride, void* stream);
+int nnx_tconv3d_bf16_pack_weight(const float* d_weight /* (Cout,kD,kH,kW,Cin) */, int cout,
+                                 const int* ksize, int cin, float scale, void* d_packed,
+                                 void* stream);
+int nnx_tconv3d_bf16(const float* d_x, int cin, const void* d_packed, float scale,
+                     const float* d_bias, float* d_y, int batch, const int* in_size, int cout,
+                     const int* ksize, void* stream);
 
 /* 1x1x1 convolution with bias (segmentation head), NDHWC.
  * Replaces seg{n-1} (src/nnunet_mlx/model/network.py:804-808,875-876). */

@@ -528,12 +528,60 @@ __device__ __forceinline__ void split_half(float v, _Float16& hi, _Float16& lo) 
   lo = (_Float16)(v - (float)hi);
 }
 
+// Operand arithmetic of the split kernels.  kSplit3: fp16 hi/lo halves, three products
+// hi*hi + hi*lo + lo*hi (float32 class).  kBf16: one bf16 operand per value (round to
+// nearest even), one product; its bits travel in the same fp16-typed planes and words.
+constexpr int kSplit3 = kArithSplit3;
+constexpr int kBf16 = kArithBf16;
+typedef __bf16 bf8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f4 mfma16x16x32bf(h8 a, h8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf8, a),
+                                                 __builtin_bit_cast(bf8, b), c, 0, 0, 0);
+}
+
+template <int AR>
+__device__ __forceinline__ void to_operand(float v, _Float16& hi, _Float16& lo) {
+  if constexpr (AR == kBf16) {
+    hi = __builtin_bit_cast(_Float16, (__bf16)v);
+    lo = (_Float16)0.f;
+  } else {
+    split_half(v, hi, lo);
+  }
+}
+
+// acc[mb][nb] += A[mb] * B[nb] in the arithmetic AR; the passes touch MB*NB independent
+// accumulators in turn (hi*hi, then hi*lo, then lo*hi for kSplit3).
+template <int AR, int MB, int NB>
+__device__ __forceinline__ void mma_products(f4 (&acc)[MB][NB], const h8 (&A)[MB][2],
+                                             const h8 (&B)[NB][2]) {
+  if constexpr (AR == kBf16) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma16x16x32bf(A[mb][0], B[nb][0], acc[mb][nb]);
+  } else {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma16x16x32h(A[mb][0], B[nb][0], acc[mb][nb]);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma16x16x32h(A[mb][0], B[nb][1], acc[mb][nb]);
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = mfma16x16x32h(A[mb][1], B[nb][0], acc[mb][nb]);
+  }
+}
+
 // Halo lines (8-byte halves of a voxel's 8-channel chunk, 4 floats) per thread: the
 // split kernel stages the next chunk's halo in registers while the current chunk computes.
 constexpr int kX3MaxLines = 6;  // halo lines per thread in flight (register staging)
 constexpr int kX3Threads = 256;
 
-template <int MB, int NB, int WM, int WN, int NTG>
+template <int MB, int NB, int WM, int WN, int NTG, int AR>
 __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
   extern __shared__ __align__(16) float lds[];
   constexpr int NT = 64 * WM * WN;
@@ -650,12 +698,12 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           _Float16 hh, ll;
-          split_half(stage[j][q], hh, ll);
+          to_operand<AR>(stage[j][q], hh, ll);
           hv[q] = hh;
           lv[q] = ll;
         }
         *reinterpret_cast<h4*>(hi_plane + line * 4) = hv;
-        *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
+        if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
       }
     }
   };
@@ -670,16 +718,18 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const uint4 wh = wc[g * group_stride + nb * 128];
-        const uint4 wl = wc[g * group_stride + nb * 128 + 64];
         B[p][nb][0] = *reinterpret_cast<const h8*>(&wh);
-        B[p][nb][1] = *reinterpret_cast<const h8*>(&wl);
+        if constexpr (AR == kSplit3) {
+          const uint4 wl = wc[g * group_stride + nb * 128 + 64];
+          B[p][nb][1] = *reinterpret_cast<const h8*>(&wl);
+        }
       }
     };
     auto load_a = [&](int p, int g) {
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         A[p][mb][0] = hi8[hbase[mb] + toff[g]];
-        A[p][mb][1] = lo8[hbase[mb] + toff[g]];
+        if constexpr (AR == kSplit3) A[p][mb][1] = lo8[hbase[mb] + toff[g]];
       }
     };
     load_b(0, 0);  // in flight across the barriers below
@@ -695,22 +745,7 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
         load_a(cur ^ 1, g + 1);
         load_b(cur ^ 1, g + 1);
       }
-      // hi*hi, hi*lo, lo*hi: the three passes touch MB*NB independent accumulators in turn
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][0], acc[mb][nb]);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][1], acc[mb][nb]);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = mfma16x16x32h(A[cur][mb][1], B[cur][nb][0], acc[mb][nb]);
+      mma_products<AR>(acc, A[cur], B[cur]);
     }
   }
   igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
@@ -722,7 +757,7 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
 // then computes from LDS only.  The main loop issues no global loads, so its LDS waits
 // never queue behind memory traffic; the chunk-boundary load latency is covered by the
 // other resident workgroups.  LDS: 32 bytes per halo voxel + NTG * WN*NB * 2 KB.
-template <int MB, int NB, int WM, int WN, int NTG, bool VEC>
+template <int MB, int NB, int WM, int WN, int NTG, bool VEC, int AR>
 __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) {
   extern __shared__ __align__(16) float lds[];
   constexpr int NT = 64 * WM * WN;
@@ -836,12 +871,12 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
 #pragma unroll
           for (int q = 0; q < 4; ++q) {
             _Float16 hh, ll;
-            split_half(val[j][q], hh, ll);
+            to_operand<AR>(val[j][q], hh, ll);
             hv[q] = hh;
             lv[q] = ll;
           }
           *reinterpret_cast<h4*>(hi_plane + line * 4) = hv;
-          *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
+          if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
         }
       }
     }
@@ -866,13 +901,13 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         A[p][mb][0] = hi8[hbase[mb] + toff[g]];
-        A[p][mb][1] = lo8[hbase[mb] + toff[g]];
+        if constexpr (AR == kSplit3) A[p][mb][1] = lo8[hbase[mb] + toff[g]];
       }
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const int wb = (g * WBLK + wn * NB + nb) * 128 + lane;
         B[p][nb][0] = wl8[wb];
-        B[p][nb][1] = wl8[wb + 64];
+        if constexpr (AR == kSplit3) B[p][nb][1] = wl8[wb + 64];
       }
     };
     load(0, 0);
@@ -880,21 +915,7 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
     for (int g = 0; g < NTG; ++g) {
       const int cur = g & 1;
       if (g + 1 < NTG) load(cur ^ 1, g + 1);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][0], acc[mb][nb]);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = mfma16x16x32h(A[cur][mb][0], B[cur][nb][1], acc[mb][nb]);
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-          acc[mb][nb] = mfma16x16x32h(A[cur][mb][1], B[cur][nb][0], acc[mb][nb]);
+      mma_products<AR>(acc, A[cur], B[cur]);
     }
   }
   igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
@@ -906,7 +927,8 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
 // q)], q = 0..7, n = nb * 16 + lane % 16.
 __global__ void pack_conv_weight_x3_kernel(const float* __restrict__ w, uint4* __restrict__ out,
                                            int cout, int taps, int c1, int c2, int chunks1,
-                                           int chunks, int groups, int nblk, float scale) {
+                                           int chunks, int groups, int nblk, float scale,
+                                           int arith) {
   const int64_t total = (int64_t)chunks * groups * nblk * 64;
   const int ctot = c1 + c2;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -935,7 +957,10 @@ __global__ void pack_conv_weight_x3_kernel(const float* __restrict__ w, uint4* _
       float v = 0.f;
       if (ok && n < cout && tap < taps) v = w[((int64_t)n * taps + tap) * ctot + cin] * scale;
       _Float16 hh, ll;
-      split_half(v, hh, ll);
+      if (arith == kBf16)
+        to_operand<kBf16>(v, hh, ll);
+      else
+        to_operand<kSplit3>(v, hh, ll);
       hv[q] = hh;
       lv[q] = ll;
     }
@@ -1026,35 +1051,62 @@ void launch_igemm(const IgemmArgs& a, int nwg, bool async, hipStream_t st, doubl
   launch_check("conv3d_igemm");
 }
 
-template <int MB, int NB, int WM, int WN>
-void launch_x3(const IgemmArgs& a, hipStream_t st, double flops, double bytes) {
-  static const std::string name = "conv3d_x3_m" + std::to_string(16 * MB * WM) + "n" +
-                                  std::to_string(16 * NB * WN);
+template <int MB, int NB, int WM, int WN, int NTG>
+void launch_x3_ntg(const IgemmArgs& a, int arith, size_t lds_bytes, hipStream_t st) {
   constexpr int nt = 64 * WM * WN;
+  if (arith == kBf16)
+    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, NTG, kBf16>), dim3(a.nwg), dim3(nt),
+                       lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, NTG, kSplit3>), dim3(a.nwg), dim3(nt),
+                       lds_bytes, st, a);
+}
+
+// Profiled kernel-class name of a split-kernel launch: "<base>_m<M>n<N>", with "_bf16"
+// before the shape for the bf16 arithmetic.
+std::string x3_launch_name(const char* base, int arith, int m, int n) {
+  return std::string(base) + (arith == kBf16 ? "_bf16" : "") + "_m" + std::to_string(m) + "n" +
+         std::to_string(n);
+}
+
+template <int MB, int NB, int WM, int WN>
+void launch_x3(const IgemmArgs& a, int arith, hipStream_t st, double flops, double bytes) {
+  static const std::string names[2] = {
+      x3_launch_name("conv3d_x3", kSplit3, 16 * MB * WM, 16 * NB * WN),
+      x3_launch_name("conv3d_x3", kBf16, 16 * MB * WM, 16 * NB * WN)};
   // two fp16 planes of [halo voxel][8] = 32 bytes per halo voxel; the epilogue reuses
   // the first WM * 16 * NB * WN floats
   const size_t halo_bytes = (size_t)a.hz * a.hy * a.hx * 32;
   const size_t red_bytes = (size_t)WM * 16 * NB * WN * sizeof(float);
   const size_t lds_bytes = halo_bytes > red_bytes ? halo_bytes : red_bytes;
-  ProfScope prof(name.c_str(), flops, bytes, st);
+  ProfScope prof(names[arith == kBf16].c_str(), flops, bytes, st);
   if (a.ntg == 7)
-    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, 7>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
+    launch_x3_ntg<MB, NB, WM, WN, 7>(a, arith, lds_bytes, st);
   else if (a.ntg == 3)
-    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, 3>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
+    launch_x3_ntg<MB, NB, WM, WN, 3>(a, arith, lds_bytes, st);
   else
-    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, 1>), dim3(a.nwg), dim3(nt), lds_bytes, st, a);
+    launch_x3_ntg<MB, NB, WM, WN, 1>(a, arith, lds_bytes, st);
   launch_check("conv3d_x3");
 }
 
 template <int MB, int NB, int WM, int WN, int NTG>
-void launch_x3s_ntg(const IgemmArgs& a, bool vec, size_t lds_bytes, hipStream_t st) {
+void launch_x3s_ntg(const IgemmArgs& a, bool vec, int arith, size_t lds_bytes, hipStream_t st) {
   constexpr int nt = 64 * WM * WN;
-  if (vec)
-    hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, true>), dim3(a.nwg), dim3(nt),
-                       lds_bytes, st, a);
-  else
-    hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, false>), dim3(a.nwg), dim3(nt),
-                       lds_bytes, st, a);
+  if (arith == kBf16) {
+    if (vec)
+      hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, true, kBf16>), dim3(a.nwg),
+                         dim3(nt), lds_bytes, st, a);
+    else
+      hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, false, kBf16>), dim3(a.nwg),
+                         dim3(nt), lds_bytes, st, a);
+  } else {
+    if (vec)
+      hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, true, kSplit3>), dim3(a.nwg),
+                         dim3(nt), lds_bytes, st, a);
+    else
+      hipLaunchKernelGGL((igemm_x3s_kernel<MB, NB, WM, WN, NTG, false, kSplit3>), dim3(a.nwg),
+                         dim3(nt), lds_bytes, st, a);
+  }
 }
 
 size_t x3s_lds_bytes(int64_t halo_voxels, int ntg, int wblk) {
@@ -1062,19 +1114,21 @@ size_t x3s_lds_bytes(int64_t halo_voxels, int ntg, int wblk) {
 }
 
 template <int MB, int NB, int WM, int WN>
-void launch_x3s(const IgemmArgs& a, bool vec, hipStream_t st, double flops, double bytes) {
-  static const std::string name = "conv3d_x3s_m" + std::to_string(16 * MB * WM) + "n" +
-                                  std::to_string(16 * NB * WN);
+void launch_x3s(const IgemmArgs& a, bool vec, int arith, hipStream_t st, double flops,
+                double bytes) {
+  static const std::string names[2] = {
+      x3_launch_name("conv3d_x3s", kSplit3, 16 * MB * WM, 16 * NB * WN),
+      x3_launch_name("conv3d_x3s", kBf16, 16 * MB * WM, 16 * NB * WN)};
   const size_t red_bytes = (size_t)WM * 16 * NB * WN * sizeof(float);
   size_t lds_bytes = x3s_lds_bytes((int64_t)a.hz * a.hy * a.hx, a.ntg, WN * NB);
   if (lds_bytes < red_bytes) lds_bytes = red_bytes;
-  ProfScope prof(name.c_str(), flops, bytes, st);
+  ProfScope prof(names[arith == kBf16].c_str(), flops, bytes, st);
   if (a.ntg == 7)
-    launch_x3s_ntg<MB, NB, WM, WN, 7>(a, vec, lds_bytes, st);
+    launch_x3s_ntg<MB, NB, WM, WN, 7>(a, vec, arith, lds_bytes, st);
   else if (a.ntg == 3)
-    launch_x3s_ntg<MB, NB, WM, WN, 3>(a, vec, lds_bytes, st);
+    launch_x3s_ntg<MB, NB, WM, WN, 3>(a, vec, arith, lds_bytes, st);
   else
-    launch_x3s_ntg<MB, NB, WM, WN, 1>(a, vec, lds_bytes, st);
+    launch_x3s_ntg<MB, NB, WM, WN, 1>(a, vec, arith, lds_bytes, st);
   launch_check("conv3d_x3s");
 }
 
@@ -1347,6 +1401,7 @@ struct TcArgs {
 constexpr int kTcRows = 64, kTcCols = 128, kTcKBlock = 64, kTcRowHalves = kTcKBlock + 8;
 constexpr int kTcTileStride = kTcCols + 1;  // floats per staged output row
 
+template <int AR>
 __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
   constexpr int MB = 4, NB = 2;
   extern __shared__ __align__(16) float lds[];
@@ -1390,40 +1445,36 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
         _Float16 hh, ll;
-        split_half(v[q], hh, ll);
+        to_operand<AR>(v[q], hh, ll);
         hv[q] = hh;
         lv[q] = ll;
       }
       *reinterpret_cast<h4*>(hi + r * kTcRowHalves + c4) = hv;
-      *reinterpret_cast<h4*>(lo + r * kTcRowHalves + c4) = lv;
+      if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo + r * kTcRowHalves + c4) = lv;
     }
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < kTcKBlock / 32; ++ks) {
       const int kstep = kb / 32 + ks;
       if (kstep >= a.ksteps) break;
-      h8 bh[NB], bl[NB], ah[MB], al[MB];
+      h8 B[NB][2], A[MB][2];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
         const uint4* w = a.w16 + (((int64_t)kstep * a.nblk + blk0 + nb) * 2) * 64 + lane;
-        const uint4 wh = w[0], wl = w[64];
-        bh[nb] = *reinterpret_cast<const h8*>(&wh);
-        bl[nb] = *reinterpret_cast<const h8*>(&wl);
+        const uint4 wh = w[0];
+        B[nb][0] = *reinterpret_cast<const h8*>(&wh);
+        if constexpr (AR == kSplit3) {
+          const uint4 wl = w[64];
+          B[nb][1] = *reinterpret_cast<const h8*>(&wl);
+        }
       }
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb) {
         const int off = (mb * 16 + row) * kTcRowHalves + ks * 32 + slot * 8;
-        ah[mb] = *reinterpret_cast<const h8*>(hi + off);
-        al[mb] = *reinterpret_cast<const h8*>(lo + off);
+        A[mb][0] = *reinterpret_cast<const h8*>(hi + off);
+        if constexpr (AR == kSplit3) A[mb][1] = *reinterpret_cast<const h8*>(lo + off);
       }
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          acc[mb][nb] = mfma16x16x32h(ah[mb], bh[nb], acc[mb][nb]);
-          acc[mb][nb] = mfma16x16x32h(ah[mb], bl[nb], acc[mb][nb]);
-          acc[mb][nb] = mfma16x16x32h(al[mb], bh[nb], acc[mb][nb]);
-        }
+      mma_products<AR>(acc, A, B);
     }
   }
 
@@ -1486,7 +1537,7 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
 // (C_out, kD, kH, kW, C_in) at (o, az, ay, ax, k).
 __global__ void pack_tconv_weight_x3_kernel(const float* __restrict__ w, uint4* __restrict__ out,
                                             int cout, int koff, int cin, int ksteps, int nblk,
-                                            float scale) {
+                                            float scale, int arith) {
   const int64_t total = (int64_t)ksteps * nblk * 64;
   const int ncols = koff * cout;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
@@ -1506,7 +1557,10 @@ __global__ void pack_tconv_weight_x3_kernel(const float* __restrict__ w, uint4* 
         v = w[((int64_t)o * koff + off) * cin + k] * scale;
       }
       _Float16 hh, ll;
-      split_half(v, hh, ll);
+      if (arith == kBf16)
+        to_operand<kBf16>(v, hh, ll);
+      else
+        to_operand<kSplit3>(v, hh, ll);
       hv[q] = hh;
       lv[q] = ll;
     }
@@ -1823,8 +1877,9 @@ int64_t conv_x3_packed_bytes(int cout, const int* ksize, int c1, int c2) {
 }
 
 void conv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int c2,
-                         float scale, void* d_packed, hipStream_t st) {
+                         float scale, void* d_packed, hipStream_t st, int arith) {
   require(cout >= 1 && c1 >= 1 && c2 >= 0, "invalid convolution channel counts");
+  require(arith == kSplit3 || arith == kBf16, "unknown convolution arithmetic");
   require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
   const int taps = ksize[0] * ksize[1] * ksize[2];
   const int chunks1 = (int)ceil_div(c1, kChunk);
@@ -1835,7 +1890,7 @@ void conv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int c1, i
   const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 65536);
   hipLaunchKernelGGL(pack_conv_weight_x3_kernel, dim3(blocks), dim3(256), 0, st, d_w,
                      reinterpret_cast<uint4*>(d_packed), cout, taps, c1, c2, chunks1, chunks,
-                     groups, nblk, scale);
+                     groups, nblk, scale, arith);
   launch_check("conv3d_x3_pack_weight");
 }
 
@@ -1900,10 +1955,12 @@ int conv_x3_stats_tiles(const ConvGeom& g, int cout) {
 
 void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* packed,
                float scale, const float* bias, float* y, const ConvGeom& g, int cout,
-               hipStream_t st, float4* stats, const PendingNorm& n1, const PendingNorm& n2) {
+               hipStream_t st, float4* stats, const PendingNorm& n1, const PendingNorm& n2,
+               int arith) {
   require(x1 && y && packed, "convolution pointers must not be null");
   require(c1 >= 1 && (c2 == 0 || x2), "invalid convolution inputs");
   require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+  require(arith == kSplit3 || arith == kBf16, "unknown convolution arithmetic");
   const X3Plan plan = plan_x3(g, cout);
   const Variant v = plan.v;
   IgemmArgs a = igemm_args(x1, c1, x2, c2, bias, y, g, cout, v, plan.box, stats, n1, n2);
@@ -1916,13 +1973,13 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
   igemm_work(g, c1, c2, cout, &flops, &bytes);
   if (plan.staged) {
     const bool vec = c1 % kChunk == 0 && c2 % kChunk == 0;
-    launch_x3s<4, 2, 4, 1>(a, vec, st, flops, bytes);
+    launch_x3s<4, 2, 4, 1>(a, vec, arith, st, flops, bytes);
     return;
   }
   if (v.NB == 4)
-    launch_x3<2, 4, 2, 2>(a, st, flops, bytes);
+    launch_x3<2, 4, 2, 2>(a, arith, st, flops, bytes);
   else
-    launch_x3<2, 2, 2, 2>(a, st, flops, bytes);
+    launch_x3<2, 2, 2, 2>(a, arith, st, flops, bytes);
 }
 
 int conv_direct_stats_tiles(const int* size) {
@@ -2016,8 +2073,9 @@ int64_t tconv_x3_packed_bytes(int cout, const int* ksize, int cin) {
 }
 
 void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float scale,
-                          void* d_packed, hipStream_t st) {
+                          void* d_packed, hipStream_t st, int arith) {
   require(cout >= 1 && cin >= 1, "invalid transposed-convolution channel counts");
+  require(arith == kSplit3 || arith == kBf16, "unknown transposed-convolution arithmetic");
   require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
   const int koff = ksize[0] * ksize[1] * ksize[2];
   const int ksteps = (int)ceil_div(cin, 32);
@@ -2025,15 +2083,17 @@ void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin,
   const int64_t total = (int64_t)ksteps * nblk * 64;
   const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 65536);
   hipLaunchKernelGGL(pack_tconv_weight_x3_kernel, dim3(blocks), dim3(256), 0, st, d_w,
-                     reinterpret_cast<uint4*>(d_packed), cout, koff, cin, ksteps, nblk, scale);
+                     reinterpret_cast<uint4*>(d_packed), cout, koff, cin, ksteps, nblk, scale,
+                     arith);
   launch_check("tconv3d_split_pack_weight");
 }
 
 void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const float* bias,
                 float* y, int batch, const int* in_size, int cout, const int* ksize,
-                hipStream_t st) {
+                hipStream_t st, int arith) {
   require(x && packed && y, "transposed-convolution pointers must not be null");
   require(cin >= 1 && cout >= 1, "invalid transposed-convolution channel counts");
+  require(arith == kSplit3 || arith == kBf16, "unknown transposed-convolution arithmetic");
   require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
   for (int i = 0; i < 3; ++i) require(ksize[i] >= 1 && in_size[i] >= 1, "invalid tconv geometry");
   TcArgs a{};
@@ -2062,9 +2122,13 @@ void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const 
   require(nwg < (1LL << 31), "transposed-convolution grid too large");
   a.nwg = (int)nwg;
   const size_t lds_bytes = (size_t)kTcRows * kTcTileStride * 4 + kTcRows * 8 + kTcCols * 4;
-  ProfScope prof("tconv3d_x3", 2.0 * (double)a.M * cin * a.ncols,
+  ProfScope prof(arith == kBf16 ? "tconv3d_x3_bf16" : "tconv3d_x3",
+                 2.0 * (double)a.M * cin * a.ncols,
                  4.0 * ((double)a.M * (cin + a.ncols) + (double)cin * a.ncols), st);
-  hipLaunchKernelGGL(tconv_x3_kernel, dim3(a.nwg), dim3(256), lds_bytes, st, a);
+  if (arith == kBf16)
+    hipLaunchKernelGGL(tconv_x3_kernel<kBf16>, dim3(a.nwg), dim3(256), lds_bytes, st, a);
+  else
+    hipLaunchKernelGGL(tconv_x3_kernel<kSplit3>, dim3(a.nwg), dim3(256), lds_bytes, st, a);
   launch_check("tconv3d_split");
 }
 

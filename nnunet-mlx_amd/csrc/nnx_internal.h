@@ -137,12 +137,17 @@ int conv_stats_tiles(const ConvGeom& g, int cout, int c1, int c2);
 // epilogue.  Activations must stay below the fp16 maximum (65504) in magnitude.
 float split_weight_scale(float max_abs);
 int64_t conv_x3_packed_bytes(int cout, const int* ksize, int c1, int c2);
+// Operand arithmetic of the split kernels: kArithSplit3 = fp16 hi/lo halves, three
+// products (float32 class); kArithBf16 = bf16 operands (round to nearest even), one
+// product.  Both accumulate in float32; the packed layout and size are the same.
+constexpr int kArithSplit3 = 0;
+constexpr int kArithBf16 = 1;
 void conv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int c1, int c2,
-                         float scale, void* d_packed, hipStream_t st);
+                         float scale, void* d_packed, hipStream_t st, int arith = kArithSplit3);
 void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* packed,
                float scale, const float* bias, float* y, const ConvGeom& g, int cout,
                hipStream_t st, float4* stats = nullptr, const PendingNorm& n1 = {},
-               const PendingNorm& n2 = {});
+               const PendingNorm& n2 = {}, int arith = kArithSplit3);
 int conv_x3_stats_tiles(const ConvGeom& g, int cout);
 // Whether the split kernel handles this kernel size / stride (tap count and halo size).
 bool conv_x3_supported(const int* ksize, const int* stride, int cout);
@@ -159,10 +164,10 @@ void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bia
 // Split-fp16 transposed convolution (stride == kernel), weights scaled like conv3d_x3.
 int64_t tconv_x3_packed_bytes(int cout, const int* ksize, int cin);
 void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float scale,
-                          void* d_packed, hipStream_t st);
+                          void* d_packed, hipStream_t st, int arith = kArithSplit3);
 void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const float* bias,
                 float* y, int batch, const int* in_size, int cout, const int* ksize,
-                hipStream_t st);
+                hipStream_t st, int arith = kArithSplit3);
 // `item_voxels` = voxels per batch item (to index the pending norm's parameters).
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y,
              int64_t voxels, int cout, hipStream_t st, const PendingNorm& nx = {},

@@ -332,18 +332,26 @@ const float* pdev(const nnx_model* m, int id) {
   return id < 0 ? nullptr : m->params[id].dev.as<float>();
 }
 
+// The split kernels' operand arithmetic for the model's precision.
+int split_arith(const nnx_model* m) {
+  return m->precision == NNX_PRECISION_BF16 ? kArithBf16 : kArithSplit3;
+}
+bool uses_split_kernels(const nnx_model* m) {
+  return m->precision == NNX_PRECISION_FP32_SPLIT || m->precision == NNX_PRECISION_BF16;
+}
+
 void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
   if (c.direct) return;  // the direct kernel reads the reference layout
-  // Split-fp16 products for the hidden convolutions with >= 8 taps (a tap group holds 4
-  // taps; 1x1x1 convolutions would waste 3/4 of it).  The first convolution reads the
-  // raw network input, whose range is not normalised, so it keeps float32 products.
+  // Split-fp16 (or bf16) products for the hidden convolutions with >= 8 taps (a tap group
+  // holds 4 taps; 1x1x1 convolutions would waste 3/4 of it).  The first convolution reads
+  // the raw network input, whose range is not normalised, so it keeps float32 products.
   const int taps = c.k[0] * c.k[1] * c.k[2];
-  c.split = m->precision == NNX_PRECISION_FP32_SPLIT && !c.first && taps >= 8 &&
-            conv_x3_supported(c.k, c.s, c.cout);
+  c.split = uses_split_kernels(m) && !c.first && taps >= 8 && conv_x3_supported(c.k, c.s, c.cout);
   if (c.split) {
     c.scale = split_weight_scale(m->params[c.pw].max_abs);
     c.packed.ensure((size_t)conv_x3_packed_bytes(c.cout, c.k, c.cin1, c.cin2));
-    conv_x3_pack_weight(pdev(m, c.pw), c.cout, c.k, c.cin1, c.cin2, c.scale, c.packed.ptr, st);
+    conv_x3_pack_weight(pdev(m, c.pw), c.cout, c.k, c.cin1, c.cin2, c.scale, c.packed.ptr, st,
+                        split_arith(m));
     return;
   }
   const int64_t n = conv_packed_floats(c.cout, c.k, c.cin1, c.cin2);
@@ -434,7 +442,7 @@ struct Runner {
     float4* stats = plan->ws->stats.as<float4>();
     if (c.split)
       conv3d_x3(x1.data, c.cin1, x2.data, c.cin2, c.packed.ptr, c.scale, pdev(m, c.pb), out, g,
-                c.cout, st, stats, x1.norm, x2.norm);
+                c.cout, st, stats, x1.norm, x2.norm, split_arith(m));
     else
       conv3d_igemm(x1.data, c.cin1, x2.data, c.cin2, c.packed.as<float>(), pdev(m, c.pb), out, g,
                    c.cout, st, stats, x1.norm, x2.norm);
@@ -471,7 +479,7 @@ struct Runner {
       if (!plan->planning) {
         if (u.split)
           tconv3d_x3(hidden.data, u.cin, u.packed.ptr, u.scale, pdev(m, u.pb), upbuf, n, hs.d,
-                     u.cout, u.k, st);
+                     u.cout, u.k, st, split_arith(m));
         else
           tconv3d_gemm(hidden.data, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d,
                        u.cout, u.k, st);
@@ -742,7 +750,8 @@ int nnx_model_create(const nnx_spec* spec, nnx_model** out) {
     require(spec->spatial_dims == 3, "only three-dimensional networks run on the HIP path");
     require(spec->arch == NNX_ARCH_PLAIN || spec->arch == NNX_ARCH_RESIDUAL,
             "unsupported network architecture");
-    require(spec->precision == NNX_PRECISION_FP32 || spec->precision == NNX_PRECISION_FP32_SPLIT,
+    require(spec->precision == NNX_PRECISION_FP32 || spec->precision == NNX_PRECISION_FP32_SPLIT ||
+                spec->precision == NNX_PRECISION_BF16,
             "unsupported precision");
     require(spec->input_channels >= 1 && spec->num_classes >= 1,
             "network needs input channels and at least one output");
@@ -861,11 +870,12 @@ int nnx_model_finalize(nnx_model* model) {
     for (auto& stage : model->dec)
       for (auto& c : stage) pack_convnorm(model, c, st);
     for (auto& u : model->up) {
-      u.split = model->precision == NNX_PRECISION_FP32_SPLIT;
+      u.split = uses_split_kernels(model);
       if (u.split) {
         u.scale = split_weight_scale(model->params[u.pw].max_abs);
         u.packed.ensure((size_t)tconv_x3_packed_bytes(u.cout, u.k, u.cin));
-        tconv_x3_pack_weight(pdev(model, u.pw), u.cout, u.k, u.cin, u.scale, u.packed.ptr, st);
+        tconv_x3_pack_weight(pdev(model, u.pw), u.cout, u.k, u.cin, u.scale, u.packed.ptr, st,
+                             split_arith(model));
         continue;
       }
       const int64_t n = tconv_packed_floats(u.cout, u.k, u.cin);
@@ -1062,6 +1072,47 @@ int nnx_tconv3d_split(const float* d_x, int cin, const void* d_packed, float sca
     require(batch >= 1 && cout >= 1, "invalid transposed-convolution sizes");
     tconv3d_x3(d_x, cin, d_packed, scale, d_bias, d_y, batch, in_size, cout, ksize,
                as_stream(stream));
+  });
+}
+
+int nnx_conv3d_bf16_pack_weight(const float* d_weight, int cout, const int* ksize, int c1, int c2,
+                                float scale, void* d_packed, void* stream) {
+  return guarded([&] {
+    require(d_weight && ksize && d_packed, "null argument");
+    conv_x3_pack_weight(d_weight, cout, ksize, c1, c2, scale, d_packed, as_stream(stream),
+                        kArithBf16);
+  });
+}
+
+int nnx_conv3d_bf16(const float* d_x1, int c1, const float* d_x2, int c2, const void* d_packed,
+                    float scale, const float* d_bias, float* d_y, int batch, const int* in_size,
+                    int cout, const int* ksize, const int* stride, void* stream) {
+  return guarded([&] {
+    require(in_size && ksize && stride, "null argument");
+    require(cout >= 1, "convolution needs at least one output channel");
+    const ConvGeom g = make_conv_geom(batch, in_size, ksize, stride);
+    conv3d_x3(d_x1, c1, d_x2, c2, d_packed, scale, d_bias, d_y, g, cout, as_stream(stream),
+              nullptr, {}, {}, kArithBf16);
+  });
+}
+
+int nnx_tconv3d_bf16_pack_weight(const float* d_weight, int cout, const int* ksize, int cin,
+                                 float scale, void* d_packed, void* stream) {
+  return guarded([&] {
+    require(d_weight && ksize && d_packed, "null argument");
+    tconv_x3_pack_weight(d_weight, cout, ksize, cin, scale, d_packed, as_stream(stream),
+                         kArithBf16);
+  });
+}
+
+int nnx_tconv3d_bf16(const float* d_x, int cin, const void* d_packed, float scale,
+                     const float* d_bias, float* d_y, int batch, const int* in_size, int cout,
+                     const int* ksize, void* stream) {
+  return guarded([&] {
+    require(in_size && ksize, "null argument");
+    require(batch >= 1 && cout >= 1, "invalid transposed-convolution sizes");
+    tconv3d_x3(d_x, cin, d_packed, scale, d_bias, d_y, batch, in_size, cout, ksize,
+               as_stream(stream), kArithBf16);
   });
 }
 

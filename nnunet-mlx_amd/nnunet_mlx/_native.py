@@ -32,6 +32,7 @@ NNX_ARCH_PLAIN = 0
 NNX_ARCH_RESIDUAL = 1
 NNX_PRECISION_FP32 = 0
 NNX_PRECISION_FP32_SPLIT = 1
+NNX_PRECISION_BF16 = 2
 NNX_ACCUM_F32 = 0
 NNX_ACCUM_NNUNET_F16 = 1
 
@@ -152,6 +153,23 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int, [c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p]
     ),
     "nnx_tconv3d_split": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p, ctypes.c_int, c_int_p,
+         ctypes.c_int, c_int_p, c_void_p],
+    ),
+    "nnx_conv3d_bf16_pack_weight": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p],
+    ),
+    "nnx_conv3d_bf16": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p,
+         ctypes.c_int, c_int_p, ctypes.c_int, c_int_p, c_int_p, c_void_p],
+    ),
+    "nnx_tconv3d_bf16_pack_weight": (
+        ctypes.c_int, [c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p]
+    ),
+    "nnx_tconv3d_bf16": (
         ctypes.c_int,
         [c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p, ctypes.c_int, c_int_p,
          ctypes.c_int, c_int_p, c_void_p],

@@ -23,12 +23,18 @@ from nnunet_mlx.errors import ContractError
 from nnunet_mlx.model.topology import NetworkSpec, PlainConvUNetSpec, ResidualEncoderUNetSpec
 
 
-# Convolution arithmetic of the HIP network.  Both meet the float32 logits tolerance
-# (max-abs <= 1e-3, relative L2 <= 1e-5 against the float32 oracle): "fp32" multiplies in
-# float32 on fp32 MFMA; "fp32-split" (the default, ~2.5x faster convolutions) computes the
-# 3-D convolutions after the first as hi*hi + hi*lo + lo*hi of fp16-split operands with
-# float32 accumulation.
-PRECISIONS = {"fp32": _native.NNX_PRECISION_FP32, "fp32-split": _native.NNX_PRECISION_FP32_SPLIT}
+# Convolution arithmetic of the HIP network.  "fp32" and "fp32-split" meet the float32
+# logits tolerance (max-abs <= 1e-3, relative L2 <= 1e-5 against the float32 oracle):
+# "fp32" multiplies in float32 on fp32 MFMA; "fp32-split" (the default, ~2.5x faster
+# convolutions) computes the 3-D convolutions after the first as hi*hi + hi*lo + lo*hi of
+# fp16-split operands with float32 accumulation.  "bf16" rounds those convolutions' (and
+# the transposed convolutions') weights and inputs to bf16 and multiplies once, with
+# float32 accumulation and float32 norm statistics; it meets relative L2 <= 1e-2.
+PRECISIONS = {
+    "fp32": _native.NNX_PRECISION_FP32,
+    "fp32-split": _native.NNX_PRECISION_FP32_SPLIT,
+    "bf16": _native.NNX_PRECISION_BF16,
+}
 DEFAULT_PRECISION = "fp32-split"
 
 

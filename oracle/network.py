@@ -49,6 +49,11 @@ def tconv_weight_to_torch(weight: np.ndarray) -> torch.Tensor:
     return _t(weight).permute(4, 0, 1, 2, 3).contiguous()
 
 
+def round_bf16(x: torch.Tensor) -> torch.Tensor:
+    """float32 -> nearest bf16 (ties to even) -> float32 (torch's bfloat16 cast)."""
+    return x.to(torch.bfloat16).to(torch.float32)
+
+
 def instance_norm(
     values: torch.Tensor,
     gamma: torch.Tensor | None,
@@ -91,15 +96,31 @@ def instance_norm(
 class OracleNetwork:
     """Forward of a PlainConvUNet or ResidualEncoderUNet on the CPU in float32.
 
+    ``bf16=True`` emulates the bf16 arithmetic (``_bf16_operands``): operands rounded to
+    bf16 at the convolutions that run on bf16 MFMA, everything else float32.
+
     ``spec`` is any object with the PlainConvUNetSpec / ResidualEncoderUNetSpec fields
     (src/nnunet_mlx/model/topology.py:132-430); ``residual`` selects the architecture.
     ``weights`` maps reference parameter names to arrays in the reference layout.
     """
 
-    def __init__(self, spec: Any, weights: Weights, *, residual: bool = False) -> None:
+    def __init__(self, spec: Any, weights: Weights, *, residual: bool = False,
+                 bf16: bool = False) -> None:
         self.spec = spec
         self.residual = residual
+        self.bf16 = bf16
         self.w = {name: _t(np.asarray(value)) for name, value in weights.items()}
+
+    def _bf16_operands(self, prefix: str, x: torch.Tensor, weight: torch.Tensor):
+        """The bf16 arithmetic's rounding points: the inputs and weights of every 3-D
+        convolution with >= 8 taps except the one reading the network input, and of the
+        transposed convolutions, are rounded to bf16 (nearest even); products and sums
+        stay float32."""
+        taps = int(np.prod(weight.shape[2:]))
+        first = prefix in ("enc0.block0", "stem")
+        if not self.bf16 or (prefix != "up" and (taps < 8 or first)):
+            return x, weight
+        return round_bf16(x), round_bf16(weight)
 
     # -- building blocks -----------------------------------------------------------
     def conv_norm(
@@ -116,6 +137,7 @@ class OracleNetwork:
         weight = conv_weight_to_torch(self.w[f"{prefix}.conv.weight"].numpy())
         kernel = weight.shape[2:]
         padding = tuple(k // 2 for k in kernel)
+        x, weight = self._bf16_operands(prefix, x, weight)
         y = F.conv3d(x, weight, None, stride=tuple(stride), padding=padding)
         has_bias = spec.conv_bias if bias is None else bias
         conv_bias = self.w[f"{prefix}.conv.bias"] if has_bias else None
@@ -130,6 +152,7 @@ class OracleNetwork:
     def upsample(self, index: int, x: torch.Tensor, stride: tuple[int, ...]) -> torch.Tensor:
         weight = tconv_weight_to_torch(self.w[f"up{index}.weight"].numpy())
         bias = self.w.get(f"up{index}.bias") if self.spec.conv_bias else None
+        x, weight = self._bf16_operands("up", x, weight)
         return F.conv_transpose3d(x, weight, bias, stride=tuple(stride))
 
     @staticmethod

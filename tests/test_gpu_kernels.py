@@ -272,6 +272,86 @@ def test_tconv3d_split_matches_float64(lib, case):
     assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
 
 
+def _bf16(a: np.ndarray) -> np.ndarray:
+    """Round to bf16 (nearest even), returned as float64."""
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.float32)).to(torch.bfloat16).double().numpy()
+
+
+@pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}-k{c[5]}-s{c[6]}")
+def test_conv3d_bf16_matches_rounded_float64(lib, case):
+    """bf16 arithmetic: the float64 convolution of the bf16-rounded input and weights (each
+    product is exact in float32) to float32 accumulation error, and the bf16 bar
+    (relative L2 <= 1e-2) against the unrounded float64 convolution."""
+    batch, size, c1, c2, cout, kernel, stride = case
+    print(f"bf16 conv case {case}", flush=True)
+    rng = np.random.default_rng((hash(case) + 11) % 2**32)
+    x1 = rng.standard_normal((batch, *size, c1)).astype(np.float32)
+    x2 = rng.standard_normal((batch, *size, c2)).astype(np.float32) if c2 else None
+    w = (rng.standard_normal((cout, *kernel, c1 + c2)) / np.sqrt((c1 + c2) * np.prod(kernel))).astype(np.float32)
+    bias = rng.standard_normal(cout).astype(np.float32)
+    out_size = [(s + 2 * (k // 2) - k) // st + 1 for s, k, st in zip(size, kernel, stride)]
+    k_c, s_c = _native.ints(kernel), _native.ints(stride)
+    scale = lib.nnx_split_weight_scale(float(np.abs(w).max()))
+    packed = torch.empty(lib.nnx_conv3d_split_packed_bytes(cout, k_c, c1, c2), dtype=torch.uint8, device="cuda")
+    dw = dev(w)
+    _native.check(lib.nnx_conv3d_bf16_pack_weight(dw.data_ptr(), cout, k_c, c1, c2, scale,
+                                                  packed.data_ptr(), stream()))
+    dx1 = dev(x1)
+    dx2 = dev(x2) if c2 else None
+    db = dev(bias)
+    y = torch.full((batch, *out_size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_conv3d_bf16(
+        dx1.data_ptr(), c1, dx2.data_ptr() if c2 else None, c2, packed.data_ptr(), scale,
+        db.data_ptr(), y.data_ptr(), batch, _native.ints(size), cout, k_c, s_c, stream()))
+    got = host(y)
+    full = np.concatenate([x1, x2], axis=-1) if c2 else x1
+    # scaling by a power of two commutes with the rounding: bf16(w * scale) / scale == bf16(w)
+    ref_rounded = _conv_ref64(_bf16(full), _bf16(w), stride) + bias.astype(np.float64)
+    ref = _conv_ref64(full, w, stride) + bias.astype(np.float64)
+    msg = report("bf16 conv", got, ref_rounded)
+    assert np.isfinite(got).all(), msg
+    assert rel_l2(got, ref_rounded) <= 1e-5, msg
+    assert rel_l2(got, ref) <= 1e-2, report("bf16 conv vs unrounded", got, ref)
+
+
+@pytest.mark.parametrize("case", [
+    (2, (4, 4, 4), 64, 32, (2, 2, 2)),
+    (1, (7, 5, 4), 320, 320, (1, 2, 2)),
+    (1, (3, 5, 2), 6, 4, (2, 1, 2)),
+], ids=str)
+def test_tconv3d_bf16_matches_rounded_float64(lib, case):
+    batch, size, cin, cout, k = case
+    print(f"bf16 tconv case {case}", flush=True)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((batch, *size, cin)).astype(np.float32)
+    w = (rng.standard_normal((cout, *k, cin)) / np.sqrt(cin)).astype(np.float32)
+    b = rng.standard_normal(cout).astype(np.float32)
+    k_c = _native.ints(k)
+    scale = lib.nnx_split_weight_scale(float(np.abs(w).max()))
+    packed = torch.empty(lib.nnx_tconv3d_split_packed_bytes(cout, k_c, cin), dtype=torch.uint8, device="cuda")
+    dx, dw, db = dev(x), dev(w), dev(b)
+    _native.check(lib.nnx_tconv3d_bf16_pack_weight(dw.data_ptr(), cout, k_c, cin, scale,
+                                                   packed.data_ptr(), stream()))
+    out_size = [s * kk for s, kk in zip(size, k)]
+    y = torch.full((batch, *out_size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_tconv3d_bf16(dx.data_ptr(), cin, packed.data_ptr(), scale, db.data_ptr(),
+                                       y.data_ptr(), batch, _native.ints(size), cout, k_c, stream()))
+    got = host(y)
+
+    def tconv64(xa, wa):
+        xt = torch.from_numpy(xa).permute(0, 4, 1, 2, 3)
+        wt = torch.from_numpy(wa).permute(4, 0, 1, 2, 3)
+        r = F.conv_transpose3d(xt, wt, torch.from_numpy(b.astype(np.float64)), stride=k)
+        return r.permute(0, 2, 3, 4, 1).numpy()
+
+    ref_rounded = tconv64(_bf16(x), _bf16(w))
+    ref = tconv64(x.astype(np.float64), w.astype(np.float64))
+    msg = report("bf16 tconv", got, ref_rounded)
+    assert np.isfinite(got).all(), msg
+    assert rel_l2(got, ref_rounded) <= 1e-5, msg
+    assert rel_l2(got, ref) <= 1e-2, report("bf16 tconv vs unrounded", got, ref)
+
+
 def test_conv1x1_seg_head(lib):
     rng = np.random.default_rng(5)
     x = rng.standard_normal((2, 6, 7, 8, 32)).astype(np.float32)

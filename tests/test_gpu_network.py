@@ -63,15 +63,20 @@ CASES = {
 
 @pytest.mark.parametrize("name", list(CASES))
 def test_forward_matches_oracle(device, name):
-    """Both convolution arithmetics ("fp32" products and "fp32-split" fp16-split products)
-    against one oracle run."""
+    """All three convolution arithmetics against the float32 oracle: "fp32" products and
+    "fp32-split" fp16-split products at the float32 bar.  "bf16" against the oracle's bf16
+    emulation (operands rounded at the same points): identical up to float32 accumulation
+    on the two-stage network; on deeper networks a bf16 rounding flipped by a last-bit
+    accumulation difference cascades, so there the bar is that the bf16 network lies no
+    further from the float32 logits than bf16 rounding itself puts the emulation (x1.25)."""
     spec, patch, batch, affine = CASES[name]
     weights = random_weights(spec, seed=1, random_affine=affine)
     rng = np.random.default_rng(0)
     x = rng.standard_normal((batch, *patch, spec.input_channels)).astype(np.float32)
     residual = isinstance(spec, ResidualEncoderUNetSpec)
     ref = OracleNetwork(spec, weights, residual=residual)(x)
-    for precision in ("fp32", "fp32-split"):
+    ref16 = OracleNetwork(spec, weights, residual=residual, bf16=True)(x)
+    for precision in ("fp32", "fp32-split", "bf16"):
         print(f"network case {name} patch={patch} batch={batch} precision={precision}", flush=True)
         net = build_network(spec, precision=precision)
         net.load_weights(weights)
@@ -79,10 +84,19 @@ def test_forward_matches_oracle(device, name):
         msg = report(f"{name} {precision}", got, ref)
         print(msg, flush=True)
         assert got.shape == ref.shape
-        assert np.abs(got - ref).max() <= 1e-3, msg
-        assert rel_l2(got, ref) <= 1e-5, msg
-        agree = (got.argmax(-1) == ref.argmax(-1)).mean()
-        assert agree >= 0.9999, f"{msg} label agreement {agree}"
+        assert np.isfinite(got).all(), msg
+        if precision == "bf16":
+            inherent = rel_l2(ref16, ref)
+            print(f"{name} bf16: emulation vs float32 {inherent:.3e}, "
+                  f"network vs emulation {rel_l2(got, ref16):.3e}", flush=True)
+            if name == "tiny-plain":
+                assert rel_l2(got, ref16) <= 1e-5, report(f"{name} bf16 vs emulation", got, ref16)
+            assert rel_l2(got, ref) <= 1.25 * inherent, msg
+        else:
+            assert np.abs(got - ref).max() <= 1e-3, msg
+            assert rel_l2(got, ref) <= 1e-5, msg
+            agree = (got.argmax(-1) == ref.argmax(-1)).mean()
+            assert agree >= 0.9999, f"{msg} label agreement {agree}"
         net.close()
 
 

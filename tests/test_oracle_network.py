@@ -176,3 +176,58 @@ def test_plain_network_composition_against_float64():
             h = cn(f"dec{d}.block{j}", h, (1, 1, 1))
     ref = np.einsum("nzyxc,oc->nzyxo", h, w["seg1.weight"][:, 0, 0, 0, :].astype(np.float64)) + w["seg1.bias"]
     np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+def _rne_bf16_bits(x: np.ndarray) -> np.ndarray:
+    """Round-to-nearest-even to bf16 by integer arithmetic on the float32 bits (finite
+    inputs): add 0x7FFF plus the lowest kept bit, truncate the low 16 bits."""
+    u = x.astype(np.float32).view(np.uint32).astype(np.uint64)
+    u = (u + 0x7FFF + ((u >> 16) & 1)) >> 16 << 16
+    return u.astype(np.uint32).view(np.float32)
+
+
+def test_round_bf16_is_nearest_even():
+    from oracle.network import round_bf16
+
+    one = np.float32(1.0)
+    cases = {
+        1.0: 1.0,
+        1 + 2.0**-8: 1.0,                    # tie -> even (mantissa 0)
+        1 + 3 * 2.0**-8: 1 + 2.0**-6,        # tie -> even (mantissa 2)
+        1 + 2.0**-8 + 2.0**-20: 1 + 2.0**-7,  # just above the tie
+        -(1 + 3 * 2.0**-8): -(1 + 2.0**-6),
+        65504.0: 65536.0,
+    }
+    got = round_bf16(torch.tensor(list(cases), dtype=torch.float32)).numpy()
+    np.testing.assert_array_equal(got, np.array(list(cases.values()), dtype=np.float32))
+    x = (np.random.default_rng(12).standard_normal(100_000) * 10.0 ** np.random.default_rng(13)
+         .integers(-20, 20, 100_000)).astype(np.float32)
+    np.testing.assert_array_equal(round_bf16(torch.from_numpy(x)).numpy(), _rne_bf16_bits(x))
+    assert one == round_bf16(torch.tensor([one])).item()
+
+
+def test_bf16_oracle_rounding_points():
+    """bf16 mode rounds the operands of the 3-D convolutions with >= 8 taps except the one
+    reading the network input, and of the transposed convolutions; nothing else.  The
+    logits then move by a bf16-sized amount."""
+    spec = PlainConvUNetSpec(1, 3, (4, 8), ((3, 3, 3), (3, 3, 3)), ((1, 1, 1), (2, 2, 2)), (2, 2), (2,))
+    w = random_weights(spec, seed=5, random_affine=True)
+    net = OracleNetwork(spec, w, bf16=True)
+    x = torch.randn(1, 4, 6, 6, 6, generator=torch.Generator().manual_seed(0))
+    k3 = torch.randn(8, 4, 3, 3, 3, generator=torch.Generator().manual_seed(1))
+    k1 = torch.randn(8, 4, 1, 1, 1, generator=torch.Generator().manual_seed(2))
+    from oracle.network import round_bf16
+
+    for prefix, weight, rounded in (("enc0.block1", k3, True), ("dec0.block0", k3, True),
+                                    ("up", k3, True), ("enc0.block0", k3, False),
+                                    ("stem", k3, False), ("res1.block0.proj", k1, False)):
+        xo, wo = net._bf16_operands(prefix, x, weight)
+        assert torch.equal(xo, round_bf16(x) if rounded else x), prefix
+        assert torch.equal(wo, round_bf16(weight) if rounded else weight), prefix
+    xo, wo = OracleNetwork(spec, w)._bf16_operands("enc0.block1", x, k3)
+    assert xo is x and wo is k3
+    xs = np.random.default_rng(6).standard_normal((1, 8, 8, 8, 1)).astype(np.float32)
+    full = OracleNetwork(spec, w)(xs)
+    emulated = net(xs)
+    rel = np.linalg.norm(emulated - full) / np.linalg.norm(full)
+    assert 1e-5 < rel < 3e-2
