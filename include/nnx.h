@@ -251,6 +251,17 @@ int nnx_tconv3d_bf16(const float* d_x, int cin, const void* d_packed, float scal
                      const float* d_bias, float* d_y, int batch, const int* in_size, int cout,
                      const int* ksize, void* stream);
 
+/* Restoration of class logits to the original grid: half-pixel trilinear resampling
+ * (coordinates clamped to the source edges) of channels-last logits
+ * (src_shape[0], src_shape[1], src_shape[2], classes) to dst_shape, evaluated in float64,
+ * then the first-maximum argmax into uint16 labels (dst_shape). half != 0: the logits are
+ * float16 and each interpolated value is rounded to float16 (nearest even) before the
+ * comparison.  classes <= 65536.
+ * Replaces the fused Metal restoration _launch / resample_device_logits_argmax
+ * (src/nnunet_mlx/kernels/metal_restore.py:358-427, kernel :69-137). */
+int nnx_restore_labels(const void* d_logits, int half, int classes, const int* src_shape,
+                       const int* dst_shape, uint16_t* d_labels, void* stream);
+
 /* 1x1x1 convolution with bias (segmentation head), NDHWC.
  * Replaces seg{n-1} (src/nnunet_mlx/model/network.py:804-808,875-876). */
 int nnx_conv1x1(const float* d_x, int cin, const float* d_weight /* (Cout,1,1,1,Cin) */,

@@ -168,6 +168,12 @@ void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin,
 void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const float* bias,
                 float* y, int batch, const int* in_size, int cout, const int* ksize,
                 hipStream_t st, int arith = kArithSplit3);
+// Class-logit restoration: half-pixel trilinear (edge-clamped, float64) resampling of
+// channels-last logits (src[0], src[1], src[2], classes) to dst, then first-maximum argmax
+// into uint16 labels (dst[0], dst[1], dst[2]).  `half`: float16 logits, values rounded to
+// float16 before the comparison.
+void restore_labels(const void* logits, bool half, int classes, const int* src, const int* dst,
+                    uint16_t* labels, hipStream_t st);
 // `item_voxels` = voxels per batch item (to index the pending norm's parameters).
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y,
              int64_t voxels, int cout, hipStream_t st, const PendingNorm& nx = {},

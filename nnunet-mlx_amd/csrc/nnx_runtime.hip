@@ -1116,6 +1116,15 @@ int nnx_tconv3d_bf16(const float* d_x, int cin, const void* d_packed, float scal
   });
 }
 
+int nnx_restore_labels(const void* d_logits, int half, int classes, const int* src_shape,
+                       const int* dst_shape, uint16_t* d_labels, void* stream) {
+  return guarded([&] {
+    require(src_shape && dst_shape, "null argument");
+    restore_labels(d_logits, half != 0, classes, src_shape, dst_shape, d_labels,
+                   as_stream(stream));
+  });
+}
+
 int nnx_conv1x1(const float* d_x, int cin, const float* d_weight, const float* d_bias, float* d_y,
                 int64_t voxels, int cout, void* stream) {
   return guarded([&] { conv1x1(d_x, cin, d_weight, d_bias, d_y, voxels, cout, as_stream(stream)); });

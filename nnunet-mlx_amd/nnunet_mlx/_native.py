@@ -174,6 +174,9 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p, ctypes.c_int, c_int_p,
          ctypes.c_int, c_int_p, c_void_p],
     ),
+    "nnx_restore_labels": (
+        ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, c_int_p, c_int_p, c_void_p, c_void_p]
+    ),
     "nnx_tconv3d_gemm": (
         ctypes.c_int,
         [c_void_p, ctypes.c_int, c_void_p, c_void_p, c_void_p, ctypes.c_int, c_int_p, ctypes.c_int,

@@ -2,13 +2,15 @@
 
 Reference: PlansContract / PlanConfiguration (src/nnunet_mlx/plans.py:154-372).  Only
 what the inference path consumes is parsed here: the inheritance-resolved
-configuration, its ``patch_size`` and ``architecture``.
+configuration, its ``patch_size`` and ``architecture``, and the resampling contract
+that restoration reads.
 """
 
 from __future__ import annotations
 
 import json
 from collections.abc import Mapping
+from dataclasses import dataclass
 from pathlib import Path
 
 from nnunet_mlx.errors import ContractError
@@ -61,3 +63,54 @@ def patch_size(plans: Mapping[str, object], configuration: str) -> tuple[int, ..
     if not isinstance(raw, list) or not all(isinstance(v, int) and not isinstance(v, bool) and v > 0 for v in raw):
         raise ContractError("plans patch_size must be a list of positive integers")
     return tuple(raw)
+
+
+# ---- resampling contract ------------------------------------------------------------
+# Reference: ResamplingContract (src/nnunet_mlx/plans.py:31-160).  The fields the
+# restoration policy reads; the parser accepts the two upstream resampling functions and
+# keeps nnU-Net 2.8.1's defaults for omitted spline options (order 3, order_z 0,
+# force_separate_z False, anisotropy threshold 3; the Torch resampler: order 1, order_z 0,
+# force_separate_z None).
+
+
+RESAMPLING_FUNCTIONS = ("resample_data_or_seg_to_shape", "resample_torch_fornnunet")
+
+
+@dataclass(frozen=True)
+class ResamplingContract:
+    """One upstream ``resampling_fn_*`` plan entry (the fields restoration reads)."""
+
+    function_name: str
+    order: int
+    order_z: int
+    force_separate_z: bool | None
+    separate_z_anisotropy_threshold: float = 3.0
+
+    @classmethod
+    def from_configuration(cls, configuration: Mapping[str, object], *, field: str,
+                           expected_is_seg: bool) -> "ResamplingContract":
+        """Parse ``configuration[field]`` and ``<field>_kwargs``
+        (src/nnunet_mlx/plans.py:60-160); raises ContractError on unsupported entries."""
+        name = configuration.get(field)
+        if name not in RESAMPLING_FUNCTIONS:
+            raise ContractError(f"unsupported nnU-Net resampling function {name!r}")
+        kwargs = configuration.get(f"{field}_kwargs", {})
+        if not isinstance(kwargs, Mapping):
+            raise ContractError(f"{field}_kwargs must be a mapping")
+        torch_resampling = name == "resample_torch_fornnunet"
+        is_seg = kwargs.get("is_seg", False)
+        if not isinstance(is_seg, bool) or is_seg is not expected_is_seg:
+            raise ContractError(f"{field}.is_seg does not match its runtime role")
+        force = kwargs.get("force_separate_z", None if torch_resampling else False)
+        if force is not None and not isinstance(force, bool):
+            raise ContractError(f"{field}.force_separate_z must be boolean or null")
+        threshold = kwargs.get("separate_z_anisotropy_threshold", 3.0)
+        if isinstance(threshold, bool) or not isinstance(threshold, (int, float)) or threshold <= 0:
+            raise ContractError(f"{field}.separate_z_anisotropy_threshold must be positive")
+        if torch_resampling:
+            return cls(name, 1, 0, force, float(threshold))
+        order, order_z = kwargs.get("order", 3), kwargs.get("order_z", 0)
+        for label, value in (("order", order), ("order_z", order_z)):
+            if isinstance(value, bool) or not isinstance(value, int) or not 0 <= value <= 5:
+                raise ContractError(f"{field}.{label} must be an integer in [0, 5]")
+        return cls(name, order, order_z, force, float(threshold))

@@ -12,6 +12,9 @@ Modules:
                          src/nnunet_mlx/kernels/metal_native_norm.py.
   * ``sliding_window`` — numpy restatement of src/nnunet_mlx/prediction/sliding_window.py
                          and the fold ensemble of src/nnunet_mlx/prediction/inference.py.
+  * ``restore``        — numpy float64 restatement of the class-logit restoration
+                         (half-pixel trilinear + argmax) of
+                         src/nnunet_mlx/kernels/metal_restore.py.
 
 Pinning (what checks each function against something other than itself) is listed
 in the module docstrings and exercised by ``tests/test_oracle_*.py``.  Nothing here
