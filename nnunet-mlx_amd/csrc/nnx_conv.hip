@@ -1133,83 +1133,96 @@ void launch_x3s(const IgemmArgs& a, bool vec, int arith, hipStream_t st, double 
 }
 
 // ---------------------------------------------------------------------------------
-// One-input-channel 3x3x3 convolution: one thread per output voxel keeps the 27 taps
-// in registers (zeros in the padding) and starts every output channel from 0 with
-// fma over the taps in (kd, kh, kw) order.  The optional bias is a separate addition.
+// One-input-channel 3x3x3 convolution: one thread per output voxel takes its 27 taps
+// (zeros in the padding) and starts every output channel from 0 with fma over the taps
+// in (kd, kh, kw) order.  The optional bias is a separate addition.
+// Grid: (4 x 8 x 8 tiles per batch item, batch); the tile's 6 x 10 x 10 input halo is read
+// once into LDS.  Weights and bias are read through the constant address space: the
+// loads are uniform, so they become scalar loads and every fma takes its weight from an
+// SGPR.  The output rows are staged in LDS and leave as contiguous runs of 8 voxels.
+// With `stats`, the tile also writes the InstanceNorm partials of its voxels,
+// stats[(b * gridDim.x + tile) * cout + c] = (mean, M2, n, 0) of conv + bias, two-pass
+// over the tile's outputs in LDS.
 // ---------------------------------------------------------------------------------
-// Grid: (blocks of 256 voxels per batch item, batch).  With `stats`, the block also writes
-// the InstanceNorm partials of its voxels, stats[(b * gridDim.x + block) * cout + c] =
-// (mean, M2, n, 0) of conv + bias, two-pass over the block's outputs in LDS.
-// Weights and bias are read through the constant address space: the loads are uniform,
-// so they become scalar loads and every fma takes its weight from an SGPR (no LDS reads).
+constexpr int kDirTz = 4, kDirTy = 8, kDirTx = 8;
+constexpr int kDirHz = kDirTz + 2, kDirHy = kDirTy + 2, kDirHx = kDirTx + 2;
+
 template <int COUT>
 __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restrict__ x,
                                                           const float* __restrict__ w,
                                                           const float* __restrict__ bias,
-                                                          float* __restrict__ y, int64_t S,
-                                                          int D, int H, int W,
+                                                          float* __restrict__ y, int D, int H,
+                                                          int W, int tiles_y, int tiles_x,
                                                           float4* __restrict__ stats) {
   typedef const __attribute__((address_space(4))) float* cfloat_p;
   constexpr int cout = COUT;
+  constexpr int stride = cout + 1;  // padded output rows: no bank conflicts
+  __shared__ float halo[kDirHz * kDirHy * kDirHx];
   __shared__ float red[256];
-  extern __shared__ float out_s[];  // 256 voxels x (cout + 1): padded rows, no bank conflicts
+  extern __shared__ float out_s[];  // 256 voxels x (cout + 1)
   const cfloat_p wc = (cfloat_p)w;
   const cfloat_p bc = (cfloat_p)bias;
-  const int64_t s0 = blockIdx.x * (int64_t)blockDim.x;
-  const int64_t v0 = (int64_t)blockIdx.y * S + s0;  // first voxel of the block in the batch
-  const int64_t vox = v0 + threadIdx.x;
-  const int64_t nvox = (int64_t)blockIdx.y * S + S;  // end of this batch item
-  const int stride = cout + 1;
-  if (vox < nvox) {
-    const int xx = (int)(vox % W);
-    const int yy = (int)((vox / W) % H);
-    const int zz = (int)((vox / ((int64_t)W * H)) % D);
-    const int64_t plane = (vox / ((int64_t)W * H * D)) * D;
+  const int tid = threadIdx.x;
+  const int tile = blockIdx.x;
+  const int txi = tile % tiles_x, tyi = (tile / tiles_x) % tiles_y, tzi = tile / (tiles_x * tiles_y);
+  const int z0 = tzi * kDirTz, y0 = tyi * kDirTy, x0 = txi * kDirTx;
+  const int64_t item = (int64_t)blockIdx.y * D * H * W;  // first voxel of the batch item
+  for (int i = tid; i < kDirHz * kDirHy * kDirHx; i += 256) {
+    const int hz = i / (kDirHy * kDirHx), hy = (i / kDirHx) % kDirHy, hx = i % kDirHx;
+    const int z = z0 + hz - 1, yy = y0 + hy - 1, xx = x0 + hx - 1;
+    const bool inside = (unsigned)z < (unsigned)D && (unsigned)yy < (unsigned)H &&
+                        (unsigned)xx < (unsigned)W;
+    halo[i] = inside ? x[item + ((int64_t)z * H + yy) * W + xx] : 0.f;
+  }
+  __syncthreads();
+  const int tz = tid >> 6, ty = (tid >> 3) & 7, tx = tid & 7;
+  {
     float taps[27];
 #pragma unroll
-    for (int kd = 0; kd < 3; ++kd) {
-      const int d = zz + kd - 1;
+    for (int kd = 0; kd < 3; ++kd)
 #pragma unroll
-      for (int kh = 0; kh < 3; ++kh) {
-        const int h = yy + kh - 1;
+      for (int kh = 0; kh < 3; ++kh)
 #pragma unroll
-        for (int kw = 0; kw < 3; ++kw) {
-          const int ww = xx + kw - 1;
-          const bool inside = d >= 0 && d < D && h >= 0 && h < H && ww >= 0 && ww < W;
-          taps[(kd * 3 + kh) * 3 + kw] = inside ? x[((plane + d) * H + h) * W + ww] : 0.f;
-        }
-      }
-    }
+        for (int kw = 0; kw < 3; ++kw)
+          taps[(kd * 3 + kh) * 3 + kw] = halo[((tz + kd) * kDirHy + ty + kh) * kDirHx + tx + kw];
     const bool has_bias = bias != nullptr;
 #pragma unroll
     for (int c = 0; c < cout; ++c) {
       float sum = 0.f;
 #pragma unroll
       for (int t = 0; t < 27; ++t) sum = fmaf(taps[t], wc[c * 27 + t], sum);
-      out_s[threadIdx.x * stride + c] = has_bias ? sum + bc[c] : sum;
+      out_s[tid * stride + c] = has_bias ? sum + bc[c] : sum;
     }
   }
   __syncthreads();
-  const int64_t nv = nvox - v0 < (int64_t)blockDim.x ? nvox - v0 : (int64_t)blockDim.x;
-  // the block's voxels are contiguous in NDHWC: write them as one coalesced run
-  const int total4 = (int)(nv * cout / 4);
-  f4* dst = reinterpret_cast<f4*>(y + v0 * cout);
-  for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
-    const int e = e4 * 4;
-    const int v = e / cout, c = e - v * cout;
-    const float* src = out_s + v * stride + c;
-    dst[e4] = f4{src[0], src[1], src[2], src[3]};
+  // rows (tz, ty) of up to 8 voxels: cout * nx contiguous floats each, one wave per row
+  const int nx = W - x0 < kDirTx ? W - x0 : kDirTx;
+  const int wave = tid >> 6, lane = tid & 63;
+  for (int r = wave; r < kDirTz * kDirTy; r += 4) {
+    const int rz = r >> 3, ry = r & 7;
+    if (z0 + rz >= D || y0 + ry >= H) continue;
+    f4* dst = reinterpret_cast<f4*>(y + (item + ((int64_t)(z0 + rz) * H + y0 + ry) * W + x0) * cout);
+    for (int i = lane; i < nx * cout / 4; i += 64) {
+      const int e = i * 4;
+      const int v = e / cout, c = e - v * cout;
+      const float* src = out_s + (r * kDirTx + v) * stride + c;
+      dst[i] = f4{src[0], src[1], src[2], src[3]};
+    }
   }
   // statistics after the stores are issued, so they overlap the write-back
   if (stats) {
-    // channel c = tid % cout, rows part, part + parts, ...: block mean, then centred M2
-    const int parts = blockDim.x / cout;
-    const int c = threadIdx.x % cout, part = threadIdx.x / cout;
+    // channel c = tid % cout over voxels part, part + parts, ...: tile mean, then centred M2
+    const int nz = D - z0 < kDirTz ? D - z0 : kDirTz, ny = H - y0 < kDirTy ? H - y0 : kDirTy;
+    const int nv = nz * ny * nx;
+    const int parts = 256 / cout;
+    const int c = tid % cout, part = tid / cout;
     const bool active = part < parts;
+    auto in_tile = [&](int v) { return (v >> 6) < nz && ((v >> 3) & 7) < ny && (v & 7) < nx; };
     float t = 0.f;
     if (active)
-      for (int r = part; r < nv; r += parts) t += out_s[r * stride + c];
-    red[threadIdx.x] = t;
+      for (int v = part; v < 256; v += parts)
+        if (in_tile(v)) t += out_s[v * stride + c];
+    red[tid] = t;
     __syncthreads();
     float mean = 0.f;
     if (active) {
@@ -1219,11 +1232,12 @@ __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restric
     __syncthreads();
     t = 0.f;
     if (active)
-      for (int r = part; r < nv; r += parts) {
-        const float d = out_s[r * stride + c] - mean;
-        t = fmaf(d, d, t);
-      }
-    red[threadIdx.x] = t;
+      for (int v = part; v < 256; v += parts)
+        if (in_tile(v)) {
+          const float d = out_s[v * stride + c] - mean;
+          t = fmaf(d, d, t);
+        }
+    red[tid] = t;
     __syncthreads();
     if (part == 0) {
       float m2 = 0.f;
@@ -1983,7 +1997,7 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
 }
 
 int conv_direct_stats_tiles(const int* size) {
-  return (int)ceil_div((int64_t)size[0] * size[1] * size[2], 256);
+  return (int)(ceil_div(size[0], kDirTz) * ceil_div(size[1], kDirTy) * ceil_div(size[2], kDirTx));
 }
 
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
@@ -1995,14 +2009,17 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
   const int64_t S = (int64_t)size[0] * size[1] * size[2];
   require(S >= 1, "empty convolution input");
   const int64_t nvox = (int64_t)batch * S;
+  const int tiles_y = (int)ceil_div(size[1], kDirTy), tiles_x = (int)ceil_div(size[2], kDirTx);
+  const int64_t tiles = conv_direct_stats_tiles(size);
+  require(tiles < (1LL << 31), "convolution volume too large");
   ProfScope prof("conv3d_direct_cin1", 2.0 * 27 * cout * (double)nvox, 4.0 * (double)nvox * (1 + cout), st);
-  const dim3 grid((unsigned)ceil_div(S, 256), (unsigned)batch);
+  const dim3 grid((unsigned)tiles, (unsigned)batch);
   const size_t lds = (size_t)256 * (cout + 1) * sizeof(float);
   switch (cout / 4) {
 #define NNX_DIRECT_CASE(Q)                                                                     \
   case Q:                                                                                      \
-    hipLaunchKernelGGL(direct_cin1_kernel<4 * Q>, grid, dim3(256), lds, st, x, w, bias, y, S,  \
-                       size[0], size[1], size[2], stats);                                      \
+    hipLaunchKernelGGL(direct_cin1_kernel<4 * Q>, grid, dim3(256), lds, st, x, w, bias, y,     \
+                       size[0], size[1], size[2], tiles_y, tiles_x, stats);                    \
     break;
     NNX_DIRECT_CASE(1) NNX_DIRECT_CASE(2) NNX_DIRECT_CASE(3) NNX_DIRECT_CASE(4)
     NNX_DIRECT_CASE(5) NNX_DIRECT_CASE(6) NNX_DIRECT_CASE(7) NNX_DIRECT_CASE(8)
