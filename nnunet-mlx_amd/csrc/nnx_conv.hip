@@ -1619,32 +1619,37 @@ __global__ __launch_bounds__(256) void conv1x1_kernel(const float* __restrict__ 
   }
 }
 
-// Head for narrow inputs (C_in <= 63): the block's 256 input rows are loaded into LDS with
-// coalesced float4 reads (rows padded to C_in + 1 floats), each thread forms its voxel's
-// outputs (fma chain over channels, then + bias), and the outputs leave as one run.
+// Head for narrow inputs (C_in <= 64, a multiple of 4): the block's 256 input rows are
+// loaded into LDS with coalesced float4 reads (rows padded to C_in + 4 floats, so a row is
+// read back as float4s without bank conflicts), each thread keeps its voxel's row in
+// registers and forms its outputs (fma chain over channels, then + bias) with the weights
+// from scalar loads (uniform addresses in the constant address space), and the outputs
+// leave as one run.
+template <int CIN>
 __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ w,
                                                              const float* __restrict__ bias,
                                                              float* __restrict__ y, int64_t nvox,
-                                                             int cin, int cout,
+                                                             int cout,
                                                              const float4* __restrict__ nrm,
                                                              int act, float slope,
                                                              int64_t item_vox) {
-  extern __shared__ float smem[];
-  float* ws = smem;                          // cout * cin
-  float* xs = smem + cout * cin;             // 256 * (cin + 1)
-  float* os = xs + 256 * (cin + 1);          // 256 * cout
-  for (int i = threadIdx.x; i < cout * cin; i += blockDim.x) ws[i] = w[i];
+  typedef const __attribute__((address_space(4))) float* cfloat_p;
+  constexpr int cin = CIN, cin4 = CIN / 4, xstride = CIN + 4;
+  extern __shared__ __align__(16) float smem[];
+  float* xs = smem;                   // 256 * (cin + 4)
+  float* os = xs + 256 * xstride;     // 256 * cout
+  const cfloat_p wc = (cfloat_p)w;
+  const cfloat_p bc = (cfloat_p)bias;
   const int64_t v0 = blockIdx.x * (int64_t)blockDim.x;
   const int nv = (int)(nvox - v0 < 256 ? nvox - v0 : 256);
   const float4* src = reinterpret_cast<const float4*>(x + v0 * cin);
-  const int cin4 = cin / 4;
   const int total4 = nv * cin4;
   // batch item of the block's first voxel; rows from `split` on belong to the next item
   const int64_t item0 = nrm ? v0 / item_vox : 0;
   const int64_t split = nrm ? (item0 + 1) * item_vox - v0 : 0;
   // (row, channel group) of element e4 = row * cin4 + group, advanced without divisions
-  const int step_r = (int)blockDim.x / cin4, step_g = (int)blockDim.x % cin4;
+  constexpr int step_r = 256 / cin4, step_g = 256 % cin4;
   int r = (int)threadIdx.x / cin4, g = (int)threadIdx.x % cin4;
   for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
     float4 v = src[e4];
@@ -1656,11 +1661,7 @@ __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __rest
       v.z = norm_apply1(v.z, pr[2], act, slope);
       v.w = norm_apply1(v.w, pr[3], act, slope);
     }
-    float* d = xs + r * (cin + 1) + c;
-    d[0] = v.x;
-    d[1] = v.y;
-    d[2] = v.z;
-    d[3] = v.w;
+    *reinterpret_cast<f4*>(xs + r * xstride + c) = f4{v.x, v.y, v.z, v.w};
     r += step_r;
     g += step_g;
     if (g >= cin4) {
@@ -1670,12 +1671,15 @@ __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __rest
   }
   __syncthreads();
   if ((int)threadIdx.x < nv) {
-    const float* xr = xs + threadIdx.x * (cin + 1);
+    f4 xr[cin4];
+#pragma unroll
+    for (int c4 = 0; c4 < cin4; ++c4)
+      xr[c4] = *reinterpret_cast<const f4*>(xs + threadIdx.x * xstride + c4 * 4);
     for (int o = 0; o < cout; ++o) {
       float s = 0.f;
-      const float* wr = ws + o * cin;
-      for (int c = 0; c < cin; ++c) s = fmaf(xr[c], wr[c], s);
-      os[threadIdx.x * cout + o] = bias ? s + bias[o] : s;
+#pragma unroll
+      for (int c = 0; c < cin; ++c) s = fmaf(xr[c >> 2][c & 3], wc[o * cin + c], s);
+      os[threadIdx.x * cout + o] = bias ? s + bc[o] : s;
     }
   }
   __syncthreads();
@@ -2160,12 +2164,22 @@ void conv1x1(const float* x, int cin, const float* w, const float* bias, float* 
           "1x1 convolution weight too large for the head kernel");
   require(voxels >= 1, "empty 1x1 convolution input");
   ProfScope prof("conv1x1_head", 2.0 * (double)voxels * cin * cout, 4.0 * (double)voxels * (cin + cout), st);
-  const size_t staged = ((size_t)cin * cout + 256 * (cin + 1) + 256 * cout) * sizeof(float);
-  if (cin % 4 == 0 && staged <= 64 * 1024)
-    hipLaunchKernelGGL(conv1x1_staged_kernel, dim3((unsigned)ceil_div(voxels, 256)), dim3(256),
-                       staged, st, x, w, bias, y, voxels, cin, cout, nx.params, act, nx.slope,
-                       item);
-  else
+  const size_t staged = ((size_t)256 * (cin + 4) + 256 * cout) * sizeof(float);
+  const dim3 grid((unsigned)ceil_div(voxels, 256));
+  if (cin % 4 == 0 && cin <= 64 && staged <= 96 * 1024) {
+    switch (cin / 4) {
+#define NNX_HEAD_CASE(Q)                                                                        \
+  case Q:                                                                                       \
+    hipLaunchKernelGGL(conv1x1_staged_kernel<4 * Q>, grid, dim3(256), staged, st, x, w, bias, y, \
+                       voxels, cout, nx.params, act, nx.slope, item);                           \
+    break;
+      NNX_HEAD_CASE(1) NNX_HEAD_CASE(2) NNX_HEAD_CASE(3) NNX_HEAD_CASE(4)
+      NNX_HEAD_CASE(5) NNX_HEAD_CASE(6) NNX_HEAD_CASE(7) NNX_HEAD_CASE(8)
+      NNX_HEAD_CASE(9) NNX_HEAD_CASE(10) NNX_HEAD_CASE(11) NNX_HEAD_CASE(12)
+      NNX_HEAD_CASE(13) NNX_HEAD_CASE(14) NNX_HEAD_CASE(15) NNX_HEAD_CASE(16)
+#undef NNX_HEAD_CASE
+    }
+  } else
     hipLaunchKernelGGL(conv1x1_kernel, dim3((unsigned)ceil_div(voxels, 256)), dim3(256),
                        (size_t)cin * cout * sizeof(float), st, x, w, bias, y, voxels, cin, cout,
                        nx.params, act, nx.slope, item);
