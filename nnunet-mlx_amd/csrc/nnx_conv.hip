@@ -1643,31 +1643,53 @@ __global__ __launch_bounds__(256) void conv1x1_staged_kernel(const float* __rest
   const cfloat_p bc = (cfloat_p)bias;
   const int64_t v0 = blockIdx.x * (int64_t)blockDim.x;
   const int nv = (int)(nvox - v0 < 256 ? nvox - v0 : 256);
-  const float4* src = reinterpret_cast<const float4*>(x + v0 * cin);
+  const f4* src = reinterpret_cast<const f4*>(x + v0 * cin);
   const int total4 = nv * cin4;
-  // batch item of the block's first voxel; rows from `split` on belong to the next item
-  const int64_t item0 = nrm ? v0 / item_vox : 0;
-  const int64_t split = nrm ? (item0 + 1) * item_vox - v0 : 0;
-  // (row, channel group) of element e4 = row * cin4 + group, advanced without divisions
-  constexpr int step_r = 256 / cin4, step_g = 256 % cin4;
-  int r = (int)threadIdx.x / cin4, g = (int)threadIdx.x % cin4;
-  for (int e4 = threadIdx.x; e4 < total4; e4 += blockDim.x) {
-    float4 v = src[e4];
-    const int c = g * 4;
-    if (nrm) {
-      const float4* pr = nrm + (item0 + (r >= split ? 1 : 0)) * cin + c;
-      v.x = norm_apply1(v.x, pr[0], act, slope);
-      v.y = norm_apply1(v.y, pr[1], act, slope);
-      v.z = norm_apply1(v.z, pr[2], act, slope);
-      v.w = norm_apply1(v.w, pr[3], act, slope);
+  // a full block holds 256 * cin4 float4s: cin4 per thread, all loads issued before use
+  f4 v[cin4];
+#pragma unroll
+  for (int j = 0; j < cin4; ++j) {
+    const int e4 = j * 256 + (int)threadIdx.x;
+    v[j] = e4 < total4 ? src[e4] : f4{0.f, 0.f, 0.f, 0.f};
+  }
+  if (nrm) {
+    // batch item of the block's first voxel; rows from `split` on belong to the next item
+    const int64_t item0 = v0 / item_vox;
+    const int64_t split = (item0 + 1) * item_vox - v0;
+    auto apply = [&](f4& val, const float4* pr) {
+      val[0] = norm_apply1(val[0], pr[0], act, slope);
+      val[1] = norm_apply1(val[1], pr[1], act, slope);
+      val[2] = norm_apply1(val[2], pr[2], act, slope);
+      val[3] = norm_apply1(val[3], pr[3], act, slope);
+    };
+    if constexpr (256 % cin4 == 0) {
+      // every element of this thread lies in channel group tid % cin4
+      const int c = ((int)threadIdx.x % cin4) * 4;
+      float4 pa[4], pb[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pa[q] = nrm[item0 * cin + c + q];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) pb[q] = split < nv ? nrm[(item0 + 1) * cin + c + q] : pa[q];
+#pragma unroll
+      for (int j = 0; j < cin4; ++j) {
+        const int r = (j * 256 + (int)threadIdx.x) / cin4;
+        apply(v[j], r >= split ? pb : pa);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < cin4; ++j) {
+        const int e4 = j * 256 + (int)threadIdx.x;
+        const int r = e4 / cin4;
+        if (e4 < total4)
+          apply(v[j], nrm + (item0 + (r >= split ? 1 : 0)) * cin + (e4 - r * cin4) * 4);
+      }
     }
-    *reinterpret_cast<f4*>(xs + r * xstride + c) = f4{v.x, v.y, v.z, v.w};
-    r += step_r;
-    g += step_g;
-    if (g >= cin4) {
-      g -= cin4;
-      ++r;
-    }
+  }
+#pragma unroll
+  for (int j = 0; j < cin4; ++j) {
+    const int e4 = j * 256 + (int)threadIdx.x;
+    const int r = e4 / cin4;
+    if (e4 < total4) *reinterpret_cast<f4*>(xs + r * xstride + (e4 - r * cin4) * 4) = v[j];
   }
   __syncthreads();
   if ((int)threadIdx.x < nv) {

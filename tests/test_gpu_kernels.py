@@ -46,6 +46,10 @@ CONV_CASES = [
     (1, (8, 8, 8), 16, 0, 32, (1, 1, 1), (1, 1, 1)),
     (1, (9, 9, 9), 3, 0, 5, (3, 3, 3), (1, 1, 1)),
     (1, (5, 7, 6), 12, 20, 24, (3, 3, 3), (1, 1, 1)),
+    # strided with two inputs of ragged channel counts; strided along y, x only with a
+    # 1 x 3 x 3 kernel
+    (2, (9, 12, 10), 12, 20, 24, (3, 3, 3), (2, 2, 2)),
+    (1, (6, 14, 13), 8, 0, 16, (1, 3, 3), (1, 2, 2)),
 ]
 
 

@@ -58,6 +58,10 @@ CASES = {
     "plain-nondivisible": (PlainConvUNetSpec(1, 3, (8, 16, 32), K3 * 3,
                                              ((1, 1, 1), (2, 2, 2), (2, 2, 2)), (2, 2, 2), (2, 2)),
                            (13, 18, 21), 2, True),
+    # 12 head channels (not a power-of-two number of float4 groups) and batch items that
+    # end inside a 256-voxel block of the head
+    "plain-12ch-ragged": (PlainConvUNetSpec(1, 3, (12, 24), K3 * 2, ((1, 1, 1), (2, 2, 2)),
+                                            (2, 2), (2,)), (7, 9, 11), 2, True),
 }
 
 
