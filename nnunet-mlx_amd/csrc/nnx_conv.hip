@@ -581,7 +581,7 @@ __device__ __forceinline__ void mma_products(f4 (&acc)[MB][NB], const h8 (&A)[MB
 constexpr int kX3MaxLines = 6;  // halo lines per thread in flight (register staging)
 constexpr int kX3Threads = 256;
 
-template <int MB, int NB, int WM, int WN, int NTG, int AR>
+template <int MB, int NB, int WM, int WN, int NTG, bool VEC, int AR>
 __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
   extern __shared__ __align__(16) float lds[];
   constexpr int NT = 64 * WM * WN;
@@ -667,26 +667,33 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
   }
   const int64_t bvox = (int64_t)b * a.id * a.ih * a.iw;
 
+  // two column blocks a wave: a chunk's weight fragments fit in registers at once
+  constexpr bool kPreloadB = NB <= 2;
+  // The next chunk's lines are requested without branches (lines outside the volume read
+  // a zero line) and are used only at publish time, where the pending normalisation is
+  // applied, so their loads stay in flight while the current chunk computes.
+  const float* zero = g_zero_line;
   f4 stage[kX3MaxLines];
+  NormLine nl_staged;
   auto fetch = [&](int chunk) {
     const HaloSource hs = halo_source(a, chunk);
     const int c = hs.cb + h * 4;
-    const NormLine nl = norm_line(a, chunk, b, hs.C, c);
+    nl_staged = norm_line(a, chunk, b, hs.C, c);
 #pragma unroll
     for (int j = 0; j < kX3MaxLines; ++j) {
-      f4 val = {0.f, 0.f, 0.f, 0.f};
-      if (vofs[j] >= 0) {
-        const int64_t off = (bvox + vofs[j]) * hs.C + c;
-        if ((hs.C & 3) == 0) {
-          if (c < hs.C) val = *reinterpret_cast<const f4*>(hs.src + off);
-        } else {
+      if constexpr (VEC) {
+        const float* src = vofs[j] >= 0 ? hs.src + (bvox + vofs[j]) * hs.C + c : zero;
+        stage[j] = *reinterpret_cast<const f4*>(src);
+      } else {
+        f4 val = {0.f, 0.f, 0.f, 0.f};
+        if (vofs[j] >= 0) {
+          const int64_t off = (bvox + vofs[j]) * hs.C + c;
 #pragma unroll
           for (int q = 0; q < 4; ++q)
             if (c + q < hs.C) val[q] = hs.src[off + q];
         }
-        if (nl.on) val = norm_apply4(val, nl, a.slope);
+        stage[j] = val;
       }
-      stage[j] = val;
     }
   };
   auto publish = [&]() {
@@ -694,11 +701,13 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
     for (int j = 0; j < kX3MaxLines; ++j) {
       const int line = j * NT + tid;
       if (line < nlines) {
+        f4 val = stage[j];
+        if (nl_staged.on && vofs[j] >= 0) val = norm_apply4(val, nl_staged, a.slope);
         h4 hv, lv;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
           _Float16 hh, ll;
-          to_operand<AR>(stage[j][q], hh, ll);
+          to_operand<AR>(val[q], hh, ll);
           hv[q] = hh;
           lv[q] = ll;
         }
@@ -732,6 +741,36 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
         if constexpr (AR == kSplit3) A[p][mb][1] = lo8[hbase[mb] + toff[g]];
       }
     };
+    if constexpr (kPreloadB) {
+      // every tap group's weights are requested before the next halo: vector-memory
+      // counters complete in issue order, so no weight wait queues behind the halo loads
+      __syncthreads();  // the previous chunk's fragments have been read
+      publish();
+      __syncthreads();
+      h8 BA[NTG][NB][2];
+#pragma unroll
+      for (int g = 0; g < NTG; ++g)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const uint4 wh = wc[g * group_stride + nb * 128];
+          BA[g][nb][0] = *reinterpret_cast<const h8*>(&wh);
+          if constexpr (AR == kSplit3) {
+            const uint4 wl = wc[g * group_stride + nb * 128 + 64];
+            BA[g][nb][1] = *reinterpret_cast<const h8*>(&wl);
+          }
+        }
+      // lands while this chunk computes; unconditional (the last chunk re-reads its own
+      // lines), so no control-flow join makes the weight waits cover the halo loads
+      fetch(chunk + 1 < a.chunks ? chunk + 1 : chunk);
+      load_a(0, 0);
+#pragma unroll
+      for (int g = 0; g < NTG; ++g) {
+        const int cur = g & 1;
+        if (g + 1 < NTG) load_a(cur ^ 1, g + 1);
+        mma_products<AR>(acc, A[cur], BA[g]);
+      }
+      continue;
+    }
     load_b(0, 0);  // in flight across the barriers below
     __syncthreads();  // the previous chunk's fragments have been read
     publish();
@@ -1051,15 +1090,23 @@ void launch_igemm(const IgemmArgs& a, int nwg, bool async, hipStream_t st, doubl
   launch_check("conv3d_igemm");
 }
 
-template <int MB, int NB, int WM, int WN, int NTG>
-void launch_x3_ntg(const IgemmArgs& a, int arith, size_t lds_bytes, hipStream_t st) {
+template <int MB, int NB, int WM, int WN, int NTG, bool VEC>
+void launch_x3_vec(const IgemmArgs& a, int arith, size_t lds_bytes, hipStream_t st) {
   constexpr int nt = 64 * WM * WN;
   if (arith == kBf16)
-    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, NTG, kBf16>), dim3(a.nwg), dim3(nt),
+    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, NTG, VEC, kBf16>), dim3(a.nwg), dim3(nt),
                        lds_bytes, st, a);
   else
-    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, NTG, kSplit3>), dim3(a.nwg), dim3(nt),
-                       lds_bytes, st, a);
+    hipLaunchKernelGGL((igemm_x3_kernel<MB, NB, WM, WN, NTG, VEC, kSplit3>), dim3(a.nwg),
+                       dim3(nt), lds_bytes, st, a);
+}
+
+template <int MB, int NB, int WM, int WN, int NTG>
+void launch_x3_ntg(const IgemmArgs& a, bool vec, int arith, size_t lds_bytes, hipStream_t st) {
+  if (vec)
+    launch_x3_vec<MB, NB, WM, WN, NTG, true>(a, arith, lds_bytes, st);
+  else
+    launch_x3_vec<MB, NB, WM, WN, NTG, false>(a, arith, lds_bytes, st);
 }
 
 // Profiled kernel-class name of a split-kernel launch: "<base>_m<M>n<N>", with "_bf16"
@@ -1070,7 +1117,8 @@ std::string x3_launch_name(const char* base, int arith, int m, int n) {
 }
 
 template <int MB, int NB, int WM, int WN>
-void launch_x3(const IgemmArgs& a, int arith, hipStream_t st, double flops, double bytes) {
+void launch_x3(const IgemmArgs& a, bool vec, int arith, hipStream_t st, double flops,
+               double bytes) {
   static const std::string names[2] = {
       x3_launch_name("conv3d_x3", kSplit3, 16 * MB * WM, 16 * NB * WN),
       x3_launch_name("conv3d_x3", kBf16, 16 * MB * WM, 16 * NB * WN)};
@@ -1081,11 +1129,11 @@ void launch_x3(const IgemmArgs& a, int arith, hipStream_t st, double flops, doub
   const size_t lds_bytes = halo_bytes > red_bytes ? halo_bytes : red_bytes;
   ProfScope prof(names[arith == kBf16].c_str(), flops, bytes, st);
   if (a.ntg == 7)
-    launch_x3_ntg<MB, NB, WM, WN, 7>(a, arith, lds_bytes, st);
+    launch_x3_ntg<MB, NB, WM, WN, 7>(a, vec, arith, lds_bytes, st);
   else if (a.ntg == 3)
-    launch_x3_ntg<MB, NB, WM, WN, 3>(a, arith, lds_bytes, st);
+    launch_x3_ntg<MB, NB, WM, WN, 3>(a, vec, arith, lds_bytes, st);
   else
-    launch_x3_ntg<MB, NB, WM, WN, 1>(a, arith, lds_bytes, st);
+    launch_x3_ntg<MB, NB, WM, WN, 1>(a, vec, arith, lds_bytes, st);
   launch_check("conv3d_x3");
 }
 
@@ -1969,8 +2017,18 @@ X3Plan plan_x3(const ConvGeom& g, int cout) {
     return p;
   } catch (const Error&) {
   }
-  p.v = cout <= 64 ? kX3F : kX3C;
-  p.box = choose_box(p.v, g, false, kX3MaxHalo);
+  // N 64 (weights preloaded a chunk at a time) up to 64 output channels, and wherever
+  // N 128 would leave fewer than 4 workgroups a CU; N 128 (half the halo staging per
+  // output channel) otherwise
+  p.v = kX3F;
+  p.box = choose_box(kX3F, g, false, kX3MaxHalo);
+  if (cout > 64) {
+    const Box wide = choose_box(kX3C, g, false, kX3MaxHalo);
+    if (g.batch * wide.tiles * ceil_div(cout, kX3C.n()) >= 1024) {
+      p.v = kX3C;
+      p.box = wide;
+    }
+  }
   p.staged = false;
   return p;
 }
@@ -2011,15 +2069,15 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
           "split convolution halo exceeds the staging");
   double flops, bytes;
   igemm_work(g, c1, c2, cout, &flops, &bytes);
+  const bool vec = c1 % kChunk == 0 && c2 % kChunk == 0;
   if (plan.staged) {
-    const bool vec = c1 % kChunk == 0 && c2 % kChunk == 0;
     launch_x3s<4, 2, 4, 1>(a, vec, arith, st, flops, bytes);
     return;
   }
   if (v.NB == 4)
-    launch_x3<2, 4, 2, 2>(a, arith, st, flops, bytes);
+    launch_x3<2, 4, 2, 2>(a, vec, arith, st, flops, bytes);
   else
-    launch_x3<2, 2, 2, 2>(a, arith, st, flops, bytes);
+    launch_x3<2, 2, 2, 2>(a, vec, arith, st, flops, bytes);
 }
 
 int conv_direct_stats_tiles(const int* size) {

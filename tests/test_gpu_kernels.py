@@ -50,6 +50,8 @@ CONV_CASES = [
     # 1 x 3 x 3 kernel
     (2, (9, 12, 10), 12, 20, 24, (3, 3, 3), (2, 2, 2)),
     (1, (6, 14, 13), 8, 0, 16, (1, 3, 3), (1, 2, 2)),
+    # strided with enough output tiles (1024 workgroups) for the 128-column split tiles
+    (2, (32, 64, 64), 16, 0, 256, (3, 3, 3), (2, 2, 2)),
 ]
 
 
