@@ -210,6 +210,16 @@ int nnx_conv3d_split(const float* d_x1, int c1, const float* d_x2, int c2, const
 int nnx_conv3d_direct_small_cin(const float* d_x, const float* d_weight /* (Cout,3,3,3,1) */,
                                 const float* d_bias, float* d_y, int batch, const int* size,
                                 int cout, void* stream);
+/* The same convolution with split-fp16 products on MFMA (the 27 taps of 16 voxels as one
+ * 16 x 32 fragment, hi*hi + hi*lo + lo*hi, float32 accumulation): weights times `scale`
+ * (nnx_split_weight_scale of max |w|), each 4 x 4 x 16 output tile's input times a power
+ * of two from the tile's own max |x|, products times the inverses (exact), + bias.
+ * Replaces the same reference call as nnx_conv3d_direct_small_cin in the fp32-split
+ * precision. */
+int nnx_conv3d_direct_small_cin_split(const float* d_x,
+                                      const float* d_weight /* (Cout,3,3,3,1) */, float scale,
+                                      const float* d_bias, float* d_y, int batch,
+                                      const int* size, int cout, void* stream);
 
 /* Stride==kernel ConvTranspose3d as one MFMA GEMM whose epilogue writes the interleaved
  * output directly (no transpose pass), + bias.

@@ -1194,55 +1194,34 @@ void launch_x3s(const IgemmArgs& a, bool vec, int arith, hipStream_t st, double 
 // ---------------------------------------------------------------------------------
 constexpr int kDirTz = 4, kDirTy = 8, kDirTx = 8;
 constexpr int kDirHz = kDirTz + 2, kDirHy = kDirTy + 2, kDirHx = kDirTx + 2;
+// tile of the split-product kernel (256 voxels, x fastest)
+constexpr int kDirX3Tz = 4, kDirX3Ty = 4, kDirX3Tx = 16;
+constexpr int kDirX3TilesPerBlock = 16;
 
-template <int COUT>
-__global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restrict__ x,
-                                                          const float* __restrict__ w,
-                                                          const float* __restrict__ bias,
-                                                          float* __restrict__ y, int D, int H,
-                                                          int W, int tiles_y, int tiles_x,
-                                                          float4* __restrict__ stats) {
-  typedef const __attribute__((address_space(4))) float* cfloat_p;
-  constexpr int cout = COUT;
-  constexpr int stride = cout + 1;  // padded output rows: no bank conflicts
-  __shared__ float halo[kDirHz * kDirHy * kDirHx];
-  __shared__ float red[256];
-  extern __shared__ float out_s[];  // 256 voxels x (cout + 1)
-  const cfloat_p wc = (cfloat_p)w;
-  const cfloat_p bc = (cfloat_p)bias;
-  const int tid = threadIdx.x;
-  const int tile = blockIdx.x;
-  const int txi = tile % tiles_x, tyi = (tile / tiles_x) % tiles_y, tzi = tile / (tiles_x * tiles_y);
-  const int z0 = tzi * kDirTz, y0 = tyi * kDirTy, x0 = txi * kDirTx;
-  const int64_t item = (int64_t)blockIdx.y * D * H * W;  // first voxel of the batch item
-  for (int i = tid; i < kDirHz * kDirHy * kDirHx; i += 256) {
+// the tile's 6 x 10 x 10 input halo (zeros outside the volume)
+__device__ __forceinline__ void direct_stage_halo(float* halo, const float* __restrict__ x,
+                                                  int64_t item, int D, int H, int W, int z0,
+                                                  int y0, int x0) {
+  for (int i = threadIdx.x; i < kDirHz * kDirHy * kDirHx; i += 256) {
     const int hz = i / (kDirHy * kDirHx), hy = (i / kDirHx) % kDirHy, hx = i % kDirHx;
     const int z = z0 + hz - 1, yy = y0 + hy - 1, xx = x0 + hx - 1;
     const bool inside = (unsigned)z < (unsigned)D && (unsigned)yy < (unsigned)H &&
                         (unsigned)xx < (unsigned)W;
     halo[i] = inside ? x[item + ((int64_t)z * H + yy) * W + xx] : 0.f;
   }
-  __syncthreads();
-  const int tz = tid >> 6, ty = (tid >> 3) & 7, tx = tid & 7;
-  {
-    float taps[27];
-#pragma unroll
-    for (int kd = 0; kd < 3; ++kd)
-#pragma unroll
-      for (int kh = 0; kh < 3; ++kh)
-#pragma unroll
-        for (int kw = 0; kw < 3; ++kw)
-          taps[(kd * 3 + kh) * 3 + kw] = halo[((tz + kd) * kDirHy + ty + kh) * kDirHx + tx + kw];
-    const bool has_bias = bias != nullptr;
-#pragma unroll
-    for (int c = 0; c < cout; ++c) {
-      float sum = 0.f;
-#pragma unroll
-      for (int t = 0; t < 27; ++t) sum = fmaf(taps[t], wc[c * 27 + t], sum);
-      out_s[tid * stride + c] = has_bias ? sum + bc[c] : sum;
-    }
-  }
-  __syncthreads();
+}
+
+// Stores the tile's outputs (staged in out_s, rows of cout + 1 floats) as contiguous runs,
+// then writes the tile's InstanceNorm partials when `stats` is set.  Call after a barrier
+// that follows the out_s writes.
+template <int COUT>
+__device__ __forceinline__ void direct_store_tile(const float* out_s, float* red,
+                                                  float* __restrict__ y, int64_t item, int D,
+                                                  int H, int W, int z0, int y0, int x0,
+                                                  float4* __restrict__ stats) {
+  constexpr int cout = COUT;
+  constexpr int stride = cout + 1;
+  const int tid = threadIdx.x;
   // rows (tz, ty) of up to 8 voxels: cout * nx contiguous floats each, one wave per row
   const int nx = W - x0 < kDirTx ? W - x0 : kDirTx;
   const int wave = tid >> 6, lane = tid & 63;
@@ -1292,6 +1271,274 @@ __global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restric
       for (int q = 0; q < parts; ++q) m2 += red[q * cout + c];
       stats[((int64_t)blockIdx.y * gridDim.x + blockIdx.x) * cout + c] =
           make_float4(mean, m2, (float)nv, 0.f);
+    }
+  }
+}
+
+template <int COUT>
+__global__ __launch_bounds__(256) void direct_cin1_kernel(const float* __restrict__ x,
+                                                          const float* __restrict__ w,
+                                                          const float* __restrict__ bias,
+                                                          float* __restrict__ y, int D, int H,
+                                                          int W, int tiles_y, int tiles_x,
+                                                          float4* __restrict__ stats) {
+  typedef const __attribute__((address_space(4))) float* cfloat_p;
+  constexpr int cout = COUT;
+  constexpr int stride = cout + 1;  // padded output rows: no bank conflicts
+  __shared__ float halo[kDirHz * kDirHy * kDirHx];
+  __shared__ float red[256];
+  extern __shared__ float out_s[];  // 256 voxels x (cout + 1)
+  const cfloat_p wc = (cfloat_p)w;
+  const cfloat_p bc = (cfloat_p)bias;
+  const int tid = threadIdx.x;
+  const int tile = blockIdx.x;
+  const int txi = tile % tiles_x, tyi = (tile / tiles_x) % tiles_y, tzi = tile / (tiles_x * tiles_y);
+  const int z0 = tzi * kDirTz, y0 = tyi * kDirTy, x0 = txi * kDirTx;
+  const int64_t item = (int64_t)blockIdx.y * D * H * W;  // first voxel of the batch item
+  direct_stage_halo(halo, x, item, D, H, W, z0, y0, x0);
+  __syncthreads();
+  const int tz = tid >> 6, ty = (tid >> 3) & 7, tx = tid & 7;
+  {
+    float taps[27];
+#pragma unroll
+    for (int kd = 0; kd < 3; ++kd)
+#pragma unroll
+      for (int kh = 0; kh < 3; ++kh)
+#pragma unroll
+        for (int kw = 0; kw < 3; ++kw)
+          taps[(kd * 3 + kh) * 3 + kw] = halo[((tz + kd) * kDirHy + ty + kh) * kDirHx + tx + kw];
+    const bool has_bias = bias != nullptr;
+#pragma unroll
+    for (int c = 0; c < cout; ++c) {
+      float sum = 0.f;
+#pragma unroll
+      for (int t = 0; t < 27; ++t) sum = fmaf(taps[t], wc[c * 27 + t], sum);
+      out_s[tid * stride + c] = has_bias ? sum + bc[c] : sum;
+    }
+  }
+  __syncthreads();
+  direct_store_tile<COUT>(out_s, red, y, item, D, H, W, z0, y0, x0, stats);
+}
+
+// power of two that brings max |v| into [2^14, 2^15), at most 2^100 so that its inverse
+// stays a normal float (1 for 0 or a non-finite maximum)
+__device__ __forceinline__ float split_scale_of(float max_abs) {
+  if (!(max_abs > 0.f) || !(max_abs <= 3.4e38f)) return 1.f;
+  int e;
+  frexpf(max_abs, &e);
+  return ldexpf(1.f, 15 - e < 100 ? 15 - e : 100);
+}
+
+// The same convolution with split-fp16 products on MFMA: the weights of 16 output
+// channels form one 16 x 32 A fragment (27 taps zero-padded to 32), the taps of 16 voxels
+// one 32 x 16 B fragment, hi*hi + hi*lo + lo*hi with float32 accumulation.  The raw input
+// has no normalised range, so each tile scales its halo by a power of two from the tile's
+// own max |x| (weights by `wscale`, a power of two from max |w|) before the split and the
+// products by the inverses (exact); + bias after.  Tiles of kDirX3Tz x kDirX3Ty x kDirX3Tx
+// = 256 voxels (x fastest); wave w computes voxels 64 w .. 64 w + 63 of the tile:
+// 4 blocks of 16 voxels x ceil(cout / 16) blocks of 16 channels.  A lane's accumulator
+// holds 4 consecutive channels of one voxel, stored as one 16-byte word; the tile's
+// InstanceNorm partials reduce the accumulators across lanes and waves (mean, then the
+// centred M2), so the outputs never pass through LDS.
+template <int COUT>
+__global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __restrict__ x,
+                                                             const float* __restrict__ w,
+                                                             float wscale,
+                                                             const float* __restrict__ bias,
+                                                             float* __restrict__ y, int D, int H,
+                                                             int W, int tiles_y, int tiles_x,
+                                                             int ntiles, int tpb,
+                                                             float4* __restrict__ stats) {
+  constexpr int cout = COUT;
+  constexpr int NB = (COUT + 15) / 16;
+  constexpr int MB = 4;
+  constexpr int TZ = kDirX3Tz, TY = kDirX3Ty, TX = kDirX3Tx;
+  constexpr int HY = TY + 2, HX = TX + 2;
+  constexpr int kHalo = (TZ + 2) * HY * HX;
+  constexpr int kLoads = (kHalo + 255) / 256;
+  __shared__ float halo[kHalo];
+  __shared__ float red[4][NB * 16];
+  __shared__ float wmax[4];
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int row = lane & 15, slot = lane >> 4;
+  const int64_t item = (int64_t)blockIdx.y * D * H * W;
+  const bool has_bias = bias != nullptr;
+
+  // A fragments: lane (n = 16 nb + row, k = 8 slot + q) holds wscale * W[n][k] split; bias
+  // of the lane's 4 output channels 16 nb + 4 slot + r
+  h8 A[NB][2];
+  f4 bn[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = nb * 16 + row;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int k = slot * 8 + q;
+      const float v = (n < cout && k < 27) ? w[n * 27 + k] * wscale : 0.f;
+      _Float16 hh, ll;
+      to_operand<kSplit3>(v, hh, ll);
+      A[nb][0][q] = hh;
+      A[nb][1][q] = ll;
+    }
+    const int n0 = nb * 16 + slot * 4;
+    bn[nb] = f4{0.f, 0.f, 0.f, 0.f};
+    if (has_bias && n0 < cout) bn[nb] = f4{bias[n0], bias[n0 + 1], bias[n0 + 2], bias[n0 + 3]};
+  }
+  const float inv_w = 1.f / wscale;
+
+  // tiles tpb * blockIdx.x .. of this batch item, one after the other; each tile's halo
+  // is loaded into registers while the previous tile computes
+  const int t_begin = blockIdx.x * tpb;
+  const int t_end = min(ntiles, t_begin + tpb);
+  float hv[kLoads];
+  auto load_halo = [&](int tile) {
+    const int txi = tile % tiles_x, tyi = (tile / tiles_x) % tiles_y, tzi = tile / (tiles_x * tiles_y);
+    const int z0 = tzi * TZ, y0 = tyi * TY, x0 = txi * TX;
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j) {
+      const int i = tid + 256 * j;
+      const int hz = i / (HY * HX), hy = (i / HX) % HY, hx = i % HX;
+      const int z = z0 + hz - 1, yy = y0 + hy - 1, xx = x0 + hx - 1;
+      const bool inside = i < kHalo && (unsigned)z < (unsigned)D && (unsigned)yy < (unsigned)H &&
+                          (unsigned)xx < (unsigned)W;
+      hv[j] = inside ? x[item + ((int64_t)z * H + yy) * W + xx] : 0.f;
+    }
+  };
+  if (t_begin < t_end) load_halo(t_begin);
+  for (int tile = t_begin; tile < t_end; ++tile) {
+    const int txi = tile % tiles_x, tyi = (tile / tiles_x) % tiles_y, tzi = tile / (tiles_x * tiles_y);
+    const int z0 = tzi * TZ, y0 = tyi * TY, x0 = txi * TX;
+    __syncthreads();  // the previous tile's halo, maxima and partials have been read
+    // publish the halo; tile maximum of |x| over it (zeros outside the volume) from the
+    // registers: per thread, per wave, then across the 4 waves
+    float mx = 0.f;
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j)
+      if (tid + 256 * j < kHalo) {
+        halo[tid + 256 * j] = hv[j];
+        mx = fmaxf(mx, fabsf(hv[j]));
+      }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
+    if (lane == 0) wmax[wave] = mx;
+    if (tile + 1 < t_end) load_halo(tile + 1);
+    __syncthreads();
+    const float xscale = split_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    // inverse scales, applied one after the other (exact powers of two; their product
+    // alone could leave the float range)
+    const float inv_x = 1.f / xscale;
+
+    f4 acc[MB][NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      // B fragment: lane (voxel v = 64 wave + 16 mb + row, taps 8 slot + q)
+      const int v = wave * 64 + mb * 16 + row;
+      const int base = ((v / (TX * TY)) * HY + (v / TX) % TY) * HX + v % TX;
+      h8 B[2];
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = slot * 8 + q;
+        const int off = k < 27 ? ((k / 9) * HY + (k / 3) % 3) * HX + k % 3 : 0;
+        const float hvq = k < 27 ? halo[base + off] * xscale : 0.f;
+        _Float16 hh, ll;
+        to_operand<kSplit3>(hvq, hh, ll);
+        B[0][q] = hh;
+        B[1][q] = ll;
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        acc[mb][nb] = mfma16x16x32h(A[nb][0], B[0], acc[mb][nb]);
+        acc[mb][nb] = mfma16x16x32h(A[nb][0], B[1], acc[mb][nb]);
+        acc[mb][nb] = mfma16x16x32h(A[nb][1], B[0], acc[mb][nb]);
+      }
+    }
+
+    // D[n][v]: lane holds channels 16 nb + 4 slot + r (r = 0..3) of voxel 16 mb + row
+    bool valid[MB];
+    int64_t vox[MB];  // output voxel index within the batch
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) {
+      const int v = wave * 64 + mb * 16 + row;
+      const int gz = z0 + v / (TX * TY), gy = y0 + (v / TX) % TY, gx = x0 + v % TX;
+      valid[mb] = gz < D && gy < H && gx < W;
+      vox[mb] = item + ((int64_t)gz * H + gy) * W + gx;
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int n0 = nb * 16 + slot * 4;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float t = (acc[mb][nb][r] * inv_x) * inv_w;
+          acc[mb][nb][r] = has_bias ? t + bn[nb][r] : t;
+        }
+        if (valid[mb] && n0 < cout) *reinterpret_cast<f4*>(y + vox[mb] * cout + n0) = acc[mb][nb];
+      }
+    }
+    if (!stats) continue;
+    // partials over the tile's voxels: per lane over its 4 row blocks, across the 16 lanes
+    // of its slot, then across the 4 waves
+    const int nz = D - z0 < TZ ? D - z0 : TZ, ny = H - y0 < TY ? H - y0 : TY;
+    const int nx = W - x0 < TX ? W - x0 : TX;
+    const int nv = nz * ny * nx;
+    auto reduce16 = [&](float v) {
+#pragma unroll
+      for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o);
+      return v;
+    };
+    float mean[NB][4];
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          if (valid[mb]) t += acc[mb][nb][r];
+        t = reduce16(t);
+        if (row == 0) red[wave][nb * 16 + slot * 4 + r] = t;
+      }
+    __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int n = nb * 16 + slot * 4 + r;
+        mean[nb][r] = (red[0][n] + red[1][n] + red[2][n] + red[3][n]) / (float)nv;
+      }
+    __syncthreads();
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        float t = 0.f;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          if (valid[mb]) {
+            const float d = acc[mb][nb][r] - mean[nb][r];
+            t = fmaf(d, d, t);
+          }
+        t = reduce16(t);
+        if (row == 0) red[wave][nb * 16 + slot * 4 + r] = t;
+      }
+    __syncthreads();
+    if (wave == 0 && row == 0) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int n = nb * 16 + slot * 4 + r;
+          if (n < cout)
+            stats[((int64_t)blockIdx.y * ntiles + tile) * cout + n] =
+                make_float4(mean[nb][r], red[0][n] + red[1][n] + red[2][n] + red[3][n],
+                            (float)nv, 0.f);
+        }
     }
   }
 }
@@ -2080,25 +2327,55 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
     launch_x3<2, 2, 2, 2>(a, vec, arith, st, flops, bytes);
 }
 
-int conv_direct_stats_tiles(const int* size) {
+int conv_direct_stats_tiles(const int* size, bool split) {
+  if (split)
+    return (int)(ceil_div(size[0], kDirX3Tz) * ceil_div(size[1], kDirX3Ty) *
+                 ceil_div(size[2], kDirX3Tx));
   return (int)(ceil_div(size[0], kDirTz) * ceil_div(size[1], kDirTy) * ceil_div(size[2], kDirTx));
 }
 
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
-                        const int* size, int cout, hipStream_t st, float4* stats) {
+                        const int* size, int cout, hipStream_t st, float4* stats, float wscale) {
   require(x && w && y, "convolution pointers must not be null");
   require(cout >= 4 && cout <= 64 && cout % 4 == 0,
           "one-channel direct convolution supports 4..64 outputs in steps of 4");
   require(batch >= 1 && batch <= 65535, "invalid convolution batch");
+  require(wscale == 0.f || (wscale > 0.f && std::isfinite(wscale)),
+          "weight scale must be positive (split products) or 0 (float32 products)");
   const int64_t S = (int64_t)size[0] * size[1] * size[2];
   require(S >= 1, "empty convolution input");
   const int64_t nvox = (int64_t)batch * S;
-  const int tiles_y = (int)ceil_div(size[1], kDirTy), tiles_x = (int)ceil_div(size[2], kDirTx);
-  const int64_t tiles = conv_direct_stats_tiles(size);
+  const bool split = wscale > 0.f;
+  const int tiles_y = (int)ceil_div(size[1], split ? kDirX3Ty : kDirTy);
+  const int tiles_x = (int)ceil_div(size[2], split ? kDirX3Tx : kDirTx);
+  const int64_t tiles = conv_direct_stats_tiles(size, split);
   require(tiles < (1LL << 31), "convolution volume too large");
-  ProfScope prof("conv3d_direct_cin1", 2.0 * 27 * cout * (double)nvox, 4.0 * (double)nvox * (1 + cout), st);
   const dim3 grid((unsigned)tiles, (unsigned)batch);
   const size_t lds = (size_t)256 * (cout + 1) * sizeof(float);
+  const double bytes = 4.0 * (double)nvox * (1 + cout);
+  if (split) {
+    // split products on MFMA: the output write bounds it (reported against HBM).  Each
+    // block takes kDirX3TilesPerBlock consecutive tiles (weights split once per block).
+    const int tpb = kDirX3TilesPerBlock;
+    const dim3 grid_x3((unsigned)ceil_div(tiles, tpb), (unsigned)batch);
+    ProfScope prof("conv3d_direct_cin1_x3", 0.0, bytes, st);
+    switch (cout / 4) {
+#define NNX_DIRECT_X3_CASE(Q)                                                                  \
+  case Q:                                                                                      \
+    hipLaunchKernelGGL(direct_cin1_x3_kernel<4 * Q>, grid_x3, dim3(256), 0, st, x, w, wscale,  \
+                       bias, y, size[0], size[1], size[2], tiles_y, tiles_x, (int)tiles, tpb,  \
+                       stats);                                                                 \
+    break;
+      NNX_DIRECT_X3_CASE(1) NNX_DIRECT_X3_CASE(2) NNX_DIRECT_X3_CASE(3) NNX_DIRECT_X3_CASE(4)
+      NNX_DIRECT_X3_CASE(5) NNX_DIRECT_X3_CASE(6) NNX_DIRECT_X3_CASE(7) NNX_DIRECT_X3_CASE(8)
+      NNX_DIRECT_X3_CASE(9) NNX_DIRECT_X3_CASE(10) NNX_DIRECT_X3_CASE(11) NNX_DIRECT_X3_CASE(12)
+      NNX_DIRECT_X3_CASE(13) NNX_DIRECT_X3_CASE(14) NNX_DIRECT_X3_CASE(15) NNX_DIRECT_X3_CASE(16)
+#undef NNX_DIRECT_X3_CASE
+    }
+    launch_check("conv3d_direct_small_cin_split");
+    return;
+  }
+  ProfScope prof("conv3d_direct_cin1", 2.0 * 27 * cout * (double)nvox, bytes, st);
   switch (cout / 4) {
 #define NNX_DIRECT_CASE(Q)                                                                     \
   case Q:                                                                                      \

@@ -152,9 +152,12 @@ int conv_x3_stats_tiles(const ConvGeom& g, int cout);
 // Whether the split kernel handles this kernel size / stride (tap count and halo size).
 bool conv_x3_supported(const int* ksize, const int* stride, int cout);
 // With `stats`: per-block InstanceNorm partials, conv_direct_stats_tiles(size) per item.
+// wscale 0: float32 fma products; wscale > 0 (split_weight_scale of max |w|): split-fp16
+// products on MFMA, each tile's input scaled by a power of two from its own max |x|.
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
-                        const int* size, int cout, hipStream_t st, float4* stats = nullptr);
-int conv_direct_stats_tiles(const int* size);
+                        const int* size, int cout, hipStream_t st, float4* stats = nullptr,
+                        float wscale = 0.f);
+int conv_direct_stats_tiles(const int* size, bool split = false);
 
 int64_t tconv_packed_floats(int cout, const int* ksize, int cin);
 void tconv_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float* d_packed,

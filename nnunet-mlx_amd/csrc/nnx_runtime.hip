@@ -341,7 +341,13 @@ bool uses_split_kernels(const nnx_model* m) {
 }
 
 void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
-  if (c.direct) return;  // the direct kernel reads the reference layout
+  if (c.direct) {
+    // the direct kernel reads the reference layout; split products in the fp32-split
+    // precision (the bf16 precision keeps float32 products for the first convolution)
+    c.split = m->precision == NNX_PRECISION_FP32_SPLIT;
+    c.scale = c.split ? split_weight_scale(m->params[c.pw].max_abs) : 0.f;
+    return;
+  }
   // Split-fp16 (or bf16) products for the hidden convolutions with >= 8 taps (a tap group
   // holds 4 taps; 1x1x1 convolutions would waste 3/4 of it).  The first convolution reads
   // the raw network input, whose range is not normalised, so it keeps float32 products.
@@ -416,13 +422,14 @@ struct Runner {
     if (c.direct) {
       // the direct kernel writes per-block statistics of its output
       require(!x1.norm.params, "the one-channel convolution reads the network input");
-      const int tiles = conv_direct_stats_tiles(in.d);
+      const int tiles = conv_direct_stats_tiles(in.d, c.split);
       if (plan->planning) {
         plan->stats = std::max(plan->stats, (size_t)n * tiles * c.cout * sizeof(float4));
         return result;
       }
       float4* stats = plan->ws->stats.as<float4>();
-      conv3d_direct_cin1(x1.data, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st, stats);
+      conv3d_direct_cin1(x1.data, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st, stats,
+                         c.split ? c.scale : 0.f);
       instnorm_merge_partials(stats, tiles, n, vox, c.cout, pdev(m, c.pg), pdev(m, c.pbeta),
                               m->eps, params, st);
       if (!defer)
@@ -1025,6 +1032,17 @@ int nnx_conv3d_direct_small_cin(const float* d_x, const float* d_weight, const f
   return guarded([&] {
     require(size != nullptr, "null argument");
     conv3d_direct_cin1(d_x, d_weight, d_bias, d_y, batch, size, cout, as_stream(stream));
+  });
+}
+
+int nnx_conv3d_direct_small_cin_split(const float* d_x, const float* d_weight, float scale,
+                                      const float* d_bias, float* d_y, int batch, const int* size,
+                                      int cout, void* stream) {
+  return guarded([&] {
+    require(size != nullptr, "null argument");
+    require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+    conv3d_direct_cin1(d_x, d_weight, d_bias, d_y, batch, size, cout, as_stream(stream), nullptr,
+                       scale);
   });
 }
 

@@ -141,6 +141,33 @@ def test_direct_single_channel_conv(lib, size, cout):
     assert rel_l2(got, ref) <= 1e-6, report("direct", got, ref)
 
 
+@pytest.mark.parametrize("size,cout,amplitude", [((16, 16, 16), 32, 1.0), ((5, 7, 9), 8, 1.0),
+                                                 ((9, 20, 11), 12, 3e4), ((4, 8, 8), 64, 1e-30)])
+def test_direct_single_channel_conv_split(lib, size, cout, amplitude):
+    """Split products on MFMA hold the float32 bar of the split kernels at any input range
+    (each tile scales its input by a power of two): raw CT-like magnitudes beyond the fp16
+    range, tiny values, and tiles mixing both."""
+    print(f"direct split conv {size} {cout} {amplitude}", flush=True)
+    rng = np.random.default_rng(11)
+    x = (rng.standard_normal((2, *size, 1)) * amplitude).astype(np.float32)
+    x[0, : size[0] // 2] *= 1e-3  # tiles whose values span three decades
+    w = (rng.standard_normal((cout, 3, 3, 3, 1)) * 0.3).astype(np.float32)
+    w.reshape(-1)[::5] *= 1e-3
+    b = (rng.standard_normal(cout) * amplitude * 0.1).astype(np.float32)
+    scale = lib.nnx_split_weight_scale(float(np.abs(w).max()))
+    y = torch.full((2, *size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    dx, dw, db = dev(x), dev(w), dev(b)
+    _native.check(lib.nnx_conv3d_direct_small_cin_split(
+        dx.data_ptr(), dw.data_ptr(), scale, db.data_ptr(), y.data_ptr(), 2,
+        _native.ints(size), cout, stream()))
+    got = host(y)
+    ref = _conv_ref64(x, w, (1, 1, 1)) + b.astype(np.float64)
+    msg = report("direct split", got, ref)
+    assert np.isfinite(got).all(), msg
+    assert rel_l2(got, ref) <= 1e-6, msg
+    assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), msg
+
+
 def _norm_ref64(x, in_bias, gamma, beta, eps, act, slope, residual):
     v = x.astype(np.float64)
     if in_bias is not None:
