@@ -1733,9 +1733,13 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
     for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
 
   for (int kb = 0; kb < a.cin; kb += kTcKBlock) {
-    __syncthreads();  // the previous block's fragments have been read
-    // rows m0.., channels kb..kb+63: 16 float4 lines per row
-    for (int i = tid; i < kTcRows * (kTcKBlock / 4); i += 256) {
+    // rows m0.., channels kb..kb+63: 16 float4 lines per row, 4 per thread, all requested
+    // before the barrier
+    constexpr int kLines = kTcRows * (kTcKBlock / 4) / 256;
+    f4 lines[kLines];
+#pragma unroll
+    for (int j = 0; j < kLines; ++j) {
+      const int i = tid + 256 * j;
       const int r = i >> 4, c4 = (i & 15) * 4;
       const int64_t m = m0 + r;
       const int c = kb + c4;
@@ -1750,6 +1754,14 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
             if (c + q < a.cin) v[q] = src[q];
         }
       }
+      lines[j] = v;
+    }
+    __syncthreads();  // the previous block's fragments have been read
+#pragma unroll
+    for (int j = 0; j < kLines; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i >> 4, c4 = (i & 15) * 4;
+      const f4 v = lines[j];
       h4 hv, lv;
 #pragma unroll
       for (int q = 0; q < 4; ++q) {
@@ -1832,6 +1844,19 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
       }
   }
   __syncthreads();
+  if (a.cout % 4 == 0) {
+    // 4 consecutive columns are 4 consecutive channels of one output voxel: 16-byte stores
+    for (int e4 = tid; e4 < kTcRows * kTcCols / 4; e4 += 256) {
+      const int r = e4 >> 5, cl = (e4 & 31) * 4;
+      const int64_t base = row_base[r];
+      const int off = col_off[cl];
+      if (base >= 0 && off >= 0) {
+        const float* t = tile + r * kTcTileStride + cl;
+        *reinterpret_cast<f4*>(a.y + base * a.cout + off) = f4{t[0], t[1], t[2], t[3]};
+      }
+    }
+    return;
+  }
   for (int e = tid; e < kTcRows * kTcCols; e += 256) {
     const int r = e >> 7, cl = e & (kTcCols - 1);
     const int64_t base = row_base[r];
