@@ -1704,13 +1704,16 @@ struct TcArgs {
   int kd, kh, kw;
   int id, ih, iw;
   int ntn, nwg;
+  int tpb;  // row tiles per workgroup
   float out_scale;
 };
 
 constexpr int kTcRows = 64, kTcCols = 128, kTcKBlock = 64, kTcRowHalves = kTcKBlock + 8;
 constexpr int kTcTileStride = kTcCols + 1;  // floats per staged output row
 
-template <int AR>
+// KREG > 0: the workgroup's weight fragments (at most KREG k-steps of 32 channels) are
+// loaded into registers once and serve all its row tiles; KREG = 0: read per k-step.
+template <int AR, int KREG>
 __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
   constexpr int MB = 4, NB = 2;
   extern __shared__ __align__(16) float lds[];
@@ -1723,146 +1726,166 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
   const int slot = lane >> 4;
   const int logical = xcd_remap(blockIdx.x, a.nwg);
   const int nt = logical % a.ntn;
-  const int64_t m0 = (int64_t)(logical / a.ntn) * kTcRows;
   const int blk0 = nt * (kTcCols / 16) + wave * NB;  // first 16-column block of this wave
-
-  f4 acc[MB][NB];
+  auto load_b = [&](h8 (&B)[NB][2], int kstep) {
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
-
-  for (int kb = 0; kb < a.cin; kb += kTcKBlock) {
-    // rows m0.., channels kb..kb+63: 16 float4 lines per row, 4 per thread, all requested
-    // before the barrier
-    constexpr int kLines = kTcRows * (kTcKBlock / 4) / 256;
-    f4 lines[kLines];
-#pragma unroll
-    for (int j = 0; j < kLines; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i >> 4, c4 = (i & 15) * 4;
-      const int64_t m = m0 + r;
-      const int c = kb + c4;
-      f4 v = {0.f, 0.f, 0.f, 0.f};
-      if (m < a.M) {
-        const float* src = a.x + m * a.cin + c;
-        if (c + 3 < a.cin) {
-          v = *reinterpret_cast<const f4*>(src);
-        } else {
-#pragma unroll
-          for (int q = 0; q < 4; ++q)
-            if (c + q < a.cin) v[q] = src[q];
-        }
+    for (int nb = 0; nb < NB; ++nb) {
+      const uint4* w = a.w16 + (((int64_t)kstep * a.nblk + blk0 + nb) * 2) * 64 + lane;
+      const uint4 wh = w[0];
+      B[nb][0] = *reinterpret_cast<const h8*>(&wh);
+      if constexpr (AR == kSplit3) {
+        const uint4 wl = w[64];
+        B[nb][1] = *reinterpret_cast<const h8*>(&wl);
       }
-      lines[j] = v;
     }
-    __syncthreads();  // the previous block's fragments have been read
+  };
+  h8 BR[KREG > 0 ? KREG : 1][NB][2];
+  if constexpr (KREG > 0) {
 #pragma unroll
-    for (int j = 0; j < kLines; ++j) {
-      const int i = tid + 256 * j;
-      const int r = i >> 4, c4 = (i & 15) * 4;
-      const f4 v = lines[j];
-      h4 hv, lv;
-#pragma unroll
-      for (int q = 0; q < 4; ++q) {
-        _Float16 hh, ll;
-        to_operand<AR>(v[q], hh, ll);
-        hv[q] = hh;
-        lv[q] = ll;
-      }
-      *reinterpret_cast<h4*>(hi + r * kTcRowHalves + c4) = hv;
-      if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo + r * kTcRowHalves + c4) = lv;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ks = 0; ks < kTcKBlock / 32; ++ks) {
-      const int kstep = kb / 32 + ks;
-      if (kstep >= a.ksteps) break;
-      h8 B[NB][2], A[MB][2];
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        const uint4* w = a.w16 + (((int64_t)kstep * a.nblk + blk0 + nb) * 2) * 64 + lane;
-        const uint4 wh = w[0];
-        B[nb][0] = *reinterpret_cast<const h8*>(&wh);
-        if constexpr (AR == kSplit3) {
-          const uint4 wl = w[64];
-          B[nb][1] = *reinterpret_cast<const h8*>(&wl);
-        }
-      }
-#pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
-        const int off = (mb * 16 + row) * kTcRowHalves + ks * 32 + slot * 8;
-        A[mb][0] = *reinterpret_cast<const h8*>(hi + off);
-        if constexpr (AR == kSplit3) A[mb][1] = *reinterpret_cast<const h8*>(lo + off);
-      }
-      mma_products<AR>(acc, A, B);
-    }
+    for (int ks = 0; ks < KREG; ++ks)
+      if (ks < a.ksteps) load_b(BR[ks], ks);
   }
 
-  // epilogue: tile T[r][c] (scaled, + bias) in LDS, then runs of contiguous channels
-  float* tile = lds;
-  int64_t* row_base = reinterpret_cast<int64_t*>(lds + kTcRows * kTcTileStride);
-  int* col_off = reinterpret_cast<int*>(row_base + kTcRows);
-  const int od = a.id * a.kd, oh = a.ih * a.kh, ow = a.iw * a.kw;
-  __syncthreads();  // the A planes are no longer read
-  if (tid < kTcRows) {
-    const int64_t m = m0 + tid;
-    int64_t base = -1;
-    if (m < a.M) {
-      const int xx = (int)(m % a.iw);
-      int64_t t = m / a.iw;
-      const int yy = (int)(t % a.ih);
-      t /= a.ih;
-      const int zz = (int)(t % a.id);
-      const int64_t bb = t / a.id;
-      base = ((bb * od + (int64_t)zz * a.kd) * oh + (int64_t)yy * a.kh) * ow + (int64_t)xx * a.kw;
-    }
-    row_base[tid] = base;
-  } else if (tid < kTcRows + kTcCols) {
-    const int cl = tid - kTcRows;
-    const int n = nt * kTcCols + cl;
-    int off = -1;
-    if (n < a.ncols) {
-      const int j = n / a.cout, o = n - j * a.cout;
-      const int ax = j % a.kw, ay = (j / a.kw) % a.kh, az = j / (a.kw * a.kh);
-      off = ((az * oh + ay) * ow + ax) * a.cout + o;
-    }
-    col_off[cl] = off;
-  }
-#pragma unroll
-  for (int nb = 0; nb < NB; ++nb) {
-    const int cl = (wave * NB + nb) * 16 + row;
-    const int n = nt * kTcCols + cl;
-    const float bias_n = (a.bias && n < a.ncols) ? a.bias[n % a.cout] : 0.f;
-    const bool has_bias = a.bias != nullptr;
+  // row tiles tpb * (logical / ntn) .. of column tile nt, one after the other
+  const int64_t t_begin = (int64_t)(logical / a.ntn) * a.tpb;
+  for (int64_t t = t_begin; t < t_begin + a.tpb; ++t) {
+    const int64_t m0 = t * kTcRows;
+    if (m0 >= a.M) break;
+    f4 acc[MB][NB];
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float v = acc[mb][nb][r] * a.out_scale;
-        tile[(mb * 16 + 4 * slot + r) * kTcTileStride + cl] = has_bias ? v + bias_n : v;
+      for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+
+    for (int kb = 0; kb < a.cin; kb += kTcKBlock) {
+      // rows m0.., channels kb..kb+63: 16 float4 lines per row, 4 per thread, all requested
+      // before the barrier
+      constexpr int kLines = kTcRows * (kTcKBlock / 4) / 256;
+      f4 lines[kLines];
+#pragma unroll
+      for (int j = 0; j < kLines; ++j) {
+        const int i = tid + 256 * j;
+        const int r = i >> 4, c4 = (i & 15) * 4;
+        const int64_t m = m0 + r;
+        const int c = kb + c4;
+        f4 v = {0.f, 0.f, 0.f, 0.f};
+        if (m < a.M) {
+          const float* src = a.x + m * a.cin + c;
+          if (c + 3 < a.cin) {
+            v = *reinterpret_cast<const f4*>(src);
+          } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+              if (c + q < a.cin) v[q] = src[q];
+          }
+        }
+        lines[j] = v;
       }
-  }
-  __syncthreads();
-  if (a.cout % 4 == 0) {
-    // 4 consecutive columns are 4 consecutive channels of one output voxel: 16-byte stores
-    for (int e4 = tid; e4 < kTcRows * kTcCols / 4; e4 += 256) {
-      const int r = e4 >> 5, cl = (e4 & 31) * 4;
-      const int64_t base = row_base[r];
-      const int off = col_off[cl];
-      if (base >= 0 && off >= 0) {
-        const float* t = tile + r * kTcTileStride + cl;
-        *reinterpret_cast<f4*>(a.y + base * a.cout + off) = f4{t[0], t[1], t[2], t[3]};
+      __syncthreads();  // the previous block's fragments have been read
+#pragma unroll
+      for (int j = 0; j < kLines; ++j) {
+        const int i = tid + 256 * j;
+        const int r = i >> 4, c4 = (i & 15) * 4;
+        const f4 v = lines[j];
+        h4 hv, lv;
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          _Float16 hh, ll;
+          to_operand<AR>(v[q], hh, ll);
+          hv[q] = hh;
+          lv[q] = ll;
+        }
+        *reinterpret_cast<h4*>(hi + r * kTcRowHalves + c4) = hv;
+        if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo + r * kTcRowHalves + c4) = lv;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < kTcKBlock / 32; ++ks) {
+        const int kstep = kb / 32 + ks;
+        if (kstep >= a.ksteps) break;
+        h8 A[MB][2];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) {
+          const int off = (mb * 16 + row) * kTcRowHalves + ks * 32 + slot * 8;
+          A[mb][0] = *reinterpret_cast<const h8*>(hi + off);
+          if constexpr (AR == kSplit3) A[mb][1] = *reinterpret_cast<const h8*>(lo + off);
+        }
+        if constexpr (KREG > 0) {
+          // k-steps kb / 32 + ks < ksteps <= KREG
+          mma_products<AR>(acc, A, BR[kb / 32 + ks < KREG ? kb / 32 + ks : 0]);
+        } else {
+          h8 B[NB][2];
+          load_b(B, kstep);
+          mma_products<AR>(acc, A, B);
+        }
       }
     }
-    return;
-  }
-  for (int e = tid; e < kTcRows * kTcCols; e += 256) {
-    const int r = e >> 7, cl = e & (kTcCols - 1);
-    const int64_t base = row_base[r];
-    const int off = col_off[cl];
-    if (base >= 0 && off >= 0) a.y[base * a.cout + off] = tile[r * kTcTileStride + cl];
-  }
+
+    // epilogue: tile T[r][c] (scaled, + bias) in LDS, then runs of contiguous channels
+    float* tile = lds;
+    int64_t* row_base = reinterpret_cast<int64_t*>(lds + kTcRows * kTcTileStride);
+    int* col_off = reinterpret_cast<int*>(row_base + kTcRows);
+    const int od = a.id * a.kd, oh = a.ih * a.kh, ow = a.iw * a.kw;
+    __syncthreads();  // the A planes are no longer read
+    if (tid < kTcRows) {
+      const int64_t m = m0 + tid;
+      int64_t base = -1;
+      if (m < a.M) {
+        const int xx = (int)(m % a.iw);
+        int64_t t = m / a.iw;
+        const int yy = (int)(t % a.ih);
+        t /= a.ih;
+        const int zz = (int)(t % a.id);
+        const int64_t bb = t / a.id;
+        base = ((bb * od + (int64_t)zz * a.kd) * oh + (int64_t)yy * a.kh) * ow + (int64_t)xx * a.kw;
+      }
+      row_base[tid] = base;
+    } else if (tid < kTcRows + kTcCols) {
+      const int cl = tid - kTcRows;
+      const int n = nt * kTcCols + cl;
+      int off = -1;
+      if (n < a.ncols) {
+        const int j = n / a.cout, o = n - j * a.cout;
+        const int ax = j % a.kw, ay = (j / a.kw) % a.kh, az = j / (a.kw * a.kh);
+        off = ((az * oh + ay) * ow + ax) * a.cout + o;
+      }
+      col_off[cl] = off;
+    }
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) {
+      const int cl = (wave * NB + nb) * 16 + row;
+      const int n = nt * kTcCols + cl;
+      const float bias_n = (a.bias && n < a.ncols) ? a.bias[n % a.cout] : 0.f;
+      const bool has_bias = a.bias != nullptr;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float v = acc[mb][nb][r] * a.out_scale;
+          tile[(mb * 16 + 4 * slot + r) * kTcTileStride + cl] = has_bias ? v + bias_n : v;
+        }
+    }
+    __syncthreads();
+    if (a.cout % 4 == 0) {
+      // 4 consecutive columns are 4 consecutive channels of one output voxel: 16-byte stores
+      for (int e4 = tid; e4 < kTcRows * kTcCols / 4; e4 += 256) {
+        const int r = e4 >> 5, cl = (e4 & 31) * 4;
+        const int64_t base = row_base[r];
+        const int off = col_off[cl];
+        if (base >= 0 && off >= 0) {
+          const float* tv = tile + r * kTcTileStride + cl;
+          *reinterpret_cast<f4*>(a.y + base * a.cout + off) = f4{tv[0], tv[1], tv[2], tv[3]};
+        }
+      }
+    } else {
+      for (int e = tid; e < kTcRows * kTcCols; e += 256) {
+        const int r = e >> 7, cl = e & (kTcCols - 1);
+        const int64_t base = row_base[r];
+        const int off = col_off[cl];
+        if (base >= 0 && off >= 0) a.y[base * a.cout + off] = tile[r * kTcTileStride + cl];
+      }
+    }
+  }  // row tiles
 }
 
 // Packing: words ((kstep * nblk + nb) * 2 + part) * 64 + lane = part 0: hi, part 1: lo h8 of
@@ -2521,17 +2544,25 @@ void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const 
   require(ovox * cout < (1LL << 31), "transposed-convolution output item too large");
   a.ntn = (int)ceil_div(a.ncols, kTcCols);
   require(a.nblk >= a.ntn * (kTcCols / 16), "transposed-convolution packing too small");
-  const int64_t nwg = ceil_div(a.M, kTcRows) * a.ntn;
+  // row tiles per workgroup: up to 16 while the grid keeps >= 2048 workgroups
+  const int64_t mtiles = ceil_div(a.M, kTcRows);
+  a.tpb = (int)std::max<int64_t>(1, std::min<int64_t>(16, mtiles * a.ntn / 2048));
+  const int64_t nwg = ceil_div(mtiles, a.tpb) * a.ntn;
   require(nwg < (1LL << 31), "transposed-convolution grid too large");
   a.nwg = (int)nwg;
   const size_t lds_bytes = (size_t)kTcRows * kTcTileStride * 4 + kTcRows * 8 + kTcCols * 4;
   ProfScope prof(arith == kBf16 ? "tconv3d_x3_bf16" : "tconv3d_x3",
                  2.0 * (double)a.M * cin * a.ncols,
                  4.0 * ((double)a.M * (cin + a.ncols) + (double)cin * a.ncols), st);
+  // weights held in registers for up to 2 k-steps (C_in <= 64); more would cost occupancy
+  const bool kreg = a.ksteps <= 2;
+  auto launch = [&](auto kernel) {
+    hipLaunchKernelGGL(kernel, dim3(a.nwg), dim3(256), lds_bytes, st, a);
+  };
   if (arith == kBf16)
-    hipLaunchKernelGGL(tconv_x3_kernel<kBf16>, dim3(a.nwg), dim3(256), lds_bytes, st, a);
+    kreg ? launch(tconv_x3_kernel<kBf16, 2>) : launch(tconv_x3_kernel<kBf16, 0>);
   else
-    hipLaunchKernelGGL(tconv_x3_kernel<kSplit3>, dim3(a.nwg), dim3(256), lds_bytes, st, a);
+    kreg ? launch(tconv_x3_kernel<kSplit3, 2>) : launch(tconv_x3_kernel<kSplit3, 0>);
   launch_check("tconv3d_split");
 }
 

@@ -193,8 +193,8 @@ void instnorm_params(const float* x, int batch, int64_t spatial, int channels,
                      const float* input_bias, const float* gamma, const float* beta, float eps,
                      void* ws, size_t ws_bytes, float4* params, hipStream_t st);
 // The same parameters from per-tile partials (mean, M2, n, 0) written by a convolution
-// epilogue.
-void instnorm_merge_partials(const float4* partials, int nparts, int batch, int64_t spatial,
+// epilogue.  The partials are consumed: the merge overwrites them.
+void instnorm_merge_partials(float4* partials, int nparts, int batch, int64_t spatial,
                              int channels, const float* gamma, const float* beta, float eps,
                              float4* params, hipStream_t st);
 // y = LeakyReLU?(fma(x + input_bias - mean, scale, beta) (+ residual)), elementwise.

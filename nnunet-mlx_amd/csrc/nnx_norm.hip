@@ -180,43 +180,122 @@ __global__ __launch_bounds__(256) void norm_merge_kernel(const float2* __restric
 }
 
 // Same merge for partials that carry their own counts (per-tile partials written by the
-// convolution epilogue: (mean, M2, n, 0)).
-__global__ __launch_bounds__(256) void norm_merge_counted_kernel(const float4* __restrict__ partial,
-                                                                 float4* __restrict__ params,
-                                                                 const float* __restrict__ beta,
-                                                                 const float* __restrict__ gamma,
-                                                                 int64_t S, int C, int nparts,
-                                                                 float eps) {
+// convolution epilogue: (mean, M2, n, 0) at partial[(b * nparts + i) * C + c]), in two passes.
+// Pass 1: block (j, b) merges rows [j * per, (j + 1) * per) of item b; a thread takes
+// channel cb + t % CB of every G-th row (CB = min(C, 256) channels a pass, G = 256 / CB
+// row groups), so each row is read as one contiguous run; the groups are merged through
+// LDS, and the slice's (mean, M2) in float64 and its count are written over the slice's
+// own first two rows (read by this block only, and no longer needed).
+__global__ __launch_bounds__(256) void norm_merge_slices_kernel(float4* __restrict__ partial, int C,
+                                                                int nparts, int per) {
   __shared__ double sn[256], sm[256], s2[256];
-  const int c = blockIdx.x;
-  const int b = blockIdx.y;
-  double n = 0.0, m = 0.0, m2 = 0.0;
-  for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
-    const float4 p = partial[((int64_t)b * nparts + i) * C + c];
-    chan_merge(n, m, m2, (double)p.z, (double)p.x, (double)p.y);
-  }
-  sn[threadIdx.x] = n;
-  sm[threadIdx.x] = m;
-  s2[threadIdx.x] = m2;
-  __syncthreads();
-  for (int stride = blockDim.x / 2; stride > 0; stride >>= 1) {
-    if ((int)threadIdx.x < stride) {
-      double na = sn[threadIdx.x], ma = sm[threadIdx.x], m2a = s2[threadIdx.x];
-      chan_merge(na, ma, m2a, sn[threadIdx.x + stride], sm[threadIdx.x + stride],
-                 s2[threadIdx.x + stride]);
-      sn[threadIdx.x] = na;
-      sm[threadIdx.x] = ma;
-      s2[threadIdx.x] = m2a;
+  const int j = blockIdx.x, b = blockIdx.y;
+  const int t = threadIdx.x;
+  const int CB = C < 256 ? C : 256;
+  const int G = 256 / CB;
+  const int g = t / CB;
+  const int r0 = j * per;
+  const int r1 = r0 + per < nparts ? r0 + per : nparts;
+  float4* rows = partial + (int64_t)b * nparts * C;
+  // (mean, M2) as a double pair and the count, per channel of this pass
+  double res_m[2], res_2[2];
+  float res_n[2];
+  int npass = 0;
+  for (int cb = 0; cb < C; cb += CB, ++npass) {
+    const int c = cb + t % CB;
+    const bool active = g < G && c < C;
+    double n = 0.0, m = 0.0, m2 = 0.0;
+    if (active) {
+      int r = r0 + g;
+      // four rows in flight per step
+      for (; r + 3 * G < r1; r += 4 * G) {
+        float4 p[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) p[q] = rows[(int64_t)(r + q * G) * C + c];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) chan_merge(n, m, m2, (double)p[q].z, (double)p[q].x, (double)p[q].y);
+      }
+      for (; r < r1; r += G) {
+        const float4 p = rows[(int64_t)r * C + c];
+        chan_merge(n, m, m2, (double)p.z, (double)p.x, (double)p.y);
+      }
+    }
+    sn[t] = n;
+    sm[t] = m;
+    s2[t] = m2;
+    __syncthreads();
+    // groups g = 1 .. G-1 into group 0, one thread per channel
+    if (t < CB) {
+      double na = sn[t], ma = sm[t], m2a = s2[t];
+      for (int q = 1; q < G; ++q) chan_merge(na, ma, m2a, sn[q * CB + t], sm[q * CB + t], s2[q * CB + t]);
+      if (npass < 2) {
+        res_m[npass] = ma;
+        res_2[npass] = m2a;
+        res_n[npass] = (float)na;
+      }
     }
     __syncthreads();
   }
-  if (threadIdx.x == 0) {
-    const double var = s2[0] / (double)S;
-    float varf = (float)(var > 0.0 ? var : 0.0);
-    float scale = 1.0f / sqrtf(varf + eps);
-    if (gamma) scale = gamma[c] * scale;
-    params[(int64_t)b * C + c] = make_float4((float)sm[0], scale, beta ? beta[c] : 0.f, 0.f);
+  // every read of the slice is done: row r0 holds (mean, M2) as doubles, row r0 + 1 the count
+  if (t < CB) {
+    for (int q = 0; q < npass && q < 2; ++q) {
+      const int c = q * CB + t;
+      if (c < C) {
+        double2* out = reinterpret_cast<double2*>(rows + (int64_t)r0 * C + c);
+        *out = make_double2(res_m[q], res_2[q]);
+        rows[(int64_t)(r0 + 1) * C + c] = make_float4(res_n[q], 0.f, 0.f, 0.f);
+      }
+    }
   }
+}
+
+// Pass 2: one thread per (b, c) merges the slices' results in slice order.  With `raw`
+// (at most 64 partial rows: no pass 1) it merges the partial rows themselves.
+__global__ __launch_bounds__(64) void norm_merge_final_kernel(const float4* __restrict__ partial,
+                                                              float4* __restrict__ params,
+                                                              const float* __restrict__ beta,
+                                                              const float* __restrict__ gamma,
+                                                              int64_t S, int C, int nparts,
+                                                              int per, int nslices, int raw,
+                                                              float eps) {
+  const int c = blockIdx.x * 64 + threadIdx.x;
+  const int b = blockIdx.y;
+  if (c >= C) return;
+  const float4* rows = partial + (int64_t)b * nparts * C;
+  double n = 0.0, m = 0.0, m2 = 0.0;
+  // eight entries requested per step, then merged in order
+  const int count = raw ? nparts : nslices;
+  for (int j0 = 0; j0 < count; j0 += 8) {
+    double en[8], em[8], e2[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int j = j0 + q;
+      en[q] = 0.0;
+      em[q] = 0.0;
+      e2[q] = 0.0;
+      if (j < count) {
+        if (raw) {
+          const float4 p = rows[(int64_t)j * C + c];
+          en[q] = p.z;
+          em[q] = p.x;
+          e2[q] = p.y;
+        } else {
+          const int64_t r0 = (int64_t)j * per;
+          const double2 mv = *reinterpret_cast<const double2*>(rows + r0 * C + c);
+          en[q] = rows[(r0 + 1) * C + c].x;
+          em[q] = mv.x;
+          e2[q] = mv.y;
+        }
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; ++q) chan_merge(n, m, m2, en[q], em[q], e2[q]);
+  }
+  const double var = m2 / (double)S;
+  float varf = (float)(var > 0.0 ? var : 0.0);
+  float scale = 1.0f / sqrtf(varf + eps);
+  if (gamma) scale = gamma[c] * scale;
+  params[(int64_t)b * C + c] = make_float4((float)m, scale, beta ? beta[c] : 0.f, 0.f);
 }
 
 template <int VW>
@@ -420,14 +499,30 @@ void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int ch
                         st);
 }
 
-void instnorm_merge_partials(const float4* partials, int nparts, int batch, int64_t spatial,
+void instnorm_merge_partials(float4* partials, int nparts, int batch, int64_t spatial,
                              int channels, const float* gamma, const float* beta, float eps,
                              float4* params, hipStream_t st) {
   require(partials && params, "instance normalisation partials must not be null");
-  require(nparts >= 1 && batch >= 1 && batch <= 65535 && channels >= 1, "invalid partial layout");
+  require(nparts >= 1 && batch >= 1 && batch <= 65535 && channels >= 1 && channels <= 512,
+          "invalid partial layout");
   ProfScope prof("instnorm_merge", 0.0, 16.0 * (double)batch * nparts * channels, st);
-  hipLaunchKernelGGL(norm_merge_counted_kernel, dim3(channels, batch), dim3(256), 0, st, partials,
-                     params, beta, gamma, spatial, channels, nparts, eps);
+  const dim3 fgrid((unsigned)ceil_div(channels, 64), batch);
+  if (nparts <= 64) {
+    hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(64), 0, st, partials, params, beta,
+                       gamma, spatial, channels, nparts, 1, nparts, 1, eps);
+    launch_check("instnorm merge partials");
+    return;
+  }
+  // slices of >= 2 rows (a slice's result takes its first two rows), ~2048 blocks in all
+  int nslices = (int)std::min<int64_t>(ceil_div(2048, batch), nparts / 2);
+  if (nslices < 1) nslices = 1;
+  const int per = (int)ceil_div(nparts, nslices);
+  nslices = (int)ceil_div(nparts, per);
+  hipLaunchKernelGGL(norm_merge_slices_kernel, dim3(nslices, batch), dim3(256), 0, st, partials,
+                     channels, nparts, per);
+  launch_check("instnorm merge slices");
+  hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(64), 0, st, partials, params, beta,
+                     gamma, spatial, channels, nparts, per, nslices, 0, eps);
   launch_check("instnorm merge partials");
 }
 
