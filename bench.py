@@ -95,7 +95,7 @@ def kernel_class_of(short: str) -> str | None:
     return f"{prefix}_m{16 * mb * wm}n{16 * nb * wn}"
 
 
-TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_liver_tile.md"
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_liver_case.md"
 
 
 def summarize_profiles(directory: str) -> None:
@@ -145,14 +145,14 @@ def summarize_profiles(directory: str) -> None:
         a[1] += v.get("FETCH_SIZE", 0.0) * fetch_factor * 1024
         a[2] += v.get("WRITE_SIZE", 0.0) * write_factor * 1024
     lines = [
-        "# HBM traffic per launch, one liver tile (8 views of 128^3) through the forward",
+        "# HBM traffic per launch, liver-shape case (121 tiles x 8 views, 32 views a forward batch)",
         "",
         "Commands (repo root on the MI355X box), one counter per run:",
         "",
         "    rocprofv3 --pmc FETCH_SIZE -f csv -d gpurun_out/prof_fetch -o fetch -- \\",
-        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt --copy-calibration",
+        "        python -u bench.py --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt --copy-calibration",
         "    rocprofv3 --pmc WRITE_SIZE -f csv -d gpurun_out/prof_write -o write -- \\",
-        "        python -u bench.py --shape 101 128 128 --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt --copy-calibration",
+        "        python -u bench.py --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt --copy-calibration",
         "",
         f"Calibration: torch.neg over 1 GiB (reads 1 GiB, writes 1 GiB) reads FETCH_SIZE = "
         f"{neg['FETCH_SIZE']:.0f} KiB and WRITE_SIZE = {neg['WRITE_SIZE']:.0f} KiB, so FETCH_SIZE is "
