@@ -272,6 +272,40 @@ int nnx_tconv3d_bf16(const float* d_x, int cin, const void* d_packed, float scal
 int nnx_restore_labels(const void* d_logits, int half, int classes, const int* src_shape,
                        const int* dst_shape, uint16_t* d_labels, void* stream);
 
+/* Raw-case preprocessing on the device (volumes are (C, X, Y, Z) float32, Z fastest, in
+ * the array axis order of the raw image).
+ *
+ * nnx_nonzero_bbox: d_bbox[2a], d_bbox[2a + 1] = first and last index along axis a of a
+ * voxel where any channel is nonzero (INT_MAX and -1 when there is none); the crop of
+ * crop_to_nonzero without a mask (src/nnunet_mlx/data/preprocessing.py:166-214).
+ *
+ * nnx_crop_normalize: out (C, o0, o1, o2) with out axis k = input axis transpose[k] from
+ * start[k] (out-axis order), each channel normalised by schemes[c]: NNX_NORM_NONE copies,
+ * NNX_NORM_CT clips to [lower, upper] then (x - mean) / max(std, 1e-8) in float32, with
+ * norm[4c..4c+3] = (mean, std, lower, upper); at most 16 channels.  Replaces the transpose
+ * and crop of preprocess_raw_case and the CTNormalization / NoNormalization branches of
+ * _normalize_channel (src/nnunet_mlx/data/preprocessing.py:100-128, 263-289).
+ *
+ * nnx_resample_spline: scikit-image resize(order, mode="edge", anti_aliasing=False) of each
+ * channel to new_size (SciPy zoom in grid mode with edge extension, float64, clipped to the
+ * input's [min, max]), order 1 or 3; with separate_axis in 0..2 the other two axes are
+ * resized plane by plane (clipped per plane, float64) and separate_axis by half-pixel
+ * nearest indices (order_z 0), rounded to float32 once.  The caller passes a device
+ * workspace of nnx_resample_spline_workspace bytes.  Replaces resample_probabilities_or_data
+ * for spline plans (src/nnunet_mlx/data/resampling.py:87-172, 268-306, 379-442, 476-501). */
+#define NNX_NORM_NONE 0
+#define NNX_NORM_CT 1
+int nnx_nonzero_bbox(const float* d_data, int channels, const int64_t* size, int* d_bbox,
+                     void* stream);
+int nnx_crop_normalize(const float* d_data, int channels, const int64_t* size,
+                       const int* transpose, const int64_t* start, const int64_t* out_size,
+                       const int* schemes, const float* norm, float* d_out, void* stream);
+size_t nnx_resample_spline_workspace(const int64_t* size, const int64_t* new_size,
+                                     int separate_axis);
+int nnx_resample_spline(const float* d_data, int channels, const int64_t* size,
+                        const int64_t* new_size, int order, int separate_axis, int order_z,
+                        void* d_work, size_t work_bytes, float* d_out, void* stream);
+
 /* 1x1x1 convolution with bias (segmentation head), NDHWC.
  * Replaces seg{n-1} (src/nnunet_mlx/model/network.py:804-808,875-876). */
 int nnx_conv1x1(const float* d_x, int cin, const float* d_weight /* (Cout,1,1,1,Cin) */,

@@ -177,6 +177,15 @@ void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const 
 // float16 before the comparison.
 void restore_labels(const void* logits, bool half, int classes, const int* src, const int* dst,
                     uint16_t* labels, hipStream_t st);
+// Raw-case preprocessing (nnx_preprocess.hip).
+void nonzero_bbox(const float* x, int channels, const int64_t* size, int* bbox, hipStream_t st);
+void crop_normalize(const float* x, int channels, const int64_t* size, const int* transpose,
+                    const int64_t* start, const int64_t* out_size, const int* schemes,
+                    const float* norm, float* out, hipStream_t st);
+size_t resample_spline_workspace(const int64_t* size, const int64_t* new_size, int separate_axis);
+void resample_spline(const float* x, int channels, const int64_t* size, const int64_t* new_size,
+                     int order, int separate_axis, int order_z, void* work, size_t work_bytes,
+                     float* out, hipStream_t st);
 // `item_voxels` = voxels per batch item (to index the pending norm's parameters).
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y,
              int64_t voxels, int cout, hipStream_t st, const PendingNorm& nx = {},

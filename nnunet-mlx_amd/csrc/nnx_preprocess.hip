@@ -1,0 +1,482 @@
+// Raw-case preprocessing on the device: nonzero crop bounds, crop + transpose + per-channel
+// normalisation, and the spline resampling of image data to the plans' spacing.
+//
+// Replaces the host steps of preprocess_raw_case (src/nnunet_mlx/data/preprocessing.py:63-163):
+// the crop bounds of crop_to_nonzero (:166-214; no mask, as CT normalisation uses none),
+// the CTNormalization branch of _normalize_channel (:274-285), and the data resize of
+// resample_probabilities_or_data for spline plans (src/nnunet_mlx/data/resampling.py:87-172,
+// 268-306, 379-442, 476-501), which the reference delegates to scikit-image's
+// resize(order, mode="edge", anti_aliasing=False): scipy.ndimage.zoom in grid mode with
+// edge extension, then a clip to the input's [min, max].
+//
+// Spline arithmetic (float64 throughout, no contraction):
+//   * pad every resized axis by 12 voxels with edge replication (SciPy pads this way before
+//     building coefficients for edge extension);
+//   * order 3: per axis in turn, per line: multiply by the gain (1 - z)(1 - 1/z), causal
+//     initialisation for edge extension c0' = (c0 + z^n c[n-1] + sum_{i=1}^{n-1} z^i (c[i] +
+//     z^n c[n-1-i])) * z / (1 - z^2n) + c0, causal recursion c[i] += z c[i-1], anticausal
+//     initialisation c[n-1] *= z / (z - 1), anticausal recursion c[i] = z (c[i+1] - c[i]),
+//     pole z = sqrt(3) - 2;
+//   * evaluation one axis at a time: output index o samples the padded coordinate
+//     cc = (o + 0.5) * n_in / n_out - 0.5 + 12 with the cardinal cubic B-spline weights of
+//     t = cc - floor(cc) at floor(cc) - 1 .. floor(cc) + 2 (order 1: 1 - t, t at floor(cc),
+//     floor(cc) + 1), summed from 0 in tap order;
+//   * whole volume: cast to float32, clip to the channel's input [min, max]; separate axis:
+//     the other two axes resized per plane (float64, clipped to the plane's [min, max]),
+//     then the separate axis by half-pixel nearest indices floor(old/new (o + 0.5) - 0.5 +
+//     0.5) clamped, cast to float32 once.
+// Roofline: HBM — each pass reads and writes its float64 array once (the prefilter walks
+// each line twice); the crop/normalise pass reads and writes 4 B per kept voxel.
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <cmath>
+#include <cstdint>
+
+#include "nnx_internal.h"
+
+namespace nnx {
+namespace {
+
+constexpr int kSplinePad = 12;
+
+// ---- nonzero bounds -------------------------------------------------------------------
+
+__global__ void bbox_init_kernel(int* bbox) {
+  if (threadIdx.x < 3) {
+    bbox[2 * threadIdx.x] = INT_MAX;
+    bbox[2 * threadIdx.x + 1] = -1;
+  }
+}
+
+// bbox[2a] / bbox[2a + 1] = smallest / largest index along axis a of a voxel where any
+// channel is nonzero.  Block minima and maxima reach memory by one vector atomic each.
+__global__ __launch_bounds__(256) void bbox_kernel(const float* __restrict__ x, int C, int64_t X,
+                                                   int64_t Y, int64_t Z, int* bbox) {
+  __shared__ int red[6][4];
+  int lo[3] = {INT_MAX, INT_MAX, INT_MAX}, hi[3] = {-1, -1, -1};
+  const int64_t n = X * Y * Z;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    bool nz = false;
+    for (int c = 0; c < C; ++c) nz |= x[(int64_t)c * n + i] != 0.f;
+    if (nz) {
+      const int idx[3] = {(int)(i / (Y * Z)), (int)((i / Z) % Y), (int)(i % Z)};
+#pragma unroll
+      for (int a = 0; a < 3; ++a) {
+        lo[a] = min(lo[a], idx[a]);
+        hi[a] = max(hi[a], idx[a]);
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1)
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      lo[a] = min(lo[a], __shfl_xor(lo[a], o));
+      hi[a] = max(hi[a], __shfl_xor(hi[a], o));
+    }
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  if (lane == 0)
+#pragma unroll
+    for (int a = 0; a < 3; ++a) {
+      red[2 * a][wave] = lo[a];
+      red[2 * a + 1][wave] = hi[a];
+    }
+  __syncthreads();
+  if (threadIdx.x < 6) {
+    const int k = threadIdx.x;
+    int v = red[k][0];
+    for (int w = 1; w < 4; ++w) v = (k & 1) ? max(v, red[k][w]) : min(v, red[k][w]);
+    if (k & 1) {
+      if (v >= 0) atomicMax(&bbox[k], v);
+    } else if (v != INT_MAX) {
+      atomicMin(&bbox[k], v);
+    }
+  }
+}
+
+// ---- crop + transpose + normalise -------------------------------------------------------
+
+constexpr int kMaxNormChannels = 16;
+
+struct ChannelNorms {
+  int scheme[kMaxNormChannels];  // NNX_NORM_*
+  float mean[kMaxNormChannels], std[kMaxNormChannels];  // std already max(std, 1e-8)
+  float lower[kMaxNormChannels], upper[kMaxNormChannels];
+};
+
+// out[c][o0][o1][o2] = norm_c(x[c][r0][r1][r2]) with r[t_k] = s_k + o_k: out axis k is input
+// axis t_k, cropped to start s_k.
+__global__ __launch_bounds__(256) void crop_normalize_kernel(
+    const float* __restrict__ x, int C, int64_t X, int64_t Y, int64_t Z, int t0, int t1, int t2,
+    int64_t s0, int64_t s1, int64_t s2, int64_t O0, int64_t O1, int64_t O2, ChannelNorms norms,
+    float* __restrict__ out) {
+  const int64_t per = O0 * O1 * O2;
+  const int64_t total = per * C;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int c = (int)(e / per);
+    const int64_t p = e - c * per;
+    const int64_t o2 = p % O2, o1 = (p / O2) % O1, o0 = p / (O1 * O2);
+    const int64_t a0 = s0 + o0, a1 = s1 + o1, a2 = s2 + o2;
+    const int64_t r0 = t0 == 0 ? a0 : t1 == 0 ? a1 : a2;
+    const int64_t r1 = t0 == 1 ? a0 : t1 == 1 ? a1 : a2;
+    const int64_t r2 = t0 == 2 ? a0 : t1 == 2 ? a1 : a2;
+    float v = x[(int64_t)c * X * Y * Z + (r0 * Y + r1) * Z + r2];
+    if (norms.scheme[c] == NNX_NORM_CT) {
+      v = fminf(fmaxf(v, norms.lower[c]), norms.upper[c]);
+      v = __fdiv_rn(__fsub_rn(v, norms.mean[c]), norms.std[c]);
+    }
+    out[e] = v;
+  }
+}
+
+// ---- spline resampling -----------------------------------------------------------------
+
+// out (P0, P1, P2) float64 = in (n0, n1, n2) float32 edge-extended by p_a on each side of
+// axis a.
+__global__ __launch_bounds__(256) void pad_edge_kernel(const float* __restrict__ in, int64_t n0,
+                                                       int64_t n1, int64_t n2, int p0, int p1,
+                                                       int p2, double* __restrict__ out) {
+  const int64_t P0 = n0 + 2 * p0, P1 = n1 + 2 * p1, P2 = n2 + 2 * p2;
+  const int64_t total = P0 * P1 * P2;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i2 = e % P2, i1 = (e / P2) % P1, i0 = e / (P1 * P2);
+    const int64_t j0 = min(max(i0 - p0, (int64_t)0), n0 - 1);
+    const int64_t j1 = min(max(i1 - p1, (int64_t)0), n1 - 1);
+    const int64_t j2 = min(max(i2 - p2, (int64_t)0), n2 - 1);
+    out[e] = (double)in[(j0 * n1 + j1) * n2 + j2];
+  }
+}
+
+// Cubic B-spline coefficients along `axis` of a (P0, P1, P2) float64 array, in place, one
+// thread per line (z_n = z^n and the gain come from the host).
+__global__ __launch_bounds__(256) void prefilter_kernel(double* __restrict__ c, int64_t P0,
+                                                        int64_t P1, int64_t P2, int axis,
+                                                        double z, double z_n, double gain) {
+  const int64_t dims[3] = {P0, P1, P2};
+  const int64_t strides[3] = {P1 * P2, P2, 1};
+  const int64_t n = dims[axis], s = strides[axis];
+  const int a1 = axis == 0 ? 1 : 0, a2 = axis == 2 ? 1 : 2;
+  const int64_t lines = dims[a1] * dims[a2];
+  const int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (l >= lines || n < 2) return;
+  // lines enumerated with the last free axis fastest, so neighbouring threads touch
+  // neighbouring memory for the outer axes
+  const int64_t base = (l / dims[a2]) * strides[a1] + (l % dims[a2]) * strides[a2];
+  double* line = c + base;
+  for (int64_t i = 0; i < n; ++i) line[i * s] = line[i * s] * gain;
+  const double c0 = line[0];
+  double acc = line[0] + z_n * line[(n - 1) * s];
+  double z_i = z;
+  for (int64_t i = 1; i < n; ++i) {
+    acc = acc + z_i * (line[i * s] + z_n * line[(n - 1 - i) * s]);
+    z_i = z_i * z;
+  }
+  line[0] = acc * (z / (1.0 - z_n * z_n)) + c0;
+  for (int64_t i = 1; i < n; ++i) line[i * s] = line[i * s] + z * line[(i - 1) * s];
+  line[(n - 1) * s] = line[(n - 1) * s] * (z / (z - 1.0));
+  for (int64_t i = n - 2; i >= 0; --i) line[i * s] = z * (line[(i + 1) * s] - line[i * s]);
+}
+
+// One interpolation pass along `axis`: in (I0, I1, I2) -> out with that axis n_out long.
+// The axis holds n_in source samples padded by `pad` on each side.
+template <int ORDER>
+__global__ __launch_bounds__(256) void interp_axis_kernel(const double* __restrict__ in,
+                                                          int64_t I0, int64_t I1, int64_t I2,
+                                                          int axis, int64_t n_out, double ratio,
+                                                          int pad, double* __restrict__ out) {
+  int64_t dims[3] = {I0, I1, I2};
+  const int64_t in_stride = axis == 0 ? I1 * I2 : axis == 1 ? I2 : 1;
+  dims[axis] = n_out;
+  const int64_t total = dims[0] * dims[1] * dims[2];
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t q2 = e % dims[2], q1 = (e / dims[2]) % dims[1], q0 = e / (dims[1] * dims[2]);
+    const int64_t o = axis == 0 ? q0 : axis == 1 ? q1 : q2;
+    // source element of tap 0 with the axis coordinate set to 0
+    const int64_t row = axis == 0 ? q1 * I2 + q2 : axis == 1 ? q0 * I1 * I2 + q2
+                                                             : (q0 * I1 + q1) * I2;
+    const double cc = ((double)o + 0.5) * ratio - 0.5 + (double)pad;
+    const double f = floor(cc);
+    const double t = cc - f;
+    double sum = 0.0;
+    if constexpr (ORDER == 3) {
+      const double u = 1.0 - t;
+      const double w[4] = {u * u * u / 6.0, 2.0 / 3.0 - t * t + t * t * t / 2.0,
+                           2.0 / 3.0 - u * u + u * u * u / 2.0, t * t * t / 6.0};
+      const int64_t start = (int64_t)f - 1;
+#pragma unroll
+      for (int k = 0; k < 4; ++k) sum = sum + in[row + (start + k) * in_stride] * w[k];
+    } else {
+      const int64_t start = (int64_t)f;
+      sum = sum + in[row + start * in_stride] * (1.0 - t);
+      sum = sum + in[row + (start + 1) * in_stride] * t;
+    }
+    out[e] = sum;
+  }
+}
+
+// mm[k] = (min, max) over plane k along `axis` of a (n0, n1, n2) float32 channel; one
+// block per plane.
+__global__ __launch_bounds__(256) void plane_minmax_kernel(const float* __restrict__ in,
+                                                           int64_t n0, int64_t n1, int64_t n2,
+                                                           int axis, float2* __restrict__ mm) {
+  __shared__ float smin[4], smax[4];
+  const int64_t k = blockIdx.x;
+  const int64_t dims[3] = {n0, n1, n2};
+  const int a1 = axis == 0 ? 1 : 0, a2 = axis == 2 ? 1 : 2;
+  const int64_t strides[3] = {n1 * n2, n2, 1};
+  const int64_t m = dims[a1] * dims[a2];
+  float lo = INFINITY, hi = -INFINITY;
+  for (int64_t i = threadIdx.x; i < m; i += blockDim.x) {
+    const float v = in[k * strides[axis] + (i / dims[a2]) * strides[a1] + (i % dims[a2]) * strides[a2]];
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o));
+    hi = fmaxf(hi, __shfl_xor(hi, o));
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    smin[wave] = lo;
+    smax[wave] = hi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
+      lo = fminf(lo, smin[w]);
+      hi = fmaxf(hi, smax[w]);
+    }
+    mm[k] = make_float2(fminf(lo, smin[0]), fmaxf(hi, smax[0]));
+  }
+}
+
+// mm[n] = (min, max) over mm[0 .. n)
+__global__ __launch_bounds__(64) void reduce_minmax_kernel(float2* mm, int64_t n) {
+  float lo = INFINITY, hi = -INFINITY;
+  for (int64_t i = threadIdx.x; i < n; i += 64) {
+    lo = fminf(lo, mm[i].x);
+    hi = fmaxf(hi, mm[i].y);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o));
+    hi = fmaxf(hi, __shfl_xor(hi, o));
+  }
+  if (threadIdx.x == 0) mm[n] = make_float2(lo, hi);
+}
+
+// whole-volume resize: out = clip(float(v), min, max)
+__global__ __launch_bounds__(256) void cast_clip_kernel(const double* __restrict__ in, int64_t n,
+                                                        const float2* __restrict__ mm,
+                                                        float* __restrict__ out) {
+  const float2 b = *mm;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x)
+    out[e] = fminf(fmaxf((float)in[e], b.x), b.y);
+}
+
+// separate axis: out[.. o ..] = float(clip_k(inter[.. k ..])), k = nearest source plane of o
+__global__ __launch_bounds__(256) void plane_clip_nearest_kernel(
+    const double* __restrict__ inter, int64_t d0, int64_t d1, int64_t d2, int axis,
+    int64_t n_new, double ratio, const float2* __restrict__ mm, float* __restrict__ out) {
+  int64_t dims[3] = {d0, d1, d2};
+  const int64_t n_old = dims[axis];
+  const int64_t in_stride = axis == 0 ? d1 * d2 : axis == 1 ? d2 : 1;
+  dims[axis] = n_new;
+  const int64_t total = dims[0] * dims[1] * dims[2];
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t q2 = e % dims[2], q1 = (e / dims[2]) % dims[1], q0 = e / (dims[1] * dims[2]);
+    const int64_t o = axis == 0 ? q0 : axis == 1 ? q1 : q2;
+    const int64_t row = axis == 0 ? q1 * d2 + q2 : axis == 1 ? q0 * d1 * d2 + q2
+                                                             : (q0 * d1 + q1) * d2;
+    const double coord = ratio * ((double)o + 0.5) - 0.5;
+    int64_t k = (int64_t)floor(coord + 0.5);
+    k = min(max(k, (int64_t)0), n_old - 1);
+    const float2 b = mm[k];
+    const double v = fmin(fmax(inter[row + k * in_stride], (double)b.x), (double)b.y);
+    out[e] = (float)v;
+  }
+}
+
+int blocks_for(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 1 << 20)); }
+
+struct SplinePlan {
+  int64_t n[3], N[3];
+  int pad[3];
+  int axes[3], naxes;  // resized axes, in order
+  int64_t a_elems, b_elems, mm_elems;
+};
+
+SplinePlan spline_plan(const int64_t* size, const int64_t* new_size, int separate_axis) {
+  SplinePlan p{};
+  p.naxes = 0;
+  for (int a = 0; a < 3; ++a) {
+    p.n[a] = size[a];
+    p.N[a] = new_size[a];
+    const bool resized = a != separate_axis;
+    p.pad[a] = resized ? kSplinePad : 0;
+    if (resized) p.axes[p.naxes++] = a;
+  }
+  // ping-pong: A holds the padded copy, B the first pass, A the second, B the third
+  int64_t d[3] = {p.n[0] + 2 * p.pad[0], p.n[1] + 2 * p.pad[1], p.n[2] + 2 * p.pad[2]};
+  int64_t sizes[4];
+  sizes[0] = d[0] * d[1] * d[2];
+  for (int k = 0; k < p.naxes; ++k) {
+    d[p.axes[k]] = p.N[p.axes[k]];
+    sizes[k + 1] = d[0] * d[1] * d[2];
+  }
+  p.a_elems = p.b_elems = 0;
+  for (int k = 0; k <= p.naxes; ++k) {
+    int64_t& slot = (k % 2 == 0) ? p.a_elems : p.b_elems;
+    slot = std::max(slot, sizes[k]);
+  }
+  p.mm_elems = (separate_axis >= 0 ? p.n[separate_axis] : p.n[0]) + 1;
+  return p;
+}
+
+}  // namespace
+
+void nonzero_bbox(const float* x, int channels, const int64_t* size, int* bbox, hipStream_t st) {
+  require(x && bbox && size, "bounding-box pointers must not be null");
+  require(channels >= 1 && size[0] >= 1 && size[1] >= 1 && size[2] >= 1, "invalid volume shape");
+  const int64_t n = size[0] * size[1] * size[2];
+  require(size[0] < INT_MAX && size[1] < INT_MAX && size[2] < INT_MAX, "volume axis too long");
+  ProfScope prof("preprocess_bbox", 0.0, 4.0 * (double)n * channels, st);
+  hipLaunchKernelGGL(bbox_init_kernel, dim3(1), dim3(64), 0, st, bbox);
+  hipLaunchKernelGGL(bbox_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 8192)),
+                     dim3(256), 0, st, x, channels, size[0], size[1], size[2], bbox);
+  launch_check("nonzero_bbox");
+}
+
+void crop_normalize(const float* x, int channels, const int64_t* size, const int* transpose,
+                    const int64_t* start, const int64_t* out_size, const int* schemes,
+                    const float* norm, float* out, hipStream_t st) {
+  require(x && out && size && transpose && start && out_size && schemes,
+          "crop/normalise pointers must not be null");
+  require(channels >= 1 && channels <= kMaxNormChannels,
+          "device normalisation supports 1..16 channels");
+  bool seen[3] = {false, false, false};
+  for (int k = 0; k < 3; ++k) {
+    require(transpose[k] >= 0 && transpose[k] < 3 && !seen[transpose[k]],
+            "transpose must be a permutation of the three spatial axes");
+    seen[transpose[k]] = true;
+  }
+  for (int k = 0; k < 3; ++k) {
+    const int64_t n = size[transpose[k]];
+    require(out_size[k] >= 1 && start[k] >= 0 && start[k] + out_size[k] <= n,
+            "crop window outside the volume");
+  }
+  ChannelNorms cn{};
+  for (int c = 0; c < channels; ++c) {
+    require(schemes[c] == NNX_NORM_NONE || schemes[c] == NNX_NORM_CT,
+            "device normalisation supports NoNormalization and CTNormalization");
+    cn.scheme[c] = schemes[c];
+    if (schemes[c] == NNX_NORM_CT) {
+      require(norm != nullptr, "CT normalisation needs its statistics");
+      const float* p = norm + 4 * c;
+      require(std::isfinite(p[0]) && std::isfinite(p[1]) && p[1] > 0.f && std::isfinite(p[2]) &&
+                  std::isfinite(p[3]) && p[2] <= p[3],
+              "CT statistics must be finite, std positive and the percentiles ordered");
+      cn.mean[c] = p[0];
+      cn.std[c] = std::max(p[1], 1e-8f);
+      cn.lower[c] = p[2];
+      cn.upper[c] = p[3];
+    }
+  }
+  const int64_t total = out_size[0] * out_size[1] * out_size[2] * channels;
+  ProfScope prof("preprocess_crop_normalize", 0.0, 8.0 * (double)total, st);
+  hipLaunchKernelGGL(crop_normalize_kernel, dim3(blocks_for(total)), dim3(256), 0, st, x,
+                     channels, size[0], size[1], size[2], transpose[0], transpose[1], transpose[2],
+                     start[0], start[1], start[2], out_size[0], out_size[1], out_size[2], cn, out);
+  launch_check("crop_normalize");
+}
+
+size_t resample_spline_workspace(const int64_t* size, const int64_t* new_size, int separate_axis) {
+  const SplinePlan p = spline_plan(size, new_size, separate_axis);
+  return (size_t)(p.a_elems + p.b_elems) * sizeof(double) + (size_t)p.mm_elems * sizeof(float2) +
+         256;
+}
+
+void resample_spline(const float* x, int channels, const int64_t* size, const int64_t* new_size,
+                     int order, int separate_axis, int order_z, void* work, size_t work_bytes,
+                     float* out, hipStream_t st) {
+  require(x && out && size && new_size, "resampling pointers must not be null");
+  require(channels >= 1, "resampling needs at least one channel");
+  for (int a = 0; a < 3; ++a)
+    require(size[a] >= 1 && new_size[a] >= 1, "resampling shapes must be positive");
+  require(order == 1 || order == 3, "device spline resampling supports orders 1 and 3");
+  require(separate_axis >= -1 && separate_axis < 3, "separate axis must be -1, 0, 1 or 2");
+  require(separate_axis < 0 || order_z == 0,
+          "device separate-axis resampling supports order_z 0 (nearest)");
+  const SplinePlan p = spline_plan(size, new_size, separate_axis);
+  require(work && work_bytes >= resample_spline_workspace(size, new_size, separate_axis),
+          "resampling workspace too small");
+  double* A = static_cast<double*>(work);
+  double* B = A + p.a_elems;
+  float2* mm = reinterpret_cast<float2*>(B + p.b_elems);
+  const int64_t in_vox = size[0] * size[1] * size[2];
+  const int64_t out_vox = new_size[0] * new_size[1] * new_size[2];
+  ProfScope prof("preprocess_resample_spline", 0.0,
+                 (double)channels * (4.0 * (in_vox + out_vox) + 16.0 * (p.a_elems + p.b_elems)), st);
+  const double z = std::sqrt(3.0) - 2.0;
+  const double gain = (1.0 - z) * (1.0 - 1.0 / z);
+  const int mm_axis = separate_axis >= 0 ? separate_axis : 0;
+  for (int c = 0; c < channels; ++c) {
+    const float* xc = x + (int64_t)c * in_vox;
+    hipLaunchKernelGGL(plane_minmax_kernel, dim3((unsigned)size[mm_axis]), dim3(256), 0, st, xc,
+                       size[0], size[1], size[2], mm_axis, mm);
+    if (separate_axis < 0)
+      hipLaunchKernelGGL(reduce_minmax_kernel, dim3(1), dim3(64), 0, st, mm, size[0]);
+    int64_t d[3] = {size[0] + 2 * p.pad[0], size[1] + 2 * p.pad[1], size[2] + 2 * p.pad[2]};
+    hipLaunchKernelGGL(pad_edge_kernel, dim3(blocks_for(d[0] * d[1] * d[2])), dim3(256), 0, st,
+                       xc, size[0], size[1], size[2], p.pad[0], p.pad[1], p.pad[2], A);
+    if (order == 3) {
+      for (int k = 0; k < p.naxes; ++k) {
+        const int a = p.axes[k];
+        const int64_t lines = d[0] * d[1] * d[2] / d[a];
+        const double z_n = std::pow(z, (double)d[a]);
+        hipLaunchKernelGGL(prefilter_kernel, dim3((unsigned)ceil_div(lines, 256)), dim3(256), 0, st,
+                           A, d[0], d[1], d[2], a, z, z_n, gain);
+      }
+    }
+    double* src = A;
+    double* dst = B;
+    for (int k = 0; k < p.naxes; ++k) {
+      const int a = p.axes[k];
+      int64_t od[3] = {d[0], d[1], d[2]};
+      od[a] = new_size[a];
+      const double ratio = (double)size[a] / (double)new_size[a];
+      const int64_t total = od[0] * od[1] * od[2];
+      if (order == 3)
+        hipLaunchKernelGGL(interp_axis_kernel<3>, dim3(blocks_for(total)), dim3(256), 0, st, src,
+                           d[0], d[1], d[2], a, new_size[a], ratio, p.pad[a], dst);
+      else
+        hipLaunchKernelGGL(interp_axis_kernel<1>, dim3(blocks_for(total)), dim3(256), 0, st, src,
+                           d[0], d[1], d[2], a, new_size[a], ratio, p.pad[a], dst);
+      d[a] = new_size[a];
+      std::swap(src, dst);
+    }
+    float* oc = out + (int64_t)c * out_vox;
+    if (separate_axis < 0) {
+      hipLaunchKernelGGL(cast_clip_kernel, dim3(blocks_for(out_vox)), dim3(256), 0, st, src,
+                         out_vox, mm + size[0], oc);
+    } else {
+      const int a = separate_axis;
+      hipLaunchKernelGGL(plane_clip_nearest_kernel, dim3(blocks_for(out_vox)), dim3(256), 0, st,
+                         src, d[0], d[1], d[2], a, new_size[a],
+                         (double)size[a] / (double)new_size[a], mm, oc);
+    }
+  }
+  launch_check("resample_spline");
+}
+
+}  // namespace nnx

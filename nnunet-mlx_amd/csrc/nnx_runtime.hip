@@ -1143,6 +1143,37 @@ int nnx_restore_labels(const void* d_logits, int half, int classes, const int* s
   });
 }
 
+int nnx_nonzero_bbox(const float* d_data, int channels, const int64_t* size, int* d_bbox,
+                     void* stream) {
+  return guarded([&] { nonzero_bbox(d_data, channels, size, d_bbox, as_stream(stream)); });
+}
+
+int nnx_crop_normalize(const float* d_data, int channels, const int64_t* size,
+                       const int* transpose, const int64_t* start, const int64_t* out_size,
+                       const int* schemes, const float* norm, float* d_out, void* stream) {
+  return guarded([&] {
+    crop_normalize(d_data, channels, size, transpose, start, out_size, schemes, norm, d_out,
+                   as_stream(stream));
+  });
+}
+
+size_t nnx_resample_spline_workspace(const int64_t* size, const int64_t* new_size,
+                                     int separate_axis) {
+  if (!size || !new_size || separate_axis < -1 || separate_axis > 2) return 0;
+  for (int a = 0; a < 3; ++a)
+    if (size[a] < 1 || new_size[a] < 1) return 0;
+  return resample_spline_workspace(size, new_size, separate_axis);
+}
+
+int nnx_resample_spline(const float* d_data, int channels, const int64_t* size,
+                        const int64_t* new_size, int order, int separate_axis, int order_z,
+                        void* d_work, size_t work_bytes, float* d_out, void* stream) {
+  return guarded([&] {
+    resample_spline(d_data, channels, size, new_size, order, separate_axis, order_z, d_work,
+                    work_bytes, d_out, as_stream(stream));
+  });
+}
+
 int nnx_conv1x1(const float* d_x, int cin, const float* d_weight, const float* d_bias, float* d_y,
                 int64_t voxels, int cout, void* stream) {
   return guarded([&] { conv1x1(d_x, cin, d_weight, d_bias, d_y, voxels, cout, as_stream(stream)); });

@@ -33,6 +33,8 @@ NNX_ARCH_RESIDUAL = 1
 NNX_PRECISION_FP32 = 0
 NNX_PRECISION_FP32_SPLIT = 1
 NNX_PRECISION_BF16 = 2
+NNX_NORM_NONE = 0
+NNX_NORM_CT = 1
 NNX_ACCUM_F32 = 0
 NNX_ACCUM_NNUNET_F16 = 1
 
@@ -181,6 +183,18 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "nnx_restore_labels": (
         ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, c_int_p, c_int_p, c_void_p, c_void_p]
+    ),
+    "nnx_nonzero_bbox": (ctypes.c_int, [c_void_p, ctypes.c_int, c_i64_p, c_void_p, c_void_p]),
+    "nnx_crop_normalize": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_i64_p, c_int_p, c_i64_p, c_i64_p, c_int_p,
+         ctypes.POINTER(ctypes.c_float), c_void_p, c_void_p],
+    ),
+    "nnx_resample_spline_workspace": (ctypes.c_size_t, [c_i64_p, c_i64_p, ctypes.c_int]),
+    "nnx_resample_spline": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_i64_p, c_i64_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+         c_void_p, ctypes.c_size_t, c_void_p, c_void_p],
     ),
     "nnx_tconv3d_gemm": (
         ctypes.c_int,

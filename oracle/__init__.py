@@ -15,6 +15,10 @@ Modules:
   * ``restore``        — numpy float64 restatement of the class-logit restoration
                          (half-pixel trilinear + argmax) of
                          src/nnunet_mlx/kernels/metal_restore.py.
+  * ``preprocess``     — numpy restatement of raw-case preprocessing (crop to
+                         nonzero, CT normalisation, the scikit-image / SciPy spline
+                         resize and the separate-axis path) of
+                         src/nnunet_mlx/data/preprocessing.py and resampling.py.
 
 Pinning (what checks each function against something other than itself) is listed
 in the module docstrings and exercised by ``tests/test_oracle_*.py``.  Nothing here

@@ -1,0 +1,210 @@
+"""Device preprocessing against the oracle (crop bounds, crop/transpose/normalise bit-exact;
+spline resampling to one float32 rounding of the float64 oracle)."""
+
+from __future__ import annotations
+
+import ctypes
+import itertools
+
+import numpy as np
+import pytest
+import torch
+
+from nnunet_mlx import _native
+from nnunet_mlx.data.preprocessing import PreprocessPlan, preprocess_raw_case
+from nnunet_mlx.errors import ContractError
+from oracle import preprocess as op
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _native.load()
+
+
+def stream():
+    return _native.stream_handle()
+
+
+def dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def sparse_volume(rng, shape, boxes):
+    data = np.zeros(shape, dtype=np.float32)
+    for c, (lo, hi) in boxes:
+        sl = tuple(slice(a, b) for a, b in zip(lo, hi))
+        data[(c, *sl)] = rng.standard_normal(tuple(b - a for a, b in zip(lo, hi))).astype(np.float32)
+    return data
+
+
+@pytest.mark.parametrize("shape,boxes", [
+    ((1, 9, 10, 11), [(0, ((2, 3, 4), (5, 9, 6)))]),
+    ((2, 17, 5, 33), [(0, ((0, 1, 30), (3, 2, 33))), (1, ((10, 0, 2), (17, 4, 3)))]),
+    ((3, 64, 48, 40), [(2, ((1, 1, 1), (63, 47, 39)))]),
+])
+def test_nonzero_bbox(lib, shape, boxes):
+    print(f"bbox case {shape}", flush=True)
+    data = sparse_volume(np.random.default_rng(len(shape) + shape[1]), shape, boxes)
+    bbox = torch.empty(6, dtype=torch.int32, device="cuda")
+    _native.check(lib.nnx_nonzero_bbox(dev(data).data_ptr(), shape[0], _native.i64s(shape[1:]),
+                                       bbox.data_ptr(), stream()))
+    got = bbox.cpu().numpy().reshape(3, 2)
+    want = op.nonzero_bbox(data)
+    assert [(int(a), int(b) + 1) for a, b in got] == list(want)
+
+
+def test_nonzero_bbox_empty(lib):
+    data = np.zeros((1, 4, 5, 6), dtype=np.float32)
+    bbox = torch.empty(6, dtype=torch.int32, device="cuda")
+    _native.check(lib.nnx_nonzero_bbox(dev(data).data_ptr(), 1, _native.i64s((4, 5, 6)),
+                                       bbox.data_ptr(), stream()))
+    got = bbox.cpu().numpy().reshape(3, 2)
+    assert (got[:, 1] == -1).all()
+
+
+@pytest.mark.parametrize("transpose", list(itertools.permutations(range(3))))
+def test_crop_normalize_exact(lib, transpose):
+    print(f"crop/normalise transpose {transpose}", flush=True)
+    rng = np.random.default_rng(sum(i * 3 ** k for k, i in enumerate(transpose)))
+    raw = (rng.standard_normal((2, 11, 13, 7)) * 900).astype(np.float32)
+    norm = np.array([[41.5, 60.25, -1000.0, 1500.0], [0, 0, 0, 0]], dtype=np.float32)
+    schemes = [_native.NNX_NORM_CT, _native.NNX_NORM_NONE]
+    tshape = tuple(raw.shape[1 + a] for a in transpose)
+    start = (1, 2, 0)
+    out_size = tuple(s - st - 1 for s, st in zip(tshape, start))
+    out = torch.full((2, *out_size), float("nan"), device="cuda")
+    _native.check(lib.nnx_crop_normalize(
+        dev(raw).data_ptr(), 2, _native.i64s(raw.shape[1:]), _native.ints(transpose),
+        _native.i64s(start), _native.i64s(out_size), _native.ints(schemes),
+        norm.ctypes.data_as(ctypes.POINTER(ctypes.c_float)), out.data_ptr(),
+        stream()))
+    t = raw.transpose((0, *(a + 1 for a in transpose)))
+    crop = t[(slice(None), *(slice(s, s + n) for s, n in zip(start, out_size)))]
+    want0 = op.ct_normalize(crop[0], 41.5, 60.25, -1000.0, 1500.0)
+    got = out.cpu().numpy()
+    np.testing.assert_array_equal(got[0], want0)
+    np.testing.assert_array_equal(got[1], crop[1])
+
+
+def spline_device(lib, data, new_shape, order=3, separate_axis=-1):
+    size = data.shape[1:]
+    work = lib.nnx_resample_spline_workspace(_native.i64s(size), _native.i64s(new_shape), separate_axis)
+    assert work > 0
+    buf = torch.empty(work, dtype=torch.uint8, device="cuda")
+    out = torch.full((data.shape[0], *new_shape), float("nan"), device="cuda")
+    _native.check(lib.nnx_resample_spline(dev(data).data_ptr(), data.shape[0], _native.i64s(size),
+                                          _native.i64s(new_shape), order, separate_axis, 0,
+                                          buf.data_ptr(), work, out.data_ptr(), stream()))
+    return out.cpu().numpy()
+
+
+def assert_one_rounding(got, want):
+    """float32 results of the same float64 value: equal, or one float32 step apart where
+    the two float64 evaluations straddle a rounding boundary."""
+    assert got.shape == want.shape and np.isfinite(got).all()
+    ulp = np.spacing(np.abs(want).astype(np.float32))
+    diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    assert (diff <= ulp).all(), float((diff / np.maximum(ulp, 1e-45)).max())
+    assert (got == want).mean() >= 0.999
+
+
+SPLINE_CASES = [
+    ((1, 20, 24, 18), (33, 17, 18), 3),
+    ((2, 31, 12, 40), (19, 25, 57), 3),
+    ((1, 9, 64, 64), (9, 101, 77), 3),
+    ((1, 20, 24, 18), (33, 17, 29), 1),
+]
+
+
+@pytest.mark.parametrize("shape,new_shape,order", SPLINE_CASES)
+def test_resample_spline_whole_volume(lib, shape, new_shape, order):
+    print(f"spline case {shape} -> {new_shape} order {order}", flush=True)
+    rng = np.random.default_rng(shape[1] + new_shape[2])
+    data = (rng.standard_normal(shape) * 3).astype(np.float32)
+    got = spline_device(lib, data, new_shape, order)
+    want = op.resample_data(data, new_shape, order=order)
+    assert_one_rounding(got, want)
+    # the clip keeps every channel inside its input range
+    for c in range(shape[0]):
+        assert got[c].min() >= data[c].min() and got[c].max() <= data[c].max()
+
+
+@pytest.mark.parametrize("axis", [0, 1, 2])
+def test_resample_spline_separate_axis(lib, axis):
+    print(f"separate-axis spline case axis {axis}", flush=True)
+    rng = np.random.default_rng(40 + axis)
+    shape = (2, 11, 23, 19)
+    new_shape = [30, 16, 27]
+    new_shape[axis] = {0: 26, 1: 41, 2: 8}[axis]
+    data = (rng.standard_normal(shape) * 5).astype(np.float32)
+    got = spline_device(lib, data, tuple(new_shape), 3, axis)
+    want = op.resample_data(data, tuple(new_shape), separate_axis=axis)
+    assert_one_rounding(got, want)
+
+
+def ct_plan(spacing, transpose=(0, 1, 2), resampling=None):
+    plans = {
+        "transpose_forward": list(transpose),
+        "transpose_backward": [list(transpose).index(a) for a in range(3)],
+        "foreground_intensity_properties_per_channel": {
+            "0": {"mean": 99.4, "std": 137.2, "percentile_00_5": -958.0, "percentile_99_5": 327.0}},
+        "configurations": {"3d_fullres": {
+            "spacing": list(spacing), "normalization_schemes": ["CTNormalization"],
+            "use_mask_for_norm": [False], "patch_size": [64, 64, 64],
+            "resampling_fn_data": resampling or "resample_data_or_seg_to_shape",
+            "resampling_fn_data_kwargs": {"is_seg": False, "order": 3, "order_z": 0,
+                                          "force_separate_z": None}}},
+    }
+    return PreprocessPlan.from_plans(plans, "3d_fullres")
+
+
+def oracle_case(raw, spacing, plan):
+    forward = plan.transpose_forward
+    t = raw.astype(np.float32).transpose((0, *(a + 1 for a in forward)))
+    bbox = op.nonzero_bbox(t)
+    crop = t[(slice(None), *(slice(a, b) for a, b in bbox))]
+    st = plan.intensity_properties["0"]
+    norm = op.ct_normalize(crop[0], st["mean"], st["std"], st["percentile_00_5"],
+                           st["percentile_99_5"])[None]
+    original = tuple(spacing[a] for a in forward)
+    target = tuple(o if c is None else c for c, o in zip(plan.spacing, original))
+    new_shape = tuple(round(o / n * s) for o, n, s in zip(original, target, crop.shape[1:]))
+    ratio = max(original) / min(original)
+    separate = None
+    if ratio > 3 or max(target) / min(target) > 3:
+        basis = original if ratio > 3 else target
+        axes = [i for i, s in enumerate(basis) if max(basis) / s == 1]
+        separate = axes[0] if len(axes) == 1 else None
+    return bbox, op.resample_data(norm, new_shape, separate_axis=separate)
+
+
+@pytest.mark.parametrize("spacing,target,transpose", [
+    ((2.5, 0.8, 0.8), (1.0, 0.78, 0.78), (0, 1, 2)),      # anisotropic: separate axis 0
+    ((0.7, 0.7, 1.6), (1.0, 1.0, 1.0), (2, 0, 1)),        # isotropic-enough, transposed
+])
+def test_preprocess_raw_case_matches_oracle(spacing, target, transpose):
+    print(f"preprocess case spacing {spacing} target {target} transpose {transpose}", flush=True)
+    rng = np.random.default_rng(7)
+    raw = np.zeros((1, 24, 40, 36), dtype=np.int16)
+    raw[0, 3:21, 5:37, 2:30] = (rng.standard_normal((18, 32, 28)) * 400 - 200).astype(np.int16)
+    plan = ct_plan(target, transpose)
+    out = preprocess_raw_case(raw, {"spacing": list(spacing)}, plan)
+    bbox, want = oracle_case(raw, spacing, plan)
+    assert out.properties["bbox_used_for_cropping"] == [list(b) for b in bbox]
+    assert out.properties["shape_before_cropping"] == tuple(raw.shape[1 + a] for a in transpose)
+    assert_one_rounding(out.data.cpu().numpy(), want)
+
+
+def test_preprocess_rejects_unsupported():
+    plan = ct_plan((1.0, 1.0, 1.0))
+    with pytest.raises(ContractError):
+        preprocess_raw_case(np.zeros((1, 4, 4, 4), dtype=np.float32), {"spacing": [1, 1, 1]}, plan)
+    zplan = PreprocessPlan(plan.transpose_forward, plan.spacing, ("ZScoreNormalization",), (True,),
+                           plan.intensity_properties, plan.data_resampling)
+    with pytest.raises(ContractError):
+        preprocess_raw_case(np.ones((1, 4, 4, 4), dtype=np.float32), {"spacing": [1, 1, 1]}, zplan)
+    tplan = ct_plan((2.0, 2.0, 2.0), resampling="resample_torch_fornnunet")
+    with pytest.raises(ContractError):
+        preprocess_raw_case(np.ones((1, 8, 8, 8), dtype=np.float32), {"spacing": [1, 1, 1]}, tplan)
