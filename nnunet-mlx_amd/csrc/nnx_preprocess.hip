@@ -14,9 +14,10 @@
 //     building coefficients for edge extension);
 //   * order 3: per axis in turn, per line: multiply by the gain (1 - z)(1 - 1/z), causal
 //     initialisation for edge extension c0' = (c0 + z^n c[n-1] + sum_{i=1}^{n-1} z^i (c[i] +
-//     z^n c[n-1-i])) * z / (1 - z^2n) + c0, causal recursion c[i] += z c[i-1], anticausal
-//     initialisation c[n-1] *= z / (z - 1), anticausal recursion c[i] = z (c[i+1] - c[i]),
-//     pole z = sqrt(3) - 2;
+//     z^n c[n-1-i])) * z / (1 - z^2n) + c0 (terms past i = 48, below float64 resolution,
+//     omitted), causal recursion c[i] += z c[i-1], anticausal initialisation
+//     c[n-1] *= z / (z - 1), anticausal recursion c[i] = z (c[i+1] - c[i]), pole
+//     z = sqrt(3) - 2;
 //   * evaluation one axis at a time: output index o samples the padded coordinate
 //     cc = (o + 0.5) * n_in / n_out - 0.5 + 12 with the cardinal cubic B-spline weights of
 //     t = cc - floor(cc) at floor(cc) - 1 .. floor(cc) + 2 (order 1: 1 - t, t at floor(cc),
@@ -25,8 +26,9 @@
 //     the other two axes resized per plane (float64, clipped to the plane's [min, max]),
 //     then the separate axis by half-pixel nearest indices floor(old/new (o + 0.5) - 0.5 +
 //     0.5) clamped, cast to float32 once.
-// Roofline: HBM — each pass reads and writes its float64 array once (the prefilter walks
-// each line twice); the crop/normalise pass reads and writes 4 B per kept voxel.
+// Roofline: HBM — the edge copy writes, each prefilter axis reads and writes twice (causal,
+// anticausal) and each interpolation pass reads and writes its float64 array once; the
+// crop/normalise pass reads and writes 4 B per kept voxel.
 
 #include <hip/hip_runtime.h>
 
@@ -41,6 +43,7 @@ namespace nnx {
 namespace {
 
 constexpr int kSplinePad = 12;
+constexpr int kMinmaxParts = 16;  // blocks per plane of the min/max reduction
 
 // ---- nonzero bounds -------------------------------------------------------------------
 
@@ -52,33 +55,41 @@ __global__ void bbox_init_kernel(int* bbox) {
 }
 
 // bbox[2a] / bbox[2a + 1] = smallest / largest index along axis a of a voxel where any
-// channel is nonzero.  Block minima and maxima reach memory by one vector atomic each.
+// channel is nonzero.  One wave per (x, y) row at a time, its lanes along z (coalesced);
+// block minima and maxima reach memory by one vector atomic each.
 __global__ __launch_bounds__(256) void bbox_kernel(const float* __restrict__ x, int C, int64_t X,
                                                    int64_t Y, int64_t Z, int* bbox) {
   __shared__ int red[6][4];
   int lo[3] = {INT_MAX, INT_MAX, INT_MAX}, hi[3] = {-1, -1, -1};
   const int64_t n = X * Y * Z;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    bool nz = false;
-    for (int c = 0; c < C; ++c) nz |= x[(int64_t)c * n + i] != 0.f;
-    if (nz) {
-      const int idx[3] = {(int)(i / (Y * Z)), (int)((i / Z) % Y), (int)(i % Z)};
-#pragma unroll
-      for (int a = 0; a < 3; ++a) {
-        lo[a] = min(lo[a], idx[a]);
-        hi[a] = max(hi[a], idx[a]);
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int64_t waves = (int64_t)gridDim.x * 4;
+  for (int64_t r = blockIdx.x * (int64_t)4 + wave; r < X * Y; r += waves) {
+    const float* row = x + r * Z;
+    int zlo = INT_MAX, zhi = -1;
+    for (int64_t z = lane; z < Z; z += 64) {
+      bool nz = false;
+      for (int c = 0; c < C; ++c) nz |= row[(int64_t)c * n + z] != 0.f;
+      if (nz) {
+        zlo = min(zlo, (int)z);
+        zhi = max(zhi, (int)z);
       }
     }
-  }
 #pragma unroll
-  for (int o = 32; o >= 1; o >>= 1)
-#pragma unroll
-    for (int a = 0; a < 3; ++a) {
-      lo[a] = min(lo[a], __shfl_xor(lo[a], o));
-      hi[a] = max(hi[a], __shfl_xor(hi[a], o));
+    for (int o = 32; o >= 1; o >>= 1) {
+      zlo = min(zlo, __shfl_xor(zlo, o));
+      zhi = max(zhi, __shfl_xor(zhi, o));
     }
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (zhi >= 0) {
+      const int rx = (int)(r / Y), ry = (int)(r % Y);
+      lo[0] = min(lo[0], rx);
+      hi[0] = max(hi[0], rx);
+      lo[1] = min(lo[1], ry);
+      hi[1] = max(hi[1], ry);
+      lo[2] = min(lo[2], zlo);
+      hi[2] = max(hi[2], zhi);
+    }
+  }
   if (lane == 0)
 #pragma unroll
     for (int a = 0; a < 3; ++a) {
@@ -153,11 +164,18 @@ __global__ __launch_bounds__(256) void pad_edge_kernel(const float* __restrict__
   }
 }
 
-// Cubic B-spline coefficients along `axis` of a (P0, P1, P2) float64 array, in place, one
-// thread per line (z_n = z^n and the gain come from the host).
-__global__ __launch_bounds__(256) void prefilter_kernel(double* __restrict__ c, int64_t P0,
-                                                        int64_t P1, int64_t P2, int axis,
-                                                        double z, double z_n, double gain) {
+// The initial sums of the causal recursion run over the first and last kInitTaps
+// elements only: |z|^48 ~ 3.5e-28, so later terms lie below float64 resolution.
+constexpr int kInitTaps = 48;
+
+// Cubic B-spline coefficients along `axis` (0 or 1) of a (P0, P1, P2) float64 array, in
+// place; one thread per line, neighbouring threads on neighbouring lines (coalesced).  The
+// gain is applied as each element is first read: c'[0] from the initial sum, then
+// c[i] = gain c[i] + z c[i-1], c[n-1] *= z / (z - 1), c[i] = z (c[i+1] - c[i]).
+__global__ __launch_bounds__(256) void prefilter_strided_kernel(double* __restrict__ c,
+                                                                int64_t P0, int64_t P1,
+                                                                int64_t P2, int axis, double z,
+                                                                double z_n, double gain) {
   const int64_t dims[3] = {P0, P1, P2};
   const int64_t strides[3] = {P1 * P2, P2, 1};
   const int64_t n = dims[axis], s = strides[axis];
@@ -165,22 +183,113 @@ __global__ __launch_bounds__(256) void prefilter_kernel(double* __restrict__ c, 
   const int64_t lines = dims[a1] * dims[a2];
   const int64_t l = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
   if (l >= lines || n < 2) return;
-  // lines enumerated with the last free axis fastest, so neighbouring threads touch
-  // neighbouring memory for the outer axes
-  const int64_t base = (l / dims[a2]) * strides[a1] + (l % dims[a2]) * strides[a2];
-  double* line = c + base;
-  for (int64_t i = 0; i < n; ++i) line[i * s] = line[i * s] * gain;
-  const double c0 = line[0];
-  double acc = line[0] + z_n * line[(n - 1) * s];
+  double* line = c + (l / dims[a2]) * strides[a1] + (l % dims[a2]) * strides[a2];
+  const int64_t K = n - 1 < kInitTaps ? n - 1 : kInitTaps;
+  const double c0 = line[0] * gain;
+  double acc = c0 + z_n * (line[(n - 1) * s] * gain);
   double z_i = z;
-  for (int64_t i = 1; i < n; ++i) {
-    acc = acc + z_i * (line[i * s] + z_n * line[(n - 1 - i) * s]);
+  for (int64_t i = 1; i <= K; ++i) {
+    acc = acc + z_i * (line[i * s] * gain + z_n * (line[(n - 1 - i) * s] * gain));
     z_i = z_i * z;
   }
-  line[0] = acc * (z / (1.0 - z_n * z_n)) + c0;
-  for (int64_t i = 1; i < n; ++i) line[i * s] = line[i * s] + z * line[(i - 1) * s];
-  line[(n - 1) * s] = line[(n - 1) * s] * (z / (z - 1.0));
-  for (int64_t i = n - 2; i >= 0; --i) line[i * s] = z * (line[(i + 1) * s] - line[i * s]);
+  double prev = acc * (z / (1.0 - z_n * z_n)) + c0;
+  line[0] = prev;
+  for (int64_t i = 1; i < n; ++i) {
+    prev = line[i * s] * gain + z * prev;
+    line[i * s] = prev;
+  }
+  double next = prev * (z / (z - 1.0));
+  line[(n - 1) * s] = next;
+  for (int64_t i = n - 2; i >= 0; --i) {
+    next = z * (next - line[i * s]);
+    line[i * s] = next;
+  }
+}
+
+// The same coefficients along the contiguous axis: lines are rows of n elements.  A block
+// takes 256 consecutive rows (one per thread) and moves them through LDS in chunks of
+// kTileW elements, so every global access reads or writes 128-byte row segments.
+constexpr int kTileW = 16;
+
+__global__ __launch_bounds__(256) void prefilter_contig_kernel(double* __restrict__ c,
+                                                               int64_t lines, int64_t n,
+                                                               double z, double z_n,
+                                                               double gain) {
+  __shared__ double tile[256][kTileW + 1];
+  __shared__ double zp[kInitTaps + 1];
+  const int t = threadIdx.x;
+  const int64_t l0 = blockIdx.x * (int64_t)256;
+  if (t == 0) {
+    zp[0] = 1.0;
+    for (int i = 1; i <= kInitTaps; ++i) zp[i] = zp[i - 1] * z;
+  }
+  auto load = [&](int64_t k0) {
+    for (int p = 0; p < 256 / (256 / kTileW); ++p) {
+      const int j = p * (256 / kTileW) + t / kTileW, q = t % kTileW;
+      const int64_t i = k0 + q, line = l0 + j;
+      tile[j][q] = (line < lines && i < n) ? c[line * n + i] : 0.0;
+    }
+  };
+  auto store = [&](int64_t k0) {
+    for (int p = 0; p < 256 / (256 / kTileW); ++p) {
+      const int j = p * (256 / kTileW) + t / kTileW, q = t % kTileW;
+      const int64_t i = k0 + q, line = l0 + j;
+      if (line < lines && i < n) c[line * n + i] = tile[j][q];
+    }
+  };
+  if (n < 2) return;
+  const int64_t K = n - 1 < kInitTaps ? n - 1 : kInitTaps;
+  // initial sum: head elements 1..K and tail elements n-1-K..n-2 (as distances 1..K)
+  double c0 = 0.0, cn = 0.0, head = 0.0, tail = 0.0;
+  for (int64_t k0 = 0; k0 <= K; k0 += kTileW) {
+    __syncthreads();
+    load(k0);
+    __syncthreads();
+    for (int q = 0; q < kTileW; ++q) {
+      const int64_t i = k0 + q;
+      if (i == 0) c0 = tile[t][q] * gain;
+      else if (i <= K) head = head + zp[i] * (tile[t][q] * gain);
+    }
+  }
+  for (int64_t k0 = (n - 1 - K) / kTileW * kTileW; k0 < n; k0 += kTileW) {
+    __syncthreads();
+    load(k0);
+    __syncthreads();
+    for (int q = 0; q < kTileW; ++q) {
+      const int64_t i = k0 + q;
+      if (i == n - 1) cn = tile[t][q] * gain;
+      else if (i >= n - 1 - K && i < n - 1) tail = tail + zp[n - 1 - i] * (tile[t][q] * gain);
+    }
+  }
+  const double acc = (c0 + z_n * cn) + head + z_n * tail;
+  double prev = acc * (z / (1.0 - z_n * z_n)) + c0;
+  for (int64_t k0 = 0; k0 < n; k0 += kTileW) {
+    __syncthreads();
+    load(k0);
+    __syncthreads();
+    for (int q = 0; q < kTileW; ++q) {
+      const int64_t i = k0 + q;
+      if (i >= n) break;
+      if (i > 0) prev = tile[t][q] * gain + z * prev;
+      tile[t][q] = prev;
+    }
+    __syncthreads();
+    store(k0);
+  }
+  double next = prev * (z / (z - 1.0));
+  for (int64_t k0 = (n - 1) / kTileW * kTileW; k0 >= 0; k0 -= kTileW) {
+    __syncthreads();
+    load(k0);
+    __syncthreads();
+    for (int q = kTileW - 1; q >= 0; --q) {
+      const int64_t i = k0 + q;
+      if (i >= n) continue;
+      if (i < n - 1) next = z * (next - tile[t][q]);
+      tile[t][q] = next;
+    }
+    __syncthreads();
+    store(k0);
+  }
 }
 
 // One interpolation pass along `axis`: in (I0, I1, I2) -> out with that axis n_out long.
@@ -221,19 +330,20 @@ __global__ __launch_bounds__(256) void interp_axis_kernel(const double* __restri
   }
 }
 
-// mm[k] = (min, max) over plane k along `axis` of a (n0, n1, n2) float32 channel; one
-// block per plane.
+// part[k * parts + j] = (min, max) over part j of plane k along `axis` of a (n0, n1, n2)
+// float32 channel; grid (planes, parts).
 __global__ __launch_bounds__(256) void plane_minmax_kernel(const float* __restrict__ in,
                                                            int64_t n0, int64_t n1, int64_t n2,
-                                                           int axis, float2* __restrict__ mm) {
+                                                           int axis, float2* __restrict__ part) {
   __shared__ float smin[4], smax[4];
   const int64_t k = blockIdx.x;
+  const int parts = gridDim.y, j = blockIdx.y;
   const int64_t dims[3] = {n0, n1, n2};
   const int a1 = axis == 0 ? 1 : 0, a2 = axis == 2 ? 1 : 2;
   const int64_t strides[3] = {n1 * n2, n2, 1};
   const int64_t m = dims[a1] * dims[a2];
   float lo = INFINITY, hi = -INFINITY;
-  for (int64_t i = threadIdx.x; i < m; i += blockDim.x) {
+  for (int64_t i = j * (int64_t)blockDim.x + threadIdx.x; i < m; i += (int64_t)parts * blockDim.x) {
     const float v = in[k * strides[axis] + (i / dims[a2]) * strides[a1] + (i % dims[a2]) * strides[a2]];
     lo = fminf(lo, v);
     hi = fmaxf(hi, v);
@@ -250,12 +360,26 @@ __global__ __launch_bounds__(256) void plane_minmax_kernel(const float* __restri
   }
   __syncthreads();
   if (threadIdx.x == 0) {
-    for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
+    for (int w = 1; w < 4; ++w) {
       lo = fminf(lo, smin[w]);
       hi = fmaxf(hi, smax[w]);
     }
-    mm[k] = make_float2(fminf(lo, smin[0]), fmaxf(hi, smax[0]));
+    part[k * parts + j] = make_float2(lo, hi);
   }
+}
+
+// mm[k] = (min, max) over part[k * parts .. k * parts + parts), one thread per plane
+__global__ __launch_bounds__(256) void plane_parts_kernel(const float2* __restrict__ part,
+                                                          int64_t planes, int parts,
+                                                          float2* __restrict__ mm) {
+  const int64_t k = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (k >= planes) return;
+  float lo = INFINITY, hi = -INFINITY;
+  for (int j = 0; j < parts; ++j) {
+    lo = fminf(lo, part[k * parts + j].x);
+    hi = fmaxf(hi, part[k * parts + j].y);
+  }
+  mm[k] = make_float2(lo, hi);
 }
 
 // mm[n] = (min, max) over mm[0 .. n)
@@ -339,7 +463,9 @@ SplinePlan spline_plan(const int64_t* size, const int64_t* new_size, int separat
     int64_t& slot = (k % 2 == 0) ? p.a_elems : p.b_elems;
     slot = std::max(slot, sizes[k]);
   }
-  p.mm_elems = (separate_axis >= 0 ? p.n[separate_axis] : p.n[0]) + 1;
+  // per-plane (min, max) + the whole-volume entry, then the per-part partials
+  const int64_t planes = separate_axis >= 0 ? p.n[separate_axis] : p.n[0];
+  p.mm_elems = planes + 1 + planes * kMinmaxParts;
   return p;
 }
 
@@ -352,7 +478,8 @@ void nonzero_bbox(const float* x, int channels, const int64_t* size, int* bbox, 
   require(size[0] < INT_MAX && size[1] < INT_MAX && size[2] < INT_MAX, "volume axis too long");
   ProfScope prof("preprocess_bbox", 0.0, 4.0 * (double)n * channels, st);
   hipLaunchKernelGGL(bbox_init_kernel, dim3(1), dim3(64), 0, st, bbox);
-  hipLaunchKernelGGL(bbox_kernel, dim3((unsigned)std::min<int64_t>(ceil_div(n, 256), 8192)),
+  hipLaunchKernelGGL(bbox_kernel,
+                     dim3((unsigned)std::min<int64_t>(ceil_div(size[0] * size[1], 4), 8192)),
                      dim3(256), 0, st, x, channels, size[0], size[1], size[2], bbox);
   launch_check("nonzero_bbox");
 }
@@ -432,8 +559,12 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
   const int mm_axis = separate_axis >= 0 ? separate_axis : 0;
   for (int c = 0; c < channels; ++c) {
     const float* xc = x + (int64_t)c * in_vox;
-    hipLaunchKernelGGL(plane_minmax_kernel, dim3((unsigned)size[mm_axis]), dim3(256), 0, st, xc,
-                       size[0], size[1], size[2], mm_axis, mm);
+    const int64_t planes = size[mm_axis];
+    float2* part = mm + planes + 1;
+    hipLaunchKernelGGL(plane_minmax_kernel, dim3((unsigned)planes, kMinmaxParts), dim3(256), 0, st,
+                       xc, size[0], size[1], size[2], mm_axis, part);
+    hipLaunchKernelGGL(plane_parts_kernel, dim3((unsigned)ceil_div(planes, 256)), dim3(256), 0, st,
+                       part, planes, kMinmaxParts, mm);
     if (separate_axis < 0)
       hipLaunchKernelGGL(reduce_minmax_kernel, dim3(1), dim3(64), 0, st, mm, size[0]);
     int64_t d[3] = {size[0] + 2 * p.pad[0], size[1] + 2 * p.pad[1], size[2] + 2 * p.pad[2]};
@@ -444,8 +575,12 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
         const int a = p.axes[k];
         const int64_t lines = d[0] * d[1] * d[2] / d[a];
         const double z_n = std::pow(z, (double)d[a]);
-        hipLaunchKernelGGL(prefilter_kernel, dim3((unsigned)ceil_div(lines, 256)), dim3(256), 0, st,
-                           A, d[0], d[1], d[2], a, z, z_n, gain);
+        if (a == 2)
+          hipLaunchKernelGGL(prefilter_contig_kernel, dim3((unsigned)ceil_div(lines, 256)),
+                             dim3(256), 0, st, A, lines, d[2], z, z_n, gain);
+        else
+          hipLaunchKernelGGL(prefilter_strided_kernel, dim3((unsigned)ceil_div(lines, 256)),
+                             dim3(256), 0, st, A, d[0], d[1], d[2], a, z, z_n, gain);
       }
     }
     double* src = A;
