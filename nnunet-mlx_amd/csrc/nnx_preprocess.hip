@@ -552,8 +552,6 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
   float2* mm = reinterpret_cast<float2*>(B + p.b_elems);
   const int64_t in_vox = size[0] * size[1] * size[2];
   const int64_t out_vox = new_size[0] * new_size[1] * new_size[2];
-  ProfScope prof("preprocess_resample_spline", 0.0,
-                 (double)channels * (4.0 * (in_vox + out_vox) + 16.0 * (p.a_elems + p.b_elems)), st);
   const double z = std::sqrt(3.0) - 2.0;
   const double gain = (1.0 - z) * (1.0 - 1.0 / z);
   const int mm_axis = separate_axis >= 0 ? separate_axis : 0;
@@ -561,20 +559,29 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
     const float* xc = x + (int64_t)c * in_vox;
     const int64_t planes = size[mm_axis];
     float2* part = mm + planes + 1;
-    hipLaunchKernelGGL(plane_minmax_kernel, dim3((unsigned)planes, kMinmaxParts), dim3(256), 0, st,
-                       xc, size[0], size[1], size[2], mm_axis, part);
-    hipLaunchKernelGGL(plane_parts_kernel, dim3((unsigned)ceil_div(planes, 256)), dim3(256), 0, st,
-                       part, planes, kMinmaxParts, mm);
-    if (separate_axis < 0)
-      hipLaunchKernelGGL(reduce_minmax_kernel, dim3(1), dim3(64), 0, st, mm, size[0]);
+    {
+      ProfScope prof("spline_minmax", 0.0, 4.0 * (double)in_vox, st);
+      hipLaunchKernelGGL(plane_minmax_kernel, dim3((unsigned)planes, kMinmaxParts), dim3(256), 0,
+                         st, xc, size[0], size[1], size[2], mm_axis, part);
+      hipLaunchKernelGGL(plane_parts_kernel, dim3((unsigned)ceil_div(planes, 256)), dim3(256), 0,
+                         st, part, planes, kMinmaxParts, mm);
+      if (separate_axis < 0)
+        hipLaunchKernelGGL(reduce_minmax_kernel, dim3(1), dim3(64), 0, st, mm, size[0]);
+    }
     int64_t d[3] = {size[0] + 2 * p.pad[0], size[1] + 2 * p.pad[1], size[2] + 2 * p.pad[2]};
-    hipLaunchKernelGGL(pad_edge_kernel, dim3(blocks_for(d[0] * d[1] * d[2])), dim3(256), 0, st,
-                       xc, size[0], size[1], size[2], p.pad[0], p.pad[1], p.pad[2], A);
+    {
+      const int64_t padded = d[0] * d[1] * d[2];
+      ProfScope prof("spline_pad", 0.0, 4.0 * (double)in_vox + 8.0 * (double)padded, st);
+      hipLaunchKernelGGL(pad_edge_kernel, dim3(blocks_for(padded)), dim3(256), 0, st, xc, size[0],
+                         size[1], size[2], p.pad[0], p.pad[1], p.pad[2], A);
+    }
     if (order == 3) {
       for (int k = 0; k < p.naxes; ++k) {
         const int a = p.axes[k];
         const int64_t lines = d[0] * d[1] * d[2] / d[a];
         const double z_n = std::pow(z, (double)d[a]);
+        // causal and anticausal sweeps: each reads and writes the array once
+        ProfScope prof("spline_prefilter", 0.0, 32.0 * (double)(d[0] * d[1] * d[2]), st);
         if (a == 2)
           hipLaunchKernelGGL(prefilter_contig_kernel, dim3((unsigned)ceil_div(lines, 256)),
                              dim3(256), 0, st, A, lines, d[2], z, z_n, gain);
@@ -591,6 +598,7 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
       od[a] = new_size[a];
       const double ratio = (double)size[a] / (double)new_size[a];
       const int64_t total = od[0] * od[1] * od[2];
+      ProfScope prof("spline_interp", 0.0, 8.0 * (double)(d[0] * d[1] * d[2] + total), st);
       if (order == 3)
         hipLaunchKernelGGL(interp_axis_kernel<3>, dim3(blocks_for(total)), dim3(256), 0, st, src,
                            d[0], d[1], d[2], a, new_size[a], ratio, p.pad[a], dst);
@@ -601,6 +609,8 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
       std::swap(src, dst);
     }
     float* oc = out + (int64_t)c * out_vox;
+    ProfScope prof("spline_finish", 0.0, 8.0 * (double)(d[0] * d[1] * d[2]) + 4.0 * (double)out_vox,
+                   st);
     if (separate_axis < 0) {
       hipLaunchKernelGGL(cast_clip_kernel, dim3(blocks_for(out_vox)), dim3(256), 0, st, src,
                          out_vox, mm + size[0], oc);
