@@ -1,8 +1,9 @@
 """Upstream nnU-Net v2 trained models -> converted model folders (host, torch CPU).
 
-Reference: src/nnunet_mlx/storage/upstream.py:94-298 (``load_upstream_checkpoint``,
-``detect_upstream_folds``, ``convert_trained_model``) and src/nnunet_mlx/storage/weights.py
-:48-192 (``map_key_and_layout``, ``convert_state_dict``).
+Reference: src/nnunet_mlx/storage/upstream.py:94-405 (``load_upstream_checkpoint``,
+``detect_upstream_folds``, ``convert_trained_model``, ``resolve_results_folder``,
+``cached_conversion``) and src/nnunet_mlx/storage/weights.py:48-192
+(``map_key_and_layout``, ``convert_state_dict``).
 
 An upstream trained model folder holds ``plans.json``, ``dataset.json`` and
 ``fold_<f>/checkpoint_final.pth`` (a torch pickle with ``network_weights``,
@@ -19,6 +20,7 @@ beside tensors and containers.
 from __future__ import annotations
 
 import json
+import os
 import re
 import shutil
 import tempfile
@@ -340,3 +342,110 @@ def convert_trained_model(source: str | Path, destination: str | Path, *,
         shutil.rmtree(staging, ignore_errors=True)
         raise
     return ConversionResult(target, configuration, first.trainer_name, tuple(selected))
+
+
+RESULTS_VARIABLE = "nnUNet_results"
+CACHE_VARIABLE = "NNUNET_MLX_CACHE"
+SOURCE_MARKER = ".source"
+
+
+def resolve_results_folder(dataset: str, *, configuration: str, trainer: str = "nnUNetTrainer",
+                           plans: str = "nnUNetPlans", results: str | Path | None = None) -> Path:
+    """``<results>/<dataset>/<trainer>__<plans>__<configuration>``, nnU-Net's results layout.
+
+    ``dataset`` is a full name (``Dataset003_Liver``) or a numeric ID, which must match
+    exactly one ``DatasetNNN_*`` folder.  ``results`` defaults to ``$nnUNet_results``.
+    Reference: src/nnunet_mlx/storage/upstream.py:298-323."""
+    base = results if results is not None else os.environ.get(RESULTS_VARIABLE)
+    if not base:
+        raise ContractError(f"set {RESULTS_VARIABLE}, or pass a trained model folder with -m")
+    root = Path(base).expanduser()
+    if dataset.isdigit():
+        prefix = f"Dataset{int(dataset):03d}_"
+        names = sorted(p.name for p in root.glob(prefix + "*")
+                       if p.is_dir() and len(p.name) > len(prefix))
+        if len(names) != 1:
+            raise ContractError(f"expected one {prefix}* folder in {root}, found {len(names)}")
+        dataset = names[0]
+    folder = root / dataset / f"{trainer}__{plans}__{configuration}"
+    if not folder.is_dir():
+        raise ContractError(f"trained model folder does not exist: {folder}")
+    return folder
+
+
+def conversion_is_current(target: Path, source: Path, folds: Sequence[int | str],
+                          checkpoint_name: str) -> bool:
+    """Whether ``target`` is a complete conversion of ``source`` as it is now: same source
+    folder, same conversion contract, identical plans/dataset JSON, the same fold set, each
+    source checkpoint with its recorded size and modification time, every payload file
+    present.  Reference: src/nnunet_mlx/storage/upstream.py:366-405."""
+    marker = target / SOURCE_MARKER
+    try:
+        if not marker.is_file() or marker.read_text(encoding="utf-8").strip() != str(source):
+            return False
+        manifest = read_json_object(target / CONVERSION_FILENAME)
+        plans = read_json_object(source / "plans.json")
+        dataset = read_json_object(source / "dataset.json")
+        if (manifest.get("schema_version") != CONVERSION_SCHEMA
+                or manifest.get("conversion_contract_version") != CONVERSION_CONTRACT_VERSION
+                or manifest.get("source_plans") != plans or manifest.get("source_dataset") != dataset
+                or read_json_object(target / "plans.json") != plans
+                or read_json_object(target / "dataset.json") != dataset):
+            return False
+        entries = manifest.get("folds")
+        if not isinstance(entries, list) or not all(isinstance(e, Mapping) for e in entries):
+            return False
+        recorded = {e.get("fold"): e for e in entries}
+        if len(recorded) != len(entries) or set(recorded) != set(folds):
+            return False
+        for fold in folds:
+            entry = recorded[fold]
+            stat = (source / f"fold_{fold}" / checkpoint_name).stat()
+            if (entry.get("source_checkpoint"), entry.get("source_size_bytes"),
+                    entry.get("source_mtime_ns")) != (checkpoint_name, stat.st_size, stat.st_mtime_ns):
+                return False
+            payload = target / f"fold_{fold}" / CONVERTED_CHECKPOINT
+            if not ((payload / "weights.safetensors").is_file() and (payload / "state.json").is_file()):
+                return False
+    except (ContractError, OSError, ValueError):
+        return False
+    return True
+
+
+def cached_conversion(trained_folder: str | Path, *, folds: Sequence[int | str] | None = None,
+                      checkpoint_name: str = UPSTREAM_CHECKPOINT,
+                      cache: str | Path | None = None) -> Path:
+    """A converted copy of ``trained_folder``, converting only when no current one exists.
+
+    Entries live at ``<cache>/converted/<dataset folder>/<model folder>`` with ``cache``
+    defaulting to ``$NNUNET_MLX_CACHE`` or ``~/.cache/nnunet-mlx``; every available fold is
+    converted so later fold selections reuse the entry.  A stale entry (see
+    ``conversion_is_current``) is deleted and rebuilt.  Symlinked cache parents or entries
+    are refused, so the deletion never leaves the cache.
+    Reference: src/nnunet_mlx/storage/upstream.py:326-363."""
+    from nnunet_mlx.model.folder import validate_folds
+
+    source = Path(os.path.normpath(str(Path(trained_folder).absolute())))
+    if not source.name or not source.parent.name:
+        raise ContractError("trained folder needs dataset and model directory names")
+    available = detect_upstream_folds(source, checkpoint_name=checkpoint_name)
+    if folds is not None:
+        absent = [f for f in validate_folds(folds) if f not in available]
+        if absent:
+            raise ContractError(f"folds {absent} have no {checkpoint_name} in {source}")
+    root = Path(cache if cache is not None else
+                os.environ.get(CACHE_VARIABLE, "~/.cache/nnunet-mlx")).expanduser()
+    parent = root / "converted" / source.parent.name
+    parent.mkdir(parents=True, exist_ok=True)
+    if parent.resolve() != root.resolve() / "converted" / source.parent.name:
+        raise ContractError(f"conversion cache has a symlinked parent: {parent}")
+    target = parent / source.name
+    if target.is_symlink():
+        raise ContractError(f"conversion cache entry must not be a symlink: {target}")
+    if conversion_is_current(target, source, available, checkpoint_name):
+        return target
+    if target.exists():
+        shutil.rmtree(target)
+    convert_trained_model(source, target, folds=available, checkpoint_name=checkpoint_name)
+    (target / SOURCE_MARKER).write_text(f"{source}\n", encoding="utf-8")
+    return target

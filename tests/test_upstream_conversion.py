@@ -280,3 +280,63 @@ def test_converted_folder_runs_on_the_device(tmp_path):
     assert bundle.mirroring_axes == (0, 1, 2) and bundle.folds == (0,)
     for model in bundle.models:
         model.close()
+
+
+def test_resolve_results_folder(tmp_path, monkeypatch):
+    model = tmp_path / "Dataset003_Liver" / "nnUNetTrainer__nnUNetPlans__3d_fullres"
+    model.mkdir(parents=True)
+    assert upstream.resolve_results_folder("3", configuration="3d_fullres", results=tmp_path) == model
+    monkeypatch.setenv("nnUNet_results", str(tmp_path))
+    assert upstream.resolve_results_folder("Dataset003_Liver", configuration="3d_fullres") == model
+    with pytest.raises(ContractError, match="does not exist"):
+        upstream.resolve_results_folder("3", configuration="2d")
+    (tmp_path / "Dataset003_Other").mkdir()
+    with pytest.raises(ContractError, match="expected one"):
+        upstream.resolve_results_folder("3", configuration="3d_fullres")
+    monkeypatch.delenv("nnUNet_results")
+    with pytest.raises(ContractError, match="nnUNet_results"):
+        upstream.resolve_results_folder("3", configuration="3d_fullres")
+
+
+def test_cached_conversion_reuses_and_rebuilds(tmp_path):
+    import os
+
+    source = tmp_path / "results" / "Dataset003_Liver" / "nnUNetTrainer__nnUNetPlans__3d_fullres"
+    source.parent.mkdir(parents=True)
+    write_upstream_folder(source, PLAIN, folds=(0, 1))
+    cache = tmp_path / "cache"
+    entry = upstream.cached_conversion(source, folds=(1,), cache=cache)
+    assert entry == cache / "converted" / "Dataset003_Liver" / source.name
+    weights = entry / "fold_0" / "checkpoint_final" / "weights.safetensors"
+    assert weights.is_file()          # every available fold is converted
+    stamp = weights.stat().st_mtime_ns
+    marker = (entry / ".source").read_text()
+    assert upstream.cached_conversion(source, cache=cache) == entry
+    assert weights.stat().st_mtime_ns == stamp and (entry / ".source").read_text() == marker
+    # a retrained fold (new modification time) makes the entry stale
+    ckpt_path = source / "fold_1" / "checkpoint_final.pth"
+    st = ckpt_path.stat()
+    os.utime(ckpt_path, ns=(st.st_atime_ns, st.st_mtime_ns + 10**9))
+    assert not upstream.conversion_is_current(entry, source, (0, 1), "checkpoint_final.pth")
+    upstream.cached_conversion(source, cache=cache)
+    assert upstream.conversion_is_current(entry, source, (0, 1), "checkpoint_final.pth")
+    # so does edited plans JSON, and a missing payload file
+    plans = json.loads((source / "plans.json").read_text())
+    plans["plans_name"] = "edited"
+    (source / "plans.json").write_text(json.dumps(plans))
+    assert not upstream.conversion_is_current(entry, source, (0, 1), "checkpoint_final.pth")
+    upstream.cached_conversion(source, cache=cache)
+    assert json.loads((entry / "plans.json").read_text())["plans_name"] == "edited"
+    (entry / "fold_0" / "checkpoint_final" / "state.json").unlink()
+    assert not upstream.conversion_is_current(entry, source, (0, 1), "checkpoint_final.pth")
+    with pytest.raises(ContractError, match="have no"):
+        upstream.cached_conversion(source, folds=(4,), cache=cache)
+    # a symlinked entry is refused rather than deleted through
+    elsewhere = tmp_path / "elsewhere"
+    elsewhere.mkdir()
+    os.symlink(elsewhere, cache / "converted" / "Dataset003_Liver" / "linked")
+    linked_source = source.parent / "linked"
+    write_upstream_folder(linked_source, PLAIN, folds=(0,))
+    with pytest.raises(ContractError, match="symlink"):
+        upstream.cached_conversion(linked_source, cache=cache)
+    assert elsewhere.is_dir()
