@@ -272,6 +272,23 @@ int nnx_tconv3d_bf16(const float* d_x, int cin, const void* d_packed, float scal
 int nnx_restore_labels(const void* d_logits, int half, int classes, const int* src_shape,
                        const int* dst_shape, uint16_t* d_labels, void* stream);
 
+/* Restoration along the plans' spline resampler, for the cases the trilinear entry does not
+ * take (separate-axis resampling with order_z 0, or order 3): each class of the
+ * channels-last logits (src_shape, classes) is resampled to dst_shape as
+ * nnx_resample_spline does (order 1 or 3, separate_axis -1 or 0..2), rounded once to
+ * float32 — or to float16 when half != 0 (float16 logits) — and folded into a
+ * first-maximum argmax (strict ">", ties keep the earliest class) written as uint16 labels.
+ * One class at a time through a device workspace of
+ * nnx_restore_labels_spline_workspace bytes (0 = invalid shapes).  Replaces the host
+ * restoration resample_class_logits_argmax_parallel / separate_plane_argmax
+ * (src/nnunet_mlx/prediction/restore.py:28-158) over resample_probabilities_or_data
+ * (src/nnunet_mlx/data/resampling.py:87-172). */
+size_t nnx_restore_labels_spline_workspace(const int* src_shape, const int* dst_shape,
+                                           int separate_axis);
+int nnx_restore_labels_spline(const void* d_logits, int half, int classes, const int* src_shape,
+                              const int* dst_shape, int order, int separate_axis, void* d_work,
+                              size_t work_bytes, uint16_t* d_labels, void* stream);
+
 /* Raw-case preprocessing on the device (volumes are (C, X, Y, Z) float32, Z fastest, in
  * the array axis order of the raw image).
  *

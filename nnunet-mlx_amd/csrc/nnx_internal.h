@@ -185,7 +185,14 @@ void crop_normalize(const float* x, int channels, const int64_t* size, const int
 size_t resample_spline_workspace(const int64_t* size, const int64_t* new_size, int separate_axis);
 void resample_spline(const float* x, int channels, const int64_t* size, const int64_t* new_size,
                      int order, int separate_axis, int order_z, void* work, size_t work_bytes,
-                     float* out, hipStream_t st);
+                     float* out, hipStream_t st, bool round_half = false);
+// Class-logit restoration along a spline plan: each class of channels-last logits
+// (src, classes) resampled like resample_spline (rounded to float16 when `half`), then the
+// first-maximum argmax into uint16 labels (dst); one class at a time through `work`.
+size_t restore_labels_spline_workspace(const int* src, const int* dst, int separate_axis);
+void restore_labels_spline(const void* logits, bool half, int classes, const int* src,
+                           const int* dst, int order, int separate_axis, void* work,
+                           size_t work_bytes, uint16_t* labels, hipStream_t st);
 // `item_voxels` = voxels per batch item (to index the pending norm's parameters).
 void conv1x1(const float* x, int cin, const float* w, const float* bias, float* y,
              int64_t voxels, int cout, hipStream_t st, const PendingNorm& nx = {},

@@ -30,6 +30,7 @@
 // anticausal) and each interpolation pass reads and writes its float64 array once; the
 // crop/normalise pass reads and writes 4 B per kept voxel.
 
+#include <hip/hip_fp16.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
@@ -397,17 +398,28 @@ __global__ __launch_bounds__(64) void reduce_minmax_kernel(float2* mm, int64_t n
   if (threadIdx.x == 0) mm[n] = make_float2(lo, hi);
 }
 
-// whole-volume resize: out = clip(float(v), min, max)
+// One rounding of a float64 result: to float32, or to float16 (nearest even) when HALF,
+// returned as float32.
+template <bool HALF>
+__device__ inline float round_result(double v) {
+  if constexpr (HALF) return (float)(_Float16)v;  // correctly rounded (integer sequence)
+  else return (float)v;
+}
+
+// whole-volume resize: out = clip(round(v), min, max); the bounds are values of the input,
+// so clipping before or after the monotone rounding gives the same result
+template <bool HALF>
 __global__ __launch_bounds__(256) void cast_clip_kernel(const double* __restrict__ in, int64_t n,
                                                         const float2* __restrict__ mm,
                                                         float* __restrict__ out) {
   const float2 b = *mm;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
        e += (int64_t)gridDim.x * blockDim.x)
-    out[e] = fminf(fmaxf((float)in[e], b.x), b.y);
+    out[e] = fminf(fmaxf(round_result<HALF>(in[e]), b.x), b.y);
 }
 
-// separate axis: out[.. o ..] = float(clip_k(inter[.. k ..])), k = nearest source plane of o
+// separate axis: out[.. o ..] = round(clip_k(inter[.. k ..])), k = nearest source plane of o
+template <bool HALF>
 __global__ __launch_bounds__(256) void plane_clip_nearest_kernel(
     const double* __restrict__ inter, int64_t d0, int64_t d1, int64_t d2, int axis,
     int64_t n_new, double ratio, const float2* __restrict__ mm, float* __restrict__ out) {
@@ -427,7 +439,7 @@ __global__ __launch_bounds__(256) void plane_clip_nearest_kernel(
     k = min(max(k, (int64_t)0), n_old - 1);
     const float2 b = mm[k];
     const double v = fmin(fmax(inter[row + k * in_stride], (double)b.x), (double)b.y);
-    out[e] = (float)v;
+    out[e] = round_result<HALF>(v);
   }
 }
 
@@ -535,7 +547,7 @@ size_t resample_spline_workspace(const int64_t* size, const int64_t* new_size, i
 
 void resample_spline(const float* x, int channels, const int64_t* size, const int64_t* new_size,
                      int order, int separate_axis, int order_z, void* work, size_t work_bytes,
-                     float* out, hipStream_t st) {
+                     float* out, hipStream_t st, bool round_half) {
   require(x && out && size && new_size, "resampling pointers must not be null");
   require(channels >= 1, "resampling needs at least one channel");
   for (int a = 0; a < 3; ++a)
@@ -612,13 +624,14 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
     ProfScope prof("spline_finish", 0.0, 8.0 * (double)(d[0] * d[1] * d[2]) + 4.0 * (double)out_vox,
                    st);
     if (separate_axis < 0) {
-      hipLaunchKernelGGL(cast_clip_kernel, dim3(blocks_for(out_vox)), dim3(256), 0, st, src,
-                         out_vox, mm + size[0], oc);
+      auto kernel = round_half ? cast_clip_kernel<true> : cast_clip_kernel<false>;
+      hipLaunchKernelGGL(kernel, dim3(blocks_for(out_vox)), dim3(256), 0, st, src, out_vox,
+                         mm + size[0], oc);
     } else {
       const int a = separate_axis;
-      hipLaunchKernelGGL(plane_clip_nearest_kernel, dim3(blocks_for(out_vox)), dim3(256), 0, st,
-                         src, d[0], d[1], d[2], a, new_size[a],
-                         (double)size[a] / (double)new_size[a], mm, oc);
+      auto kernel = round_half ? plane_clip_nearest_kernel<true> : plane_clip_nearest_kernel<false>;
+      hipLaunchKernelGGL(kernel, dim3(blocks_for(out_vox)), dim3(256), 0, st, src, d[0], d[1],
+                         d[2], a, new_size[a], (double)size[a] / (double)new_size[a], mm, oc);
     }
   }
   launch_check("resample_spline");

@@ -20,6 +20,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdint>
 
@@ -94,7 +95,87 @@ __global__ __launch_bounds__(256) void restore_argmax_kernel(const void* __restr
   }
 }
 
+// out[v] = class c of channels-last logits (n voxels, `classes` per voxel) as float32
+template <bool HALF>
+__global__ __launch_bounds__(256) void extract_class_kernel(const void* __restrict__ logits,
+                                                            int classes, int c, int64_t n,
+                                                            float* __restrict__ out) {
+  for (int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; v < n;
+       v += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i = v * classes + c;
+    if constexpr (HALF) out[v] = __half2float(static_cast<const __half*>(logits)[i]);
+    else out[v] = static_cast<const float*>(logits)[i];
+  }
+}
+
+// running first-maximum argmax: class 0 initialises, later classes win only when strictly
+// greater (ties keep the earliest class)
+__global__ __launch_bounds__(256) void argmax_update_kernel(const float* __restrict__ value,
+                                                            int64_t n, int c,
+                                                            float* __restrict__ best,
+                                                            uint16_t* __restrict__ labels) {
+  for (int64_t v = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; v < n;
+       v += (int64_t)gridDim.x * blockDim.x) {
+    const float x = value[v];
+    if (c == 0) {
+      best[v] = x;
+      labels[v] = 0;
+    } else if (x > best[v]) {
+      best[v] = x;
+      labels[v] = (uint16_t)c;
+    }
+  }
+}
+
+int grid_for(int64_t n) { return (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 1 << 20)); }
+
+int64_t align256(int64_t bytes) { return ceil_div(bytes, 256) * 256; }
+
 }  // namespace
+
+size_t restore_labels_spline_workspace(const int* src, const int* dst, int separate_axis) {
+  const int64_t s[3] = {src[0], src[1], src[2]}, d[3] = {dst[0], dst[1], dst[2]};
+  const int64_t n_src = s[0] * s[1] * s[2], n_dst = d[0] * d[1] * d[2];
+  return (size_t)(align256(4 * n_src) + 2 * align256(4 * n_dst)) +
+         resample_spline_workspace(s, d, separate_axis);
+}
+
+void restore_labels_spline(const void* logits, bool half, int classes, const int* src,
+                           const int* dst, int order, int separate_axis, void* work,
+                           size_t work_bytes, uint16_t* labels, hipStream_t st) {
+  require(logits && labels && src && dst && work, "restoration pointers must not be null");
+  require(classes >= 1 && classes <= 65536, "restoration supports 1..65536 classes");
+  for (int i = 0; i < 3; ++i)
+    require(src[i] >= 1 && dst[i] >= 1, "restoration shapes must be positive");
+  require(separate_axis >= -1 && separate_axis < 3, "separate axis must be -1, 0, 1 or 2");
+  require(work_bytes >= restore_labels_spline_workspace(src, dst, separate_axis),
+          "restoration workspace too small");
+  const int64_t s[3] = {src[0], src[1], src[2]}, d[3] = {dst[0], dst[1], dst[2]};
+  const int64_t n_src = s[0] * s[1] * s[2], n_dst = d[0] * d[1] * d[2];
+  char* base = static_cast<char*>(work);
+  float* channel = reinterpret_cast<float*>(base);
+  float* value = reinterpret_cast<float*>(base + align256(4 * n_src));
+  float* best = reinterpret_cast<float*>(base + align256(4 * n_src) + align256(4 * n_dst));
+  void* spline_work = base + align256(4 * n_src) + 2 * align256(4 * n_dst);
+  const size_t spline_bytes = work_bytes - (size_t)(align256(4 * n_src) + 2 * align256(4 * n_dst));
+  for (int c = 0; c < classes; ++c) {
+    {
+      ProfScope prof("restore_extract", 0.0, (half ? 2.0 : 4.0) * classes * n_src + 4.0 * n_src, st);
+      if (half)
+        hipLaunchKernelGGL(extract_class_kernel<true>, dim3(grid_for(n_src)), dim3(256), 0, st,
+                           logits, classes, c, n_src, channel);
+      else
+        hipLaunchKernelGGL(extract_class_kernel<false>, dim3(grid_for(n_src)), dim3(256), 0, st,
+                           logits, classes, c, n_src, channel);
+    }
+    resample_spline(channel, 1, s, d, order, separate_axis, 0, spline_work, spline_bytes, value,
+                    st, half);
+    ProfScope prof("restore_argmax_update", 0.0, 4.0 * n_dst + (c ? 8.0 : 6.0) * n_dst, st);
+    hipLaunchKernelGGL(argmax_update_kernel, dim3(grid_for(n_dst)), dim3(256), 0, st, value,
+                       n_dst, c, best, labels);
+  }
+  launch_check("restore_labels_spline");
+}
 
 void restore_labels(const void* logits, bool half, int classes, const int* src, const int* dst,
                     uint16_t* labels, hipStream_t st) {

@@ -1143,6 +1143,24 @@ int nnx_restore_labels(const void* d_logits, int half, int classes, const int* s
   });
 }
 
+size_t nnx_restore_labels_spline_workspace(const int* src_shape, const int* dst_shape,
+                                           int separate_axis) {
+  if (!src_shape || !dst_shape || separate_axis < -1 || separate_axis > 2) return 0;
+  for (int a = 0; a < 3; ++a)
+    if (src_shape[a] < 1 || dst_shape[a] < 1) return 0;
+  return restore_labels_spline_workspace(src_shape, dst_shape, separate_axis);
+}
+
+int nnx_restore_labels_spline(const void* d_logits, int half, int classes, const int* src_shape,
+                              const int* dst_shape, int order, int separate_axis, void* d_work,
+                              size_t work_bytes, uint16_t* d_labels, void* stream) {
+  return guarded([&] {
+    require(src_shape && dst_shape, "null argument");
+    restore_labels_spline(d_logits, half != 0, classes, src_shape, dst_shape, order,
+                          separate_axis, d_work, work_bytes, d_labels, as_stream(stream));
+  });
+}
+
 int nnx_nonzero_bbox(const float* d_data, int channels, const int64_t* size, int* d_bbox,
                      void* stream) {
   return guarded([&] { nonzero_bbox(d_data, channels, size, d_bbox, as_stream(stream)); });

@@ -184,6 +184,12 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     "nnx_restore_labels": (
         ctypes.c_int, [c_void_p, ctypes.c_int, ctypes.c_int, c_int_p, c_int_p, c_void_p, c_void_p]
     ),
+    "nnx_restore_labels_spline_workspace": (ctypes.c_size_t, [c_int_p, c_int_p, ctypes.c_int]),
+    "nnx_restore_labels_spline": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, ctypes.c_int, c_int_p, c_int_p, ctypes.c_int, ctypes.c_int,
+         c_void_p, ctypes.c_size_t, c_void_p, c_void_p],
+    ),
     "nnx_nonzero_bbox": (ctypes.c_int, [c_void_p, ctypes.c_int, c_i64_p, c_void_p, c_void_p]),
     "nnx_crop_normalize": (
         ctypes.c_int,

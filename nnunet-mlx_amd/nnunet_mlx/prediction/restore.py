@@ -12,6 +12,12 @@ the policy), or the spline resampler ``resample_data_or_seg_to_shape`` with ``or
 and no separate-axis resampling.  Other cases return ``None`` so the caller restores on
 the host.  float16 logits (the runner's fp16 accumulation) are rounded to float16 after
 the interpolation, as the reference's host path stores them.
+
+``restore_class_labels_device`` adds the cases the reference leaves to its host
+restoration (src/nnunet_mlx/prediction/restore.py:28-158): spline plans with separate-axis
+resampling (``order_z`` 0) or ``order`` 3 run ``nnx_restore_labels_spline`` — each class
+resampled as ``resample_probabilities_or_data`` does (float64, clipped, one rounding to
+the logits' precision) and folded into the first-maximum argmax on the device.
 """
 
 from __future__ import annotations
@@ -121,3 +127,78 @@ def resample_device_logits_argmax(logits: torch.Tensor, new_shape: Sequence[int]
     if return_device:
         return labels
     return np.ascontiguousarray(labels.cpu().numpy().view(np.uint16))
+
+
+def device_spline_restore_supported(source_shape: Sequence[int], new_shape: Sequence[int],
+                                    contract: ResamplingContract, *, classes: int) -> bool:
+    """Whether ``nnx_restore_labels_spline`` covers the plans' probability resampling:
+    the spline resampler with order 1 or 3 and, when an axis is resampled separately,
+    nearest indices along it (``order_z`` 0)."""
+    target = _target_shape(new_shape)
+    if len(source_shape) != 3 or classes < 1 or classes > np.iinfo(np.uint16).max + 1:
+        return False
+    _validate_index_range((classes, *source_shape), target)
+    return (contract.function_name == "resample_data_or_seg_to_shape"
+            and contract.order in (1, 3) and contract.order_z == 0)
+
+
+def resample_class_logits_argmax_spline_device(logits: torch.Tensor, new_shape: Sequence[int], *,
+                                               order: int, separate_axis: int | None,
+                                               out: torch.Tensor | None = None) -> torch.Tensor:
+    """Channels-last (D, H, W, C) float32/float16 device logits -> (D', H', W') uint16
+    first-maximum labels along the spline resampler (``separate_axis`` None: whole volume)."""
+    target = _target_shape(new_shape)
+    if logits.ndim != 4 or logits.dtype not in (torch.float32, torch.float16):
+        raise ContractError("restoration requires non-empty float32 or float16 (D,H,W,C) logits")
+    if logits.device.type != "cuda":
+        raise ContractError("device restoration requires logits on the GPU")
+    classes = int(logits.shape[-1])
+    if classes < 1 or classes > np.iinfo(np.uint16).max + 1 or logits.numel() == 0:
+        raise ContractError("restoration requires 1..65536 classes and a non-empty grid")
+    if order not in (1, 3):
+        raise ContractError("device spline restoration supports orders 1 and 3")
+    _validate_index_range(logits.shape, target)
+    axis = -1 if separate_axis is None else int(separate_axis)
+    logits = logits.contiguous()
+    if out is None:
+        out = torch.empty(target, dtype=torch.uint16, device=logits.device)
+    elif tuple(out.shape) != target or out.dtype != torch.uint16 or not out.is_contiguous():
+        raise ContractError("restoration output must be a contiguous uint16 target-shape tensor")
+    lib = _native.load()
+    src = _native.ints(logits.shape[:3])
+    dst = _native.ints(target)
+    size = lib.nnx_restore_labels_spline_workspace(src, dst, axis)
+    if size == 0:
+        raise ContractError("invalid restoration shapes")
+    work = torch.empty(size, dtype=torch.uint8, device=logits.device)
+    _native.check(lib.nnx_restore_labels_spline(
+        logits.data_ptr(), 1 if logits.dtype == torch.float16 else 0, classes, src, dst, order,
+        axis, work.data_ptr(), size, out.data_ptr(), _native.stream_handle(logits.device)),
+        "nnx_restore_labels_spline")
+    return out
+
+
+def restore_class_labels_device(logits: torch.Tensor, new_shape: Sequence[int],
+                                current_spacing: Sequence[float], new_spacing: Sequence[float],
+                                contract: ResamplingContract) -> torch.Tensor | None:
+    """Device uint16 labels on the target grid for every spline plan: the trilinear entry
+    where the reference's fused path applies, the spline entry for separate-axis or
+    order-3 plans (the reference's host restoration); ``None`` for other plans."""
+    if logits.ndim != 4 or logits.dtype not in (torch.float32, torch.float16):
+        raise ContractError("restoration requires float32 or float16 (D,H,W,C) logits")
+    labels = resample_device_logits_argmax(logits, new_shape, current_spacing, new_spacing,
+                                           contract, return_device=True)
+    if labels is not None:
+        return labels
+    classes = int(logits.shape[-1])
+    source = tuple(int(v) for v in logits.shape[:3])
+    if not device_spline_restore_supported(source, new_shape, contract, classes=classes):
+        return None
+    separate, axis = separate_z_axis(
+        validate_spacing(current_spacing, name="current spacing"),
+        validate_spacing(new_spacing, name="new spacing"),
+        force=contract.force_separate_z,
+        threshold=contract.separate_z_anisotropy_threshold,
+    )
+    return resample_class_logits_argmax_spline_device(
+        logits, new_shape, order=contract.order, separate_axis=axis if separate else None)

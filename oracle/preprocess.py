@@ -155,16 +155,24 @@ def nearest_axis_indices(old: int, new: int) -> np.ndarray:
 
 
 def resample_data(data: np.ndarray, new_shape, *, order: int = 3, order_z: int = 0,
-                  separate_axis: int | None = None) -> np.ndarray:
-    """(C, X, Y, Z) float32 -> (C, *new_shape) float32 along the spline plan."""
+                  separate_axis: int | None = None, dtype=np.float32) -> np.ndarray:
+    """(C, X, Y, Z) float32 -> (C, *new_shape) float32 along the spline plan.
+
+    ``dtype=np.float16`` is the reference's float16-logit case
+    (src/nnunet_mlx/data/resampling.py:133, 484-501): the float64 result is rounded once
+    to float16 and returned as float32."""
     data = np.asarray(data)
     new_shape = tuple(int(s) for s in new_shape)
     if data.shape[1:] == new_shape:
-        return data.astype(np.float32)
+        return data.astype(dtype).astype(np.float32)
     out = np.empty((data.shape[0], *new_shape), dtype=np.float32)
     for ch in range(data.shape[0]):
         if separate_axis is None:
-            out[ch] = resize_spline(data[ch].astype(np.float32), new_shape, order)
+            if dtype == np.float32:
+                out[ch] = resize_spline(data[ch].astype(np.float32), new_shape, order)
+            else:
+                out[ch] = resize_spline(data[ch].astype(np.float64), new_shape, order,
+                                        dtype=np.float64).astype(dtype)
             continue
         axis = separate_axis
         plane_shape = tuple(s for i, s in enumerate(new_shape) if i != axis)
@@ -180,5 +188,5 @@ def resample_data(data: np.ndarray, new_shape, *, order: int = 3, order_z: int =
         if order_z != 0:
             raise ValueError("order_z 0 is restated")
         idx = nearest_axis_indices(inter_shape[axis], new_shape[axis])
-        out[ch] = np.take(inter, idx, axis=axis).astype(np.float32)
+        out[ch] = np.take(inter, idx, axis=axis).astype(dtype)
     return out

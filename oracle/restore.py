@@ -102,3 +102,20 @@ def brute_force_labels(logits: np.ndarray, target: tuple[int, int, int]) -> np.n
                         best, label = value, k
                 out[z, y, x] = label
     return out
+
+
+def restore_labels_spline(logits: np.ndarray, target: tuple[int, int, int], *, order: int,
+                          separate_axis: int | None) -> tuple[np.ndarray, np.ndarray]:
+    """The reference's host restoration for spline plans
+    (src/nnunet_mlx/prediction/restore.py:28-158 over
+    src/nnunet_mlx/data/resampling.py:87-172): each class of channels-last (D, H, W, C)
+    logits resampled by the spline plan (``preprocess.resample_data``; float16 logits
+    rounded to float16), then the first-maximum argmax.  Returns (labels uint16, the
+    resampled (C, D', H', W') float32 values)."""
+    from oracle.preprocess import resample_data
+
+    values = np.moveaxis(np.asarray(logits), -1, 0)
+    dtype = np.float16 if values.dtype == np.float16 else np.float32
+    resampled = resample_data(values.astype(np.float32), target, order=order,
+                              separate_axis=separate_axis, dtype=dtype)
+    return np.argmax(resampled, axis=0).astype(np.uint16), resampled

@@ -78,3 +78,67 @@ def test_restore_policy_dispatch(device):
                                          auto) is None
     assert resample_device_logits_argmax(logits, (7, 9, 12), (4.0, 1.0, 1.0), (4.0, 1.0, 1.0),
                                          order1) is not None
+
+
+SPLINE_CASES = [
+    ((5, 9, 7), (12, 6, 11), 3, 1, 0),        # separate axis 0, upsampled along it
+    ((11, 6, 9), (7, 13, 9), 4, 1, 1),        # separate axis 1, downsampled along it
+    ((8, 10, 5), (16, 12, 3), 2, 1, 2),
+    ((6, 7, 8), (9, 5, 12), 3, 3, None),      # order 3, whole volume
+    ((6, 20, 18), (15, 31, 27), 3, 3, 0),     # order 3 in-plane, separate axis 0
+    ((24, 40, 40), (60, 52, 52), 3, 1, 0),    # liver-like anisotropic restoration
+]
+
+
+def near_tie(values, got, ref, dtype):
+    """Voxels where the device and oracle winners differ by at most one rounding step of
+    the logits' precision (both evaluate the same float64 sum; one rounding may differ)."""
+    flat = values.reshape(values.shape[0], -1)
+    g, r = got.reshape(-1).astype(np.int64), ref.reshape(-1).astype(np.int64)
+    idx = np.nonzero(g != r)[0]
+    a, b = flat[g[idx], idx], flat[r[idx], idx]
+    step = np.spacing(np.abs(b).astype(dtype)).astype(np.float32)
+    return bool((np.abs(a - b) <= step).all())
+
+
+@pytest.mark.parametrize("source,target,classes,order,axis", SPLINE_CASES, ids=str)
+@pytest.mark.parametrize("dtype", [np.float32, np.float16], ids=["f32", "f16"])
+def test_spline_restore_labels_match_oracle(device, source, target, classes, order, axis, dtype):
+    from nnunet_mlx.prediction.restore import resample_class_logits_argmax_spline_device
+    from oracle.restore import restore_labels_spline
+
+    print(f"spline restore {source} -> {target} K={classes} order {order} axis {axis} "
+          f"{np.dtype(dtype).name}", flush=True)
+    rng = np.random.default_rng(sum(source) + 7 * classes + order)
+    logits = (rng.standard_normal((*source, classes)) * 3).astype(dtype)
+    got = resample_class_logits_argmax_spline_device(torch.from_numpy(logits).to(device), target,
+                                                     order=order, separate_axis=axis)
+    got = got.cpu().numpy().view(np.uint16)
+    ref, values = restore_labels_spline(logits, target, order=order, separate_axis=axis)
+    assert got.shape == tuple(target)
+    assert (got == ref).mean() >= 0.9999
+    assert near_tie(values, got, ref, dtype)
+
+
+def test_restore_class_labels_device_policy(device):
+    """Separate-axis plans restore on the device through the spline entry; the trilinear
+    entry keeps the cases the reference's fused path takes; other plans return None."""
+    from nnunet_mlx.prediction.restore import restore_class_labels_device
+    from oracle.restore import restore_labels_spline
+
+    rng = np.random.default_rng(11)
+    logits = rng.standard_normal((10, 16, 16, 3)).astype(np.float32)
+    dev = torch.from_numpy(logits).to(device)
+    spline = ResamplingContract("resample_data_or_seg_to_shape", 1, 0, None)
+    # 2.5 mm slices -> 1 mm: anisotropic, separate axis 0
+    got = restore_class_labels_device(dev, (25, 20, 20), (2.5, 0.8, 0.8), (1.0, 0.64, 0.64), spline)
+    ref, _ = restore_labels_spline(logits, (25, 20, 20), order=1, separate_axis=0)
+    assert (got.cpu().numpy().view(np.uint16) == ref).mean() >= 0.9999
+    got = restore_class_labels_device(dev, (12, 20, 20), (1.0, 1.0, 1.0), (0.8, 0.8, 0.8), spline)
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16), restore_labels(logits, (12, 20, 20)))
+    torch_plan = ResamplingContract("resample_torch_fornnunet", 1, 0, None)
+    assert restore_class_labels_device(dev, (12, 20, 20), (1.0, 1.0, 1.0), (0.8, 0.8, 0.8),
+                                       torch_plan) is None
+    order_z1 = ResamplingContract("resample_data_or_seg_to_shape", 1, 1, None)
+    assert restore_class_labels_device(dev, (25, 20, 20), (2.5, 0.8, 0.8), (1.0, 0.64, 0.64),
+                                       order_z1) is None

@@ -50,3 +50,37 @@ def test_axis_metadata_closed_form():
     lower, upper, wl, wu = axis_metadata(9, 3)  # downsampling by 3: centres 1, 4, 7
     np.testing.assert_array_equal(lower, [1, 4, 7])
     np.testing.assert_array_equal(wu, [0, 0, 0])
+
+
+@pytest.mark.parametrize("source,target", SHAPES)
+@pytest.mark.parametrize("dtype", [np.float32, np.float16])
+def test_spline_route_order1_equals_trilinear_route(source, target, dtype):
+    """Order-1 whole-volume spline restoration and the trilinear restoration are the same
+    half-pixel interpolation reached by two independent oracle routes."""
+    from oracle.restore import restore_labels_spline
+
+    logits = np.random.default_rng(3).standard_normal((*source, 3)).astype(dtype)
+    labels, values = restore_labels_spline(logits, target, order=1, separate_axis=None)
+    assert labels.shape == tuple(target)
+    agree = (labels == restore_labels(logits, target)).mean()
+    assert agree >= 0.999
+    if dtype == np.float16:
+        np.testing.assert_array_equal(values, values.astype(np.float16).astype(np.float32))
+
+
+def test_spline_route_separate_axis_is_planewise_then_nearest():
+    """Separate-axis restoration: every target plane is the in-plane resize of the nearest
+    source plane (scipy.ndimage.zoom order 1 on that plane), argmax over classes."""
+    from oracle.restore import restore_labels_spline
+
+    rng = np.random.default_rng(4)
+    logits = rng.standard_normal((5, 9, 7, 3)).astype(np.float32)
+    target = (12, 6, 11)
+    labels, values = restore_labels_spline(logits, target, order=1, separate_axis=0)
+    for o in range(target[0]):
+        k = min(max(int(np.floor(5 / 12 * (o + 0.5) - 0.5 + 0.5)), 0), 4)
+        for c in range(3):
+            plane = logits[k, :, :, c].astype(np.float64)
+            ref = ndimage.zoom(plane, (6 / 9, 11 / 7), order=1, mode="nearest", grid_mode=True)
+            np.testing.assert_allclose(values[c, o], ref, rtol=1e-6, atol=1e-6)
+    np.testing.assert_array_equal(labels, np.argmax(values, axis=0))
