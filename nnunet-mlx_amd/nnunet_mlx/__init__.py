@@ -18,7 +18,9 @@ __all__ = [
     "ContractError",
     "PlainConvUNetSpec",
     "ResidualEncoderUNetSpec",
+    "load_model",
     "load_model_bundle",
+    "run",
 ]
 
 
@@ -27,4 +29,8 @@ def __getattr__(name: str):
         from nnunet_mlx.model.folder import load_model_bundle
 
         return load_model_bundle
+    if name in ("run", "load_model"):
+        from nnunet_mlx import medmlx
+
+        return getattr(medmlx, name)
     raise AttributeError(name)

@@ -1,0 +1,40 @@
+"""nnU-Net BraTS brain-tumor MRI segmentation (``nnunet-brats2021``).
+
+Reference: src/nnunet_mlx/named_models/brats.py:15-62.
+"""
+
+from __future__ import annotations
+
+from collections.abc import Mapping
+
+from nnunet_mlx import medmlx
+from nnunet_mlx.errors import ContractError
+from nnunet_mlx.named_models import (READINESS, PathLike, input_channels, model_folder,
+                                     segment_folder)
+
+MODEL = {
+    "id": "nnunet-brats2021", "label": "nnU-Net BraTS 2021", "task": "segmentation",
+    "readiness": READINESS, "run": "nnunet_mlx.named_models.brats:run",
+    "summary": "Dataset002_BRATS19 with its original BAMF labels.",
+    "labels": {"1": "edema", "2": "nonenhancing", "3": "empty", "4": "enhancing"},
+}
+
+CHANNELS = ("t1", "t1ce", "t2", "flair")
+
+
+def run(*, image_paths: Mapping[str, PathLike], output_dir: PathLike,
+        weights_path: PathLike | None = None, overwrite: bool = False, fold: int | None = None,
+        use_mirroring: bool = True) -> dict:
+    """Segment four co-registered MRI sequences ``{"t1", "t1ce", "t2", "flair"}``; all five
+    folds are ensembled unless ``fold`` (0..4) selects one."""
+    if fold is not None and (isinstance(fold, bool) or fold not in range(5)):
+        raise ContractError("BraTS fold must be between 0 and 4")
+    channels = input_channels(image_paths, CHANNELS)
+    images, _ = medmlx.check_request(list(channels.values()), output_dir=output_dir,
+                                     overwrite=overwrite,
+                                     folds=None if fold is None else [fold],
+                                     use_mirroring=use_mirroring)
+    folder = model_folder("nnunet-brats2021", weights_path)
+    folds = list(range(5)) if fold is None else [fold]
+    return segment_folder(folder, images, output_dir, "3d_fullres", folds, overwrite=overwrite,
+                          grid_of="image_paths", use_mirroring=use_mirroring)

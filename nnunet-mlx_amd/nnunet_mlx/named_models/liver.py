@@ -1,0 +1,59 @@
+"""nnU-Net liver and liver-cancer CT segmentation (``nnunet-liver``).
+
+Reference: src/nnunet_mlx/named_models/liver.py:12-99.
+"""
+
+from __future__ import annotations
+
+from nnunet_mlx import medmlx
+from nnunet_mlx.named_models import READINESS, PathLike, model_folder, segment_folder
+
+MODEL = {
+    "id": "nnunet-liver", "label": "nnU-Net liver CT", "task": "segmentation",
+    "readiness": READINESS, "run": "nnunet_mlx.named_models.liver:run",
+    "cohort": "nnunet_mlx.named_models.liver:load_model",
+    "summary": "Liver and liver cancer segmentation of one CT volume.",
+    "labels": {"1": "liver", "2": "cancer"},
+}
+
+
+def run(*, image_path: PathLike, output_dir: PathLike, weights_path: PathLike | None = None,
+        overwrite: bool = False, use_mirroring: bool = True, step_fraction: float = 0.5) -> dict:
+    """Segment liver (1) and liver cancer (2) in one CT (NIfTI, Hounsfield units), on the
+    CT's grid; ``mask.nii.gz`` goes to ``output_dir``.  Three-axis mirroring (8 network
+    passes per tile) and a 0.5 step by default."""
+    images, _ = medmlx.check_request([image_path], output_dir=output_dir, overwrite=overwrite,
+                                     use_mirroring=use_mirroring, step_fraction=step_fraction)
+    folder = model_folder("nnunet-liver", weights_path)
+    return segment_folder(folder, images, output_dir, "3d_fullres", None, overwrite=overwrite,
+                          grid_of="image_path", use_mirroring=use_mirroring,
+                          step_fraction=step_fraction)
+
+
+class LiverModel:
+    """The liver model loaded once; :meth:`run` takes the per-CT arguments."""
+
+    def __init__(self, model: medmlx.NnUNetModel) -> None:
+        self._model = model
+
+    def run(self, *, image_path: PathLike, output_dir: PathLike, overwrite: bool = False) -> dict:
+        return self._model.segment_case(image_paths=[image_path], output_dir=output_dir,
+                                        overwrite=overwrite, grid_of="image_path")
+
+    def close(self) -> None:
+        self._model.close()
+
+    def __enter__(self) -> "LiverModel":
+        return self
+
+    def __exit__(self, *args: object) -> None:
+        self.close()
+
+
+def load_model(*, weights_path: PathLike | None = None, use_mirroring: bool = True,
+               step_fraction: float = 0.5) -> LiverModel:
+    """Load the liver model once to segment several CTs."""
+    folder = model_folder("nnunet-liver", weights_path)
+    return LiverModel(medmlx.load_model(weights_path=folder, configuration="3d_fullres",
+                                        use_mirroring=use_mirroring,
+                                        step_fraction=step_fraction))

@@ -1,0 +1,27 @@
+"""Pancreas and pancreatic-cancer CT segmentation (``nnunet-pancreas``).
+
+Reference: src/nnunet_mlx/named_models/pancreas.py:12-49.
+"""
+
+from __future__ import annotations
+
+from nnunet_mlx import medmlx
+from nnunet_mlx.named_models import READINESS, PathLike, model_folder, segment_folder
+
+MODEL = {
+    "id": "nnunet-pancreas", "label": "Pancreas segmentation", "task": "segmentation",
+    "readiness": READINESS, "run": "nnunet_mlx.named_models.pancreas:run",
+    "summary": "PancCTMultiTalentV2 pancreas and cancer segmentation.",
+    "labels": {"1": "pancreas", "2": "cancer"},
+}
+
+
+def run(*, image_path: PathLike, output_dir: PathLike, weights_path: PathLike | None = None,
+        overwrite: bool = False, fold: int = 0, use_mirroring: bool = True) -> dict:
+    """Segment pancreas (1) and cancer (2) in one CT with the ``3d_fullres_bs4``
+    configuration; ``fold`` is the converted checkpoint slot (fold_all staged in 0)."""
+    images, _ = medmlx.check_request([image_path], output_dir=output_dir, overwrite=overwrite,
+                                     folds=[fold], use_mirroring=use_mirroring)
+    folder = model_folder("nnunet-pancreas", weights_path)
+    return segment_folder(folder, images, output_dir, "3d_fullres_bs4", [fold],
+                          overwrite=overwrite, grid_of="image_path", use_mirroring=use_mirroring)

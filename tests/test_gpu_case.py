@@ -1,0 +1,162 @@
+"""Raw case -> label image on the GPU against the oracle composition of the same steps.
+
+The oracle chain: nonzero crop, CT normalisation and spline resampling
+(``oracle.preprocess``), the float32 network (``oracle.network``) under the sliding window
+with float16 accumulation (``oracle.sliding_window``), spline restoration with the
+first-maximum argmax (``oracle.restore``), then uncrop.  The device path differs from it
+only by float32 summation order inside the network, so labels may differ where two classes
+are within a rounding of each other: the bar is 99.9 % identical voxels, identical outside
+the crop box.
+"""
+
+from __future__ import annotations
+
+import json
+
+import numpy as np
+import pytest
+import torch
+
+from nnunet_mlx.model.topology import PlainConvUNetSpec
+from nnunet_mlx.storage import nifti
+from nnunet_mlx.storage.synthetic import random_weights, write_random_model_folder
+from oracle import preprocess as op
+from oracle import sliding_window as osw
+from oracle.network import OracleNetwork
+from oracle.restore import restore_labels_spline
+
+pytestmark = pytest.mark.gpu
+
+SPEC = PlainConvUNetSpec(1, 3, (8, 16), ((3, 3, 3),) * 2, ((1, 1, 1), (2, 2, 2)), (2, 2), (2,))
+PATCH = (16, 32, 32)
+CT = {"mean": 60.0, "std": 80.0, "percentile_00_5": -150.0, "percentile_99_5": 250.0}
+TARGET_SPACING = (2.0, 0.8, 0.8)
+IMAGE_SPACING_XYZ = (0.9, 0.9, 3.0)
+
+
+def ct_model_folder(root, seeds=(0,)):
+    folder = write_random_model_folder(root, SPEC, patch_size=PATCH, seeds=seeds,
+                                       random_affine=False, labels=("liver", "tumor"))
+    plans = json.loads((folder / "plans.json").read_text())
+    cfg = plans["configurations"]["3d_fullres"]
+    cfg["spacing"] = list(TARGET_SPACING)
+    cfg["normalization_schemes"] = ["CTNormalization"]
+    plans["foreground_intensity_properties_per_channel"] = {"0": dict(CT)}
+    (folder / "plans.json").write_text(json.dumps(plans))
+    return folder
+
+
+def synthetic_ct(path, seed):
+    """(Z, Y, X) int16 CT with air outside a body box and two bright ellipsoids."""
+    rng = np.random.default_rng(seed)
+    z, y, x = np.mgrid[0:12, 0:40, 0:36]
+    ct = np.zeros((12, 40, 36), dtype=np.int16)
+    body = (y >= 4) & (y < 37) & (x >= 3) & (x < 33)
+    ct[body] = (rng.standard_normal(body.sum()) * 40 + 30).astype(np.int16)
+    blob = ((z - 6) / 4.0) ** 2 + ((y - 18) / 9.0) ** 2 + ((x - 14) / 7.0) ** 2 < 1
+    ct[blob] = (rng.standard_normal(blob.sum()) * 20 + 160).astype(np.int16)
+    nifti.write_nifti(path, ct, IMAGE_SPACING_XYZ)
+    return ct
+
+
+def oracle_case_labels(ct_zyx, seeds=(0,)):
+    """The oracle chain for a one-channel CT on the (Z, Y, X) grid, identity transpose."""
+    raw = ct_zyx.astype(np.float32)[None]
+    bbox = op.nonzero_bbox(raw)
+    crop = raw[(slice(None), *(slice(a, b) for a, b in bbox))]
+    norm = op.ct_normalize(crop[0], CT["mean"], CT["std"], CT["percentile_00_5"],
+                           CT["percentile_99_5"])[None]
+    original = tuple(reversed(IMAGE_SPACING_XYZ))
+    new_shape = tuple(round(o / n * s) for o, n, s in zip(original, TARGET_SPACING, crop.shape[1:]))
+    data = op.resample_data(norm, new_shape, separate_axis=0)
+    nets = [OracleNetwork(SPEC, random_weights(SPEC, s)) for s in seeds]
+    logits, _ = osw.predict(nets, data, PATCH, num_classes=3, axes=(0, 1, 2),
+                            step_fraction=0.5, accumulation="nnunet-fp16")
+    labels, _ = restore_labels_spline(logits, crop.shape[1:], order=1, separate_axis=0)
+    full = np.zeros(ct_zyx.shape, dtype=np.uint16)
+    full[tuple(slice(a, b) for a, b in bbox)] = labels
+    return full, bbox
+
+
+def test_run_writes_the_oracle_labels(tmp_path):
+    import nnunet_mlx
+
+    folder = ct_model_folder(tmp_path / "model")
+    ct = synthetic_ct(tmp_path / "case_0000.nii.gz", seed=3)
+    print("raw case: run() on a 12x40x36 CT, separate-z plans", flush=True)
+    result = nnunet_mlx.run(weights_path=folder, image_paths=[tmp_path / "case_0000.nii.gz"],
+                            output_dir=tmp_path / "out")
+    mask = nifti.read_nifti(result["outputs"]["mask"])
+    want, bbox = oracle_case_labels(ct)
+    assert mask.array.shape == ct.shape and mask.array.dtype == np.uint8
+    assert mask.spacing == pytest.approx(IMAGE_SPACING_XYZ)
+    agree = (mask.array == want).mean()
+    print(f"label agreement {agree:.6f}, classes {np.bincount(want.ravel(), minlength=3)}",
+          flush=True)
+    assert agree >= 0.999
+    outside = np.ones(ct.shape, dtype=bool)
+    outside[tuple(slice(a, b) for a, b in bbox)] = False
+    assert (mask.array[outside] == 0).all()
+    details = result["details"]
+    assert details["accumulation"] == "nnunet-fp16" and details["folds"] == [0]
+    assert details["preprocessed_shape"][1:] == [18, 37, 34]
+    assert result["artifacts"]["mask"]["labels"][1]["name"] == "liver"
+
+
+def test_loaded_model_and_named_model_agree_with_run(tmp_path):
+    from nnunet_mlx import medmlx
+    from nnunet_mlx.named_models import liver
+
+    folder = ct_model_folder(tmp_path / "model", seeds=(0, 1))
+    synthetic_ct(tmp_path / "a.nii.gz", seed=4)
+    synthetic_ct(tmp_path / "b.nii.gz", seed=5)
+    print("raw case: two folds, loaded model over two cases", flush=True)
+    first = medmlx.run(weights_path=folder, image_paths=[tmp_path / "a.nii.gz"],
+                       output_dir=tmp_path / "run_a")
+    with liver.load_model(weights_path=folder) as model:
+        again = model.run(image_path=tmp_path / "a.nii.gz", output_dir=tmp_path / "model_a")
+        other = model.run(image_path=tmp_path / "b.nii.gz", output_dir=tmp_path / "model_b")
+        with pytest.raises(Exception, match="exists"):
+            model.run(image_path=tmp_path / "a.nii.gz", output_dir=tmp_path / "model_a")
+    a1 = nifti.read_nifti(first["outputs"]["mask"]).array
+    a2 = nifti.read_nifti(again["outputs"]["mask"]).array
+    np.testing.assert_array_equal(a1, a2)
+    assert other["details"]["folds"] == [0, 1]
+    named = liver.run(image_path=tmp_path / "b.nii.gz", output_dir=tmp_path / "named_b",
+                      weights_path=folder)
+    np.testing.assert_array_equal(nifti.read_nifti(named["outputs"]["mask"]).array,
+                                  nifti.read_nifti(other["outputs"]["mask"]).array)
+    with pytest.raises(RuntimeError, match="closed"):
+        model.run(image_path=tmp_path / "b.nii.gz", output_dir=tmp_path / "closed")
+
+
+def test_cli_predicts_an_upstream_folder(tmp_path, monkeypatch):
+    """``nnunet-mlx predict -m`` converts an upstream results folder (cached) and predicts
+    the input folder; the labels equal run() on the converted folder."""
+    from nnunet_mlx import medmlx
+    from nnunet_mlx.cli import main
+    from tests.test_upstream_conversion import to_upstream
+
+    folder = ct_model_folder(tmp_path / "model")
+    upstream = tmp_path / "results" / "Dataset001_Ct" / "nnUNetTrainer__nnUNetPlans__3d_fullres"
+    (upstream / "fold_0").mkdir(parents=True)
+    for name in ("plans.json", "dataset.json"):
+        (upstream / name).write_text((folder / name).read_text())
+    torch.save({"network_weights": to_upstream(random_weights(SPEC, 0)),
+                "trainer_name": "nnUNetTrainer", "init_args": {"configuration": "3d_fullres"},
+                "inference_allowed_mirroring_axes": (0, 1, 2), "current_epoch": 1000},
+               upstream / "fold_0" / "checkpoint_final.pth")
+    (tmp_path / "in").mkdir()
+    synthetic_ct(tmp_path / "in" / "c1_0000.nii.gz", seed=6)
+    monkeypatch.setenv("NNUNET_MLX_CACHE", str(tmp_path / "cache"))
+    print("raw case: CLI predict -d over an upstream results folder", flush=True)
+    monkeypatch.setenv("nnUNet_results", str(tmp_path / "results"))
+    assert main(["predict", "-i", str(tmp_path / "in"), "-o", str(tmp_path / "out"), "-d", "1",
+                 "-c", "3d_fullres", "-f", "0"]) == 0
+    got = nifti.read_nifti(tmp_path / "out" / "c1.nii.gz").array
+    ref = medmlx.run(weights_path=folder, image_paths=[tmp_path / "in" / "c1_0000.nii.gz"],
+                     output_dir=tmp_path / "ref")
+    np.testing.assert_array_equal(got, nifti.read_nifti(ref["outputs"]["mask"]).array)
+    # the second call reuses the conversion and skips the finished case
+    assert main(["predict", "-i", str(tmp_path / "in"), "-o", str(tmp_path / "out"), "-d", "1",
+                 "-c", "3d_fullres", "-f", "0", "--continue_prediction"]) == 0
