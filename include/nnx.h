@@ -312,11 +312,43 @@ int nnx_restore_labels_spline(const void* d_logits, int half, int classes, const
  * for spline plans (src/nnunet_mlx/data/resampling.py:87-172, 268-306, 379-442, 476-501). */
 #define NNX_NORM_NONE 0
 #define NNX_NORM_CT 1
+#define NNX_NORM_ZSCORE 2        /* (x - mean) / max(std, 1e-8), norm[4c..4c+1] = (mean, std) */
+#define NNX_NORM_ZSCORE_MASKED 3 /* the same where the filled mask is set, else unchanged */
 int nnx_nonzero_bbox(const float* d_data, int channels, const int64_t* size, int* d_bbox,
                      void* stream);
 int nnx_crop_normalize(const float* d_data, int channels, const int64_t* size,
                        const int* transpose, const int64_t* start, const int64_t* out_size,
                        const int* schemes, const float* norm, float* d_out, void* stream);
+/* Z-score normalisation (ZScoreNormalization of _normalize_channel,
+ * src/nnunet_mlx/data/preprocessing.py:286-296, with the filled nonzero mask of
+ * crop_to_nonzero, :166-214).
+ *
+ * nnx_nonzero_mask_filled: d_mask (extent[0], extent[1], extent[2]) uint8 over the raw box
+ * at `start` = 1 where any channel is nonzero or the voxel lies in a background region
+ * enclosed by it (6-connected, not connected to the box border: SciPy's
+ * binary_fill_holes), else 0.  d_work: 256 bytes of device scratch.  Synchronises the
+ * stream once per sweep round (not capturable); returns the round count (> 0) or a
+ * negative error.
+ *
+ * nnx_zscore_stats: d_stats[0..1] = (mean, std) of channel `channel` over the raw box (only
+ * mask voxels when d_mask is not null), accumulated in float64 and rounded to float32;
+ * std about the float32 mean, biased (numpy's x.std()).  d_work: nnx_zscore_stats_workspace
+ * bytes.
+ *
+ * nnx_crop_normalize_masked: nnx_crop_normalize with NNX_NORM_ZSCORE_MASKED channels, which
+ * read d_mask over the raw box (mask_start, mask_extent) that contains the crop. */
+int nnx_nonzero_mask_filled(const float* d_data, int channels, const int64_t* size,
+                            const int64_t* start, const int64_t* extent, uint8_t* d_mask,
+                            void* d_work, void* stream);
+size_t nnx_zscore_stats_workspace(void);
+int nnx_zscore_stats(const float* d_data, int channels, const int64_t* size, int channel,
+                     const int64_t* start, const int64_t* extent, const uint8_t* d_mask,
+                     float* d_stats, void* d_work, void* stream);
+int nnx_crop_normalize_masked(const float* d_data, int channels, const int64_t* size,
+                              const int* transpose, const int64_t* start,
+                              const int64_t* out_size, const int* schemes, const float* norm,
+                              const uint8_t* d_mask, const int64_t* mask_start,
+                              const int64_t* mask_extent, float* d_out, void* stream);
 size_t nnx_resample_spline_workspace(const int64_t* size, const int64_t* new_size,
                                      int separate_axis);
 int nnx_resample_spline(const float* d_data, int channels, const int64_t* size,

@@ -182,6 +182,18 @@ void nonzero_bbox(const float* x, int channels, const int64_t* size, int* bbox, 
 void crop_normalize(const float* x, int channels, const int64_t* size, const int* transpose,
                     const int64_t* start, const int64_t* out_size, const int* schemes,
                     const float* norm, float* out, hipStream_t st);
+void crop_normalize_masked(const float* x, int channels, const int64_t* size,
+                           const int* transpose, const int64_t* start, const int64_t* out_size,
+                           const int* schemes, const float* norm, const uint8_t* mask,
+                           const int64_t* mask_start, const int64_t* mask_extent, float* out,
+                           hipStream_t st);
+// Filled nonzero mask of the raw box (start, extent): returns the number of sweep rounds.
+int nonzero_mask_filled(const float* x, int channels, const int64_t* size, const int64_t* start,
+                        const int64_t* extent, uint8_t* mask, void* work, hipStream_t st);
+size_t zscore_stats_workspace();
+void zscore_stats(const float* x, int channels, const int64_t* size, int channel,
+                  const int64_t* start, const int64_t* extent, const uint8_t* mask, float* stats,
+                  void* work, hipStream_t st);
 size_t resample_spline_workspace(const int64_t* size, const int64_t* new_size, int separate_axis);
 void resample_spline(const float* x, int channels, const int64_t* size, const int64_t* new_size,
                      int order, int separate_axis, int order_z, void* work, size_t work_bytes,

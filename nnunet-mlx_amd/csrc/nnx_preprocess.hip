@@ -120,12 +120,138 @@ struct ChannelNorms {
   float lower[kMaxNormChannels], upper[kMaxNormChannels];
 };
 
+// ---- filled nonzero mask ----------------------------------------------------------------
+// Cells of the crop box (E0, E1, E2) of the raw volume: 2 = some channel nonzero, 1 =
+// background reached from the box border through background (6-connected), 0 = background
+// not reached yet.  After the sweeps converge the filled mask is cell != 1.
+
+__global__ __launch_bounds__(256) void mask_init_kernel(const float* __restrict__ x, int C,
+                                                        int64_t X, int64_t Y, int64_t Z,
+                                                        int64_t b0, int64_t b1, int64_t b2,
+                                                        int64_t E0, int64_t E1, int64_t E2,
+                                                        uint8_t* __restrict__ cell) {
+  const int64_t n = X * Y * Z, total = E0 * E1 * E2;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i2 = e % E2, i1 = (e / E2) % E1, i0 = e / (E1 * E2);
+    const int64_t src = ((b0 + i0) * Y + (b1 + i1)) * Z + (b2 + i2);
+    bool nz = false;
+    for (int c = 0; c < C; ++c) nz |= x[(int64_t)c * n + src] != 0.f;
+    const bool border = i0 == 0 || i1 == 0 || i2 == 0 || i0 == E0 - 1 || i1 == E1 - 1 ||
+                        i2 == E2 - 1;
+    cell[e] = nz ? 2 : (border ? 1 : 0);
+  }
+}
+
+// Propagate "reached" along every line of `axis` in both directions (one thread per line;
+// for axes 0 and 1 neighbouring threads hold neighbouring lines).  *changed = 1 when a
+// cell changed.
+__global__ __launch_bounds__(256) void mask_sweep_kernel(uint8_t* __restrict__ cell, int64_t E0,
+                                                         int64_t E1, int64_t E2, int axis,
+                                                         int* __restrict__ changed) {
+  const int64_t dims[3] = {E0, E1, E2};
+  const int64_t strides[3] = {E1 * E2, E2, 1};
+  const int64_t len = dims[axis], stride = strides[axis];
+  const int64_t lines = E0 * E1 * E2 / len;
+  const int64_t line = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (line >= lines) return;
+  int64_t base;
+  if (axis == 2) base = line * E2;
+  else if (axis == 1) base = (line / E2) * E1 * E2 + line % E2;
+  else base = line;
+  bool any = false, carry = false;
+  for (int64_t i = 0; i < len; ++i) {
+    uint8_t& v = cell[base + i * stride];
+    if (v == 2) carry = false;
+    else if (v == 1) carry = true;
+    else if (carry) { v = 1; any = true; }
+  }
+  carry = false;
+  for (int64_t i = len - 1; i >= 0; --i) {
+    uint8_t& v = cell[base + i * stride];
+    if (v == 2) carry = false;
+    else if (v == 1) carry = true;
+    else if (carry) { v = 1; any = true; }
+  }
+  if (any) *changed = 1;
+}
+
+__global__ void flag_clear_kernel(int* flag) { *flag = 0; }
+
+__global__ __launch_bounds__(256) void mask_finish_kernel(uint8_t* __restrict__ cell, int64_t n) {
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < n;
+       e += (int64_t)gridDim.x * blockDim.x)
+    cell[e] = cell[e] != 1;
+}
+
+// ---- z-score statistics -----------------------------------------------------------------
+// Per block: float64 sums over the crop box of channel c (mask cells only when `mask`),
+// pass 0: (sum x, count), pass 1: (sum (x - mean32)^2, count) with mean32 = stats[2c].
+
+constexpr int kStatBlocks = 1024;
+
+__global__ __launch_bounds__(256) void zscore_partial_kernel(
+    const float* __restrict__ xc, int64_t Y, int64_t Z, int64_t b0, int64_t b1, int64_t b2,
+    int64_t E0, int64_t E1, int64_t E2, const uint8_t* __restrict__ mask, int pass,
+    const float* __restrict__ stats, double2* __restrict__ partial) {
+  __shared__ double ssum[4], scnt[4];
+  const int64_t total = E0 * E1 * E2;
+  const double mean = pass ? (double)stats[0] : 0.0;
+  double acc = 0.0, cnt = 0.0;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    if (mask && !mask[e]) continue;
+    const int64_t i2 = e % E2, i1 = (e / E2) % E1, i0 = e / (E1 * E2);
+    const double v = (double)xc[((b0 + i0) * Y + (b1 + i1)) * Z + (b2 + i2)];
+    acc += pass ? (v - mean) * (v - mean) : v;
+    cnt += 1.0;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    acc += __shfl_xor(acc, o);
+    cnt += __shfl_xor(cnt, o);
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    ssum[wave] = acc;
+    scnt[wave] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    partial[blockIdx.x] = make_double2(ssum[0] + ssum[1] + ssum[2] + ssum[3],
+                                       scnt[0] + scnt[1] + scnt[2] + scnt[3]);
+}
+
+// stats[0] = float(sum / n) (pass 0) or stats[1] = float(sqrt(sum / n)) (pass 1); a fixed
+// summation order over the partials, so the result is deterministic
+__global__ __launch_bounds__(64) void zscore_final_kernel(const double2* __restrict__ partial,
+                                                         int parts, int pass,
+                                                         float* __restrict__ stats) {
+  double acc = 0.0, cnt = 0.0;
+  for (int i = threadIdx.x; i < parts; i += 64) {
+    acc += partial[i].x;
+    cnt += partial[i].y;
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    acc += __shfl_xor(acc, o);
+    cnt += __shfl_xor(cnt, o);
+  }
+  if (threadIdx.x == 0) {
+    const double m = cnt > 0 ? acc / cnt : NAN;
+    if (pass == 0) stats[0] = (float)m;
+    else stats[1] = (float)sqrt(m);
+  }
+}
+
 // out[c][o0][o1][o2] = norm_c(x[c][r0][r1][r2]) with r[t_k] = s_k + o_k: out axis k is input
-// axis t_k, cropped to start s_k.
+// axis t_k, cropped to start s_k.  NNX_NORM_ZSCORE_MASKED normalises only where the filled
+// mask (raw-order box starting at (m0, m1, m2), extents (*, ME1, ME2)) is set.
 __global__ __launch_bounds__(256) void crop_normalize_kernel(
     const float* __restrict__ x, int C, int64_t X, int64_t Y, int64_t Z, int t0, int t1, int t2,
     int64_t s0, int64_t s1, int64_t s2, int64_t O0, int64_t O1, int64_t O2, ChannelNorms norms,
-    float* __restrict__ out) {
+    const uint8_t* __restrict__ mask, int64_t m0, int64_t m1, int64_t m2, int64_t ME1,
+    int64_t ME2, float* __restrict__ out) {
   const int64_t per = O0 * O1 * O2;
   const int64_t total = per * C;
   for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
@@ -138,8 +264,13 @@ __global__ __launch_bounds__(256) void crop_normalize_kernel(
     const int64_t r1 = t0 == 1 ? a0 : t1 == 1 ? a1 : a2;
     const int64_t r2 = t0 == 2 ? a0 : t1 == 2 ? a1 : a2;
     float v = x[(int64_t)c * X * Y * Z + (r0 * Y + r1) * Z + r2];
-    if (norms.scheme[c] == NNX_NORM_CT) {
+    const int scheme = norms.scheme[c];
+    if (scheme == NNX_NORM_CT) {
       v = fminf(fmaxf(v, norms.lower[c]), norms.upper[c]);
+      v = __fdiv_rn(__fsub_rn(v, norms.mean[c]), norms.std[c]);
+    } else if (scheme == NNX_NORM_ZSCORE ||
+               (scheme == NNX_NORM_ZSCORE_MASKED &&
+                mask[((r0 - m0) * ME1 + (r1 - m1)) * ME2 + (r2 - m2)])) {
       v = __fdiv_rn(__fsub_rn(v, norms.mean[c]), norms.std[c]);
     }
     out[e] = v;
@@ -496,9 +627,77 @@ void nonzero_bbox(const float* x, int channels, const int64_t* size, int* bbox, 
   launch_check("nonzero_bbox");
 }
 
+int nonzero_mask_filled(const float* x, int channels, const int64_t* size, const int64_t* start,
+                        const int64_t* extent, uint8_t* mask, void* work, hipStream_t st) {
+  require(x && size && start && extent && mask && work, "mask pointers must not be null");
+  require(channels >= 1, "mask needs at least one channel");
+  for (int a = 0; a < 3; ++a)
+    require(extent[a] >= 1 && start[a] >= 0 && start[a] + extent[a] <= size[a],
+            "mask box outside the volume");
+  const int64_t total = extent[0] * extent[1] * extent[2];
+  int* flag = static_cast<int*>(work);
+  ProfScope prof("preprocess_fill_holes", 0.0, 4.0 * (double)total * channels, st);
+  hipLaunchKernelGGL(mask_init_kernel, dim3(blocks_for(total)), dim3(256), 0, st, x, channels,
+                     size[0], size[1], size[2], start[0], start[1], start[2], extent[0],
+                     extent[1], extent[2], mask);
+  // every round with a change reaches at least one more cell, so at most `total` rounds
+  int rounds = 0;
+  for (int64_t r = 0; r <= total; ++r) {
+    hipLaunchKernelGGL(flag_clear_kernel, dim3(1), dim3(1), 0, st, flag);
+    for (int axis = 2; axis >= 0; --axis) {
+      const int64_t lines = total / extent[axis];
+      hipLaunchKernelGGL(mask_sweep_kernel, dim3((unsigned)ceil_div(lines, 256)), dim3(256), 0,
+                         st, mask, extent[0], extent[1], extent[2], axis, flag);
+    }
+    int changed = 0;
+    hip_check(hipMemcpyAsync(&changed, flag, sizeof(int), hipMemcpyDeviceToHost, st),
+              "mask flag copy");
+    hip_check(hipStreamSynchronize(st), "mask flag sync");
+    ++rounds;
+    if (!changed) break;
+  }
+  hipLaunchKernelGGL(mask_finish_kernel, dim3(blocks_for(total)), dim3(256), 0, st, mask, total);
+  launch_check("nonzero_mask_filled");
+  return rounds;
+}
+
+size_t zscore_stats_workspace() { return kStatBlocks * sizeof(double2); }
+
+void zscore_stats(const float* x, int channels, const int64_t* size, int channel,
+                  const int64_t* start, const int64_t* extent, const uint8_t* mask, float* stats,
+                  void* work, hipStream_t st) {
+  require(x && size && start && extent && stats && work, "z-score pointers must not be null");
+  require(channel >= 0 && channel < channels, "z-score channel out of range");
+  for (int a = 0; a < 3; ++a)
+    require(extent[a] >= 1 && start[a] >= 0 && start[a] + extent[a] <= size[a],
+            "z-score box outside the volume");
+  const int64_t total = extent[0] * extent[1] * extent[2];
+  const float* xc = x + (int64_t)channel * size[0] * size[1] * size[2];
+  double2* partial = static_cast<double2*>(work);
+  const int blocks = (int)std::min<int64_t>(kStatBlocks, ceil_div(total, 256));
+  ProfScope prof("preprocess_zscore_stats", 0.0, 8.0 * (double)total, st);
+  for (int pass = 0; pass < 2; ++pass) {
+    hipLaunchKernelGGL(zscore_partial_kernel, dim3(blocks), dim3(256), 0, st, xc, size[1],
+                       size[2], start[0], start[1], start[2], extent[0], extent[1], extent[2],
+                       mask, pass, stats, partial);
+    hipLaunchKernelGGL(zscore_final_kernel, dim3(1), dim3(64), 0, st, partial, blocks, pass,
+                       stats);
+  }
+  launch_check("zscore_stats");
+}
+
 void crop_normalize(const float* x, int channels, const int64_t* size, const int* transpose,
                     const int64_t* start, const int64_t* out_size, const int* schemes,
                     const float* norm, float* out, hipStream_t st) {
+  crop_normalize_masked(x, channels, size, transpose, start, out_size, schemes, norm, nullptr,
+                        nullptr, nullptr, out, st);
+}
+
+void crop_normalize_masked(const float* x, int channels, const int64_t* size,
+                           const int* transpose, const int64_t* start, const int64_t* out_size,
+                           const int* schemes, const float* norm, const uint8_t* mask,
+                           const int64_t* mask_start, const int64_t* mask_extent, float* out,
+                           hipStream_t st) {
   require(x && out && size && transpose && start && out_size && schemes,
           "crop/normalise pointers must not be null");
   require(channels >= 1 && channels <= kMaxNormChannels,
@@ -515,10 +714,21 @@ void crop_normalize(const float* x, int channels, const int64_t* size, const int
             "crop window outside the volume");
   }
   ChannelNorms cn{};
+  bool masked = false;
   for (int c = 0; c < channels; ++c) {
-    require(schemes[c] == NNX_NORM_NONE || schemes[c] == NNX_NORM_CT,
-            "device normalisation supports NoNormalization and CTNormalization");
+    require(schemes[c] >= NNX_NORM_NONE && schemes[c] <= NNX_NORM_ZSCORE_MASKED,
+            "device normalisation supports NoNormalization, CTNormalization and "
+            "ZScoreNormalization");
     cn.scheme[c] = schemes[c];
+    if (schemes[c] == NNX_NORM_ZSCORE || schemes[c] == NNX_NORM_ZSCORE_MASKED) {
+      require(norm != nullptr, "z-score normalisation needs its statistics");
+      const float* p = norm + 4 * c;
+      require(std::isfinite(p[0]) && std::isfinite(p[1]) && p[1] >= 0.f,
+              "z-score statistics must be finite with a non-negative std");
+      cn.mean[c] = p[0];
+      cn.std[c] = std::max(p[1], 1e-8f);
+      masked |= schemes[c] == NNX_NORM_ZSCORE_MASKED;
+    }
     if (schemes[c] == NNX_NORM_CT) {
       require(norm != nullptr, "CT normalisation needs its statistics");
       const float* p = norm + 4 * c;
@@ -531,11 +741,27 @@ void crop_normalize(const float* x, int channels, const int64_t* size, const int
       cn.upper[c] = p[3];
     }
   }
+  int64_t ms[3] = {0, 0, 0}, me[3] = {1, 1, 1};
+  if (masked) {
+    require(mask && mask_start && mask_extent, "masked z-score normalisation needs the mask");
+    // every cropped voxel (raw axis transpose[k] from start[k]) must lie in the mask box
+    for (int k = 0; k < 3; ++k) {
+      const int a = transpose[k];
+      require(mask_extent[a] >= 1 && start[k] >= mask_start[a] &&
+                  start[k] + out_size[k] <= mask_start[a] + mask_extent[a],
+              "crop window outside the mask box");
+    }
+    for (int a = 0; a < 3; ++a) {
+      ms[a] = mask_start[a];
+      me[a] = mask_extent[a];
+    }
+  }
   const int64_t total = out_size[0] * out_size[1] * out_size[2] * channels;
   ProfScope prof("preprocess_crop_normalize", 0.0, 8.0 * (double)total, st);
   hipLaunchKernelGGL(crop_normalize_kernel, dim3(blocks_for(total)), dim3(256), 0, st, x,
                      channels, size[0], size[1], size[2], transpose[0], transpose[1], transpose[2],
-                     start[0], start[1], start[2], out_size[0], out_size[1], out_size[2], cn, out);
+                     start[0], start[1], start[2], out_size[0], out_size[1], out_size[2], cn,
+                     masked ? mask : nullptr, ms[0], ms[1], ms[2], me[1], me[2], out);
   launch_check("crop_normalize");
 }
 

@@ -1175,6 +1175,39 @@ int nnx_crop_normalize(const float* d_data, int channels, const int64_t* size,
   });
 }
 
+int nnx_nonzero_mask_filled(const float* d_data, int channels, const int64_t* size,
+                            const int64_t* start, const int64_t* extent, uint8_t* d_mask,
+                            void* d_work, void* stream) {
+  int rounds = 0;
+  const int rc = guarded([&] {
+    rounds = nonzero_mask_filled(d_data, channels, size, start, extent, d_mask, d_work,
+                                 as_stream(stream));
+  });
+  return rc != 0 ? rc : rounds;
+}
+
+size_t nnx_zscore_stats_workspace(void) { return zscore_stats_workspace(); }
+
+int nnx_zscore_stats(const float* d_data, int channels, const int64_t* size, int channel,
+                     const int64_t* start, const int64_t* extent, const uint8_t* d_mask,
+                     float* d_stats, void* d_work, void* stream) {
+  return guarded([&] {
+    zscore_stats(d_data, channels, size, channel, start, extent, d_mask, d_stats, d_work,
+                 as_stream(stream));
+  });
+}
+
+int nnx_crop_normalize_masked(const float* d_data, int channels, const int64_t* size,
+                              const int* transpose, const int64_t* start,
+                              const int64_t* out_size, const int* schemes, const float* norm,
+                              const uint8_t* d_mask, const int64_t* mask_start,
+                              const int64_t* mask_extent, float* d_out, void* stream) {
+  return guarded([&] {
+    crop_normalize_masked(d_data, channels, size, transpose, start, out_size, schemes, norm,
+                          d_mask, mask_start, mask_extent, d_out, as_stream(stream));
+  });
+}
+
 size_t nnx_resample_spline_workspace(const int64_t* size, const int64_t* new_size,
                                      int separate_axis) {
   if (!size || !new_size || separate_axis < -1 || separate_axis > 2) return 0;

@@ -35,6 +35,8 @@ NNX_PRECISION_FP32_SPLIT = 1
 NNX_PRECISION_BF16 = 2
 NNX_NORM_NONE = 0
 NNX_NORM_CT = 1
+NNX_NORM_ZSCORE = 2
+NNX_NORM_ZSCORE_MASKED = 3
 NNX_ACCUM_F32 = 0
 NNX_ACCUM_NNUNET_F16 = 1
 
@@ -191,6 +193,20 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_void_p, ctypes.c_size_t, c_void_p, c_void_p],
     ),
     "nnx_nonzero_bbox": (ctypes.c_int, [c_void_p, ctypes.c_int, c_i64_p, c_void_p, c_void_p]),
+    "nnx_nonzero_mask_filled": (
+        ctypes.c_int, [c_void_p, ctypes.c_int, c_i64_p, c_i64_p, c_i64_p, c_void_p, c_void_p, c_void_p]
+    ),
+    "nnx_zscore_stats_workspace": (ctypes.c_size_t, []),
+    "nnx_zscore_stats": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_i64_p, ctypes.c_int, c_i64_p, c_i64_p, c_void_p, c_void_p,
+         c_void_p, c_void_p],
+    ),
+    "nnx_crop_normalize_masked": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_i64_p, c_int_p, c_i64_p, c_i64_p, c_int_p,
+         ctypes.POINTER(ctypes.c_float), c_void_p, c_i64_p, c_i64_p, c_void_p, c_void_p],
+    ),
     "nnx_crop_normalize": (
         ctypes.c_int,
         [c_void_p, ctypes.c_int, c_i64_p, c_int_p, c_i64_p, c_i64_p, c_int_p,

@@ -9,12 +9,14 @@ plans fields it reads (``PlansContract``, src/nnunet_mlx/plans.py:154-372).
 The same step order as the reference: the raw (C, X, Y, Z) case is cast to float32,
 transposed into the plans' axis order, cropped to the bounds of its nonzero voxels,
 normalised per channel, and resampled to the configuration's spacing.  Every array step
-runs in HIP kernels (``nnx_nonzero_bbox``, ``nnx_crop_normalize``,
-``nnx_resample_spline``); the host computes shapes and reads back the six crop bounds.
-The device path covers the CTNormalization and NoNormalization schemes (no mask needed)
-and spline plans (``resample_data_or_seg_to_shape``; orders 1 and 3, order_z 0); other
-schemes, the Torch-grid resampler and cascade inputs raise ``ContractError`` rather than
-run elsewhere.
+runs in HIP kernels (``nnx_nonzero_bbox``, ``nnx_nonzero_mask_filled``,
+``nnx_zscore_stats``, ``nnx_crop_normalize_masked``, ``nnx_resample_spline``); the host
+computes shapes and reads back the six crop bounds and the z-score statistics.  The device
+path covers CTNormalization, NoNormalization and ZScoreNormalization (with or without the
+filled nonzero mask; mean and std accumulated in float64 and rounded to float32, within a
+few float32 steps of numpy's float32 statistics) and spline plans
+(``resample_data_or_seg_to_shape``; orders 1 and 3, order_z 0); RescaleTo01/RGBTo01, the
+Torch-grid resampler and cascade inputs raise ``ContractError`` rather than run elsewhere.
 """
 
 from __future__ import annotations
@@ -30,7 +32,8 @@ from nnunet_mlx.data.resampling import separate_z_axis, validate_spacing
 from nnunet_mlx.errors import ContractError
 from nnunet_mlx.plans import ResamplingContract, resolve_configuration
 
-DEVICE_SCHEMES = {"NoNormalization": _native.NNX_NORM_NONE, "CTNormalization": _native.NNX_NORM_CT}
+DEVICE_SCHEMES = {"NoNormalization": _native.NNX_NORM_NONE, "CTNormalization": _native.NNX_NORM_CT,
+                  "ZScoreNormalization": _native.NNX_NORM_ZSCORE}
 
 
 @dataclass(frozen=True)
@@ -191,16 +194,51 @@ def preprocess_raw_case(data, properties: Mapping[str, object], plan: Preprocess
 
     schemes = [DEVICE_SCHEMES[s] for s in plan.normalization_schemes]
     norm = np.zeros((channels, 4), dtype=np.float32)
+    raw_start = [int(raw_bounds[a, 0]) for a in range(3)]
+    raw_extent = [int(raw_bounds[a, 1]) + 1 - int(raw_bounds[a, 0]) for a in range(3)]
+    mask = None
+    if any(s == "ZScoreNormalization" and m
+           for s, m in zip(plan.normalization_schemes, plan.use_mask_for_norm)):
+        # the filled nonzero mask of crop_to_nonzero, over the crop box in raw order
+        mask = torch.empty(raw_extent, dtype=torch.uint8, device=device)
+        flag = torch.empty(64, dtype=torch.int32, device=device)
+        _native.check(min(0, lib.nnx_nonzero_mask_filled(
+            values.data_ptr(), channels, _native.i64s(raw_shape), _native.i64s(raw_start),
+            _native.i64s(raw_extent), mask.data_ptr(), flag.data_ptr(), st)),
+            "nnx_nonzero_mask_filled")
+    stats = torch.empty((channels, 2), dtype=torch.float32, device=device)
+    stat_work = None
     for c, scheme in enumerate(plan.normalization_schemes):
         if scheme == "CTNormalization":
             mean, std, lower, upper = _ct_statistics(plan, c)
             norm[c] = (mean, max(std, 1e-8), lower, upper)
+        elif scheme == "ZScoreNormalization":
+            if stat_work is None:
+                stat_work = torch.empty(lib.nnx_zscore_stats_workspace(), dtype=torch.uint8,
+                                        device=device)
+            use_mask = plan.use_mask_for_norm[c]
+            _native.check(lib.nnx_zscore_stats(
+                values.data_ptr(), channels, _native.i64s(raw_shape), c,
+                _native.i64s(raw_start), _native.i64s(raw_extent),
+                mask.data_ptr() if use_mask else None, stats[c].data_ptr(),
+                stat_work.data_ptr(), st))
+            if use_mask:
+                schemes[c] = _native.NNX_NORM_ZSCORE_MASKED
+    if stat_work is not None:
+        host_stats = stats.cpu().numpy()
+        for c, scheme in enumerate(plan.normalization_schemes):
+            if scheme == "ZScoreNormalization":
+                mean, std = (float(v) for v in host_stats[c])
+                if not (np.isfinite(mean) and np.isfinite(std)):
+                    raise ContractError("z-score normalization mask is empty")
+                norm[c, :2] = (mean, std)
     cropped = torch.empty((channels, *cropped_shape), dtype=torch.float32, device=device)
-    _native.check(lib.nnx_crop_normalize(
+    _native.check(lib.nnx_crop_normalize_masked(
         values.data_ptr(), channels, _native.i64s(raw_shape), _native.ints(forward),
         _native.i64s([start for start, _ in bounds]), _native.i64s(cropped_shape),
         _native.ints(schemes), norm.ctypes.data_as(ctypes.POINTER(ctypes.c_float)),
-        cropped.data_ptr(), st))
+        mask.data_ptr() if mask is not None else None, _native.i64s(raw_start),
+        _native.i64s(raw_extent), cropped.data_ptr(), st))
     _check_finite(lib, cropped, "normalization produced non-finite values")
 
     original_spacing = tuple(spacing[a] for a in forward)

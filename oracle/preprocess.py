@@ -55,6 +55,28 @@ def nonzero_bbox(data: np.ndarray) -> tuple[tuple[int, int], ...]:
     return tuple(bounds)
 
 
+def filled_nonzero_mask(data: np.ndarray) -> np.ndarray:
+    """The mask of ``crop_to_nonzero`` (src/nnunet_mlx/data/preprocessing.py:193-195): any
+    channel nonzero, enclosed background filled by SciPy's ``binary_fill_holes`` (the
+    reference's own dependency; default 6-connected structure)."""
+    from scipy import ndimage
+
+    return ndimage.binary_fill_holes(np.any(np.asarray(data) != 0, axis=0))
+
+
+def zscore_normalize(values: np.ndarray, mask: np.ndarray | None = None) -> np.ndarray:
+    """ZScoreNormalization of ``_normalize_channel`` (src/nnunet_mlx/data/preprocessing.py:
+    286-296): numpy float32 mean and std of the selected voxels, then (x - mean) /
+    max(std, 1e-8) in float32 on the selection; other voxels unchanged."""
+    result = np.asarray(values, dtype=np.float32).copy()
+    selection = np.ones(result.shape, dtype=bool) if mask is None else np.asarray(mask, bool)
+    selected = result[selection]
+    mean = float(selected.mean())
+    std = float(selected.std())
+    result[selection] = (result[selection] - mean) / max(std, 1e-8)
+    return result
+
+
 def ct_normalize(values: np.ndarray, mean: float, std: float, lower: float,
                  upper: float) -> np.ndarray:
     """float32 clip, subtract, divide in the reference's order."""

@@ -201,10 +201,112 @@ def test_preprocess_rejects_unsupported():
     plan = ct_plan((1.0, 1.0, 1.0))
     with pytest.raises(ContractError):
         preprocess_raw_case(np.zeros((1, 4, 4, 4), dtype=np.float32), {"spacing": [1, 1, 1]}, plan)
-    zplan = PreprocessPlan(plan.transpose_forward, plan.spacing, ("ZScoreNormalization",), (True,),
-                           plan.intensity_properties, plan.data_resampling)
+    zplan = PreprocessPlan(plan.transpose_forward, plan.spacing, ("RescaleTo01Normalization",),
+                           (False,), plan.intensity_properties, plan.data_resampling)
     with pytest.raises(ContractError):
         preprocess_raw_case(np.ones((1, 4, 4, 4), dtype=np.float32), {"spacing": [1, 1, 1]}, zplan)
     tplan = ct_plan((2.0, 2.0, 2.0), resampling="resample_torch_fornnunet")
     with pytest.raises(ContractError):
         preprocess_raw_case(np.ones((1, 8, 8, 8), dtype=np.float32), {"spacing": [1, 1, 1]}, tplan)
+
+
+def hollow_volume(rng, shape):
+    """Random blobs plus a closed shell with a sealed cavity, a shell with a tunnel to the
+    outside (not a hole), and a winding corridor that needs several sweep rounds."""
+    data = np.zeros(shape, dtype=np.float32)
+    z, y, x = np.indices(shape[1:])
+    cz, cy, cx = (s // 2 for s in shape[1:])
+    r = np.sqrt((z - cz) ** 2 + (y - cy) ** 2 + (x - cx) ** 2)
+    shell = (r >= 4) & (r < 6)
+    data[0][shell] = rng.standard_normal(int(shell.sum())) + 3
+    open_shell = (np.abs(z - 3) <= 2) & (np.abs(y - 4) <= 3) & (np.abs(x - 4) <= 3)
+    inner = (np.abs(z - 3) <= 1) & (np.abs(y - 4) <= 2) & (np.abs(x - 4) <= 2)
+    data[-1][open_shell & ~inner] = 1.5
+    data[-1][(np.abs(z - 3) <= 0) & (y == 4) & (x >= 4) & (x <= 7)] = 0   # tunnel out
+    # serpentine wall: background corridor that turns several times, sealed at one end
+    wall = np.zeros(shape[1:], dtype=bool)
+    wall[:, -9:-1, -9:-1] = True
+    for k, row in enumerate(range(-8, -2, 2)):
+        wall[:, row, (-8 if k % 2 else -7):(-2 if k % 2 else -1)] = False
+    data[0][wall] = 2.0
+    return data
+
+
+@pytest.mark.parametrize("shape", [(1, 18, 20, 22), (2, 24, 17, 30)])
+def test_filled_nonzero_mask_matches_scipy(lib, shape):
+    print(f"filled mask {shape}", flush=True)
+    data = hollow_volume(np.random.default_rng(shape[1]), shape)
+    bbox = op.nonzero_bbox(data)
+    start = [a for a, _ in bbox]
+    extent = [b - a for a, b in bbox]
+    mask = torch.empty(extent, dtype=torch.uint8, device="cuda")
+    flag = torch.empty(64, dtype=torch.int32, device="cuda")
+    rounds = lib.nnx_nonzero_mask_filled(dev(data).data_ptr(), shape[0], _native.i64s(shape[1:]),
+                                         _native.i64s(start), _native.i64s(extent),
+                                         mask.data_ptr(), flag.data_ptr(), stream())
+    assert rounds >= 1
+    want = op.filled_nonzero_mask(data)[tuple(slice(a, b) for a, b in bbox)]
+    np.testing.assert_array_equal(mask.cpu().numpy().astype(bool), want)
+
+
+@pytest.mark.parametrize("use_mask", [False, True])
+def test_zscore_stats_are_float64_statistics_rounded(lib, use_mask):
+    rng = np.random.default_rng(9)
+    shape = (2, 30, 40, 50)
+    data = hollow_volume(rng, shape)
+    data[1] += (rng.standard_normal(shape[1:]) * 50 + 100).astype(np.float32) * (data[1] != 0)
+    bbox = op.nonzero_bbox(data)
+    start, extent = [a for a, _ in bbox], [b - a for a, b in bbox]
+    crop = data[(slice(None), *(slice(a, b) for a, b in bbox))]
+    mask_np = op.filled_nonzero_mask(data)[tuple(slice(a, b) for a, b in bbox)]
+    mask = torch.from_numpy(mask_np.astype(np.uint8)).cuda() if use_mask else None
+    work = torch.empty(lib.nnx_zscore_stats_workspace(), dtype=torch.uint8, device="cuda")
+    for c in range(2):
+        stats = torch.empty(2, dtype=torch.float32, device="cuda")
+        _native.check(lib.nnx_zscore_stats(dev(data).data_ptr(), 2, _native.i64s(shape[1:]), c,
+                                           _native.i64s(start), _native.i64s(extent),
+                                           mask.data_ptr() if use_mask else None,
+                                           stats.data_ptr(), work.data_ptr(), stream()))
+        sel = crop[c][mask_np] if use_mask else crop[c].ravel()
+        mean32 = np.float32(sel.astype(np.float64).mean())
+        std32 = np.float32(np.sqrt(((sel.astype(np.float64) - np.float64(mean32)) ** 2).mean()))
+        got = stats.cpu().numpy()
+        assert abs(got[0] - mean32) <= np.spacing(abs(mean32))
+        assert abs(got[1] - std32) <= np.spacing(std32)
+        # numpy's own float32 statistics (the reference's) lie within a few float32 steps
+        assert abs(got[0] - sel.mean()) <= 8 * np.spacing(max(abs(mean32), std32))
+        assert abs(got[1] - sel.std()) <= 8 * np.spacing(std32)
+
+
+@pytest.mark.parametrize("use_mask", [False, True])
+def test_preprocess_zscore_case_matches_oracle(use_mask):
+    print(f"z-score case use_mask={use_mask}", flush=True)
+    rng = np.random.default_rng(21)
+    raw = hollow_volume(rng, (2, 20, 28, 26))
+    raw[1] = raw[1] * 40 + (raw[1] != 0) * 300
+    plans = {
+        "transpose_forward": [2, 0, 1], "transpose_backward": [1, 2, 0],
+        "configurations": {"3d_fullres": {
+            "spacing": [1.0, 1.0, 1.0],
+            "normalization_schemes": ["ZScoreNormalization", "ZScoreNormalization"],
+            "use_mask_for_norm": [use_mask, use_mask], "patch_size": [16, 16, 16],
+            "resampling_fn_data": "resample_data_or_seg_to_shape",
+            "resampling_fn_data_kwargs": {"is_seg": False, "order": 3, "order_z": 0,
+                                          "force_separate_z": None}}},
+    }
+    plan = PreprocessPlan.from_plans(plans, "3d_fullres")
+    spacing = (1.3, 0.9, 1.1)
+    out = preprocess_raw_case(raw, {"spacing": list(spacing)}, plan)
+    forward = (2, 0, 1)
+    t = raw.transpose((0, *(a + 1 for a in forward)))
+    bbox = op.nonzero_bbox(t)
+    sl = tuple(slice(a, b) for a, b in bbox)
+    crop = t[(slice(None), *sl)]
+    mask = op.filled_nonzero_mask(t)[sl] if use_mask else None
+    norm = np.stack([op.zscore_normalize(crop[c], mask) for c in range(2)])
+    original = tuple(spacing[a] for a in forward)
+    new_shape = tuple(round(o / 1.0 * s) for o, s in zip(original, crop.shape[1:]))
+    want = op.resample_data(norm, new_shape)
+    got = out.data.cpu().numpy()
+    assert got.shape == want.shape
+    np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)

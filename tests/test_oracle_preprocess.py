@@ -101,3 +101,54 @@ def test_nonzero_bbox_and_ct_normalize():
     want = (clipped - np.float32(41.5)) / np.float32(60.25)
     np.testing.assert_array_equal(got, want.astype(np.float32))
     assert got.dtype == np.float32
+
+
+def _brute_force_fill(mask):
+    """Enclosed background by breadth-first search from the border (6-neighbours)."""
+    from collections import deque
+
+    reached = np.zeros(mask.shape, dtype=bool)
+    queue = deque()
+    for idx in np.ndindex(mask.shape):
+        if not mask[idx] and any(i in (0, n - 1) for i, n in zip(idx, mask.shape)):
+            reached[idx] = True
+            queue.append(idx)
+    while queue:
+        idx = queue.popleft()
+        for axis in range(3):
+            for step in (-1, 1):
+                nb = list(idx)
+                nb[axis] += step
+                nb = tuple(nb)
+                if all(0 <= i < n for i, n in zip(nb, mask.shape)) and not mask[nb] and not reached[nb]:
+                    reached[nb] = True
+                    queue.append(nb)
+    return ~reached
+
+
+@pytest.mark.parametrize("seed", [0, 1, 2])
+def test_filled_mask_is_six_connected_hole_filling(seed):
+    from oracle.preprocess import filled_nonzero_mask
+
+    rng = np.random.default_rng(seed)
+    data = (rng.random((2, 7, 8, 9)) < 0.35).astype(np.float32) * rng.standard_normal((2, 7, 8, 9))
+    data[0, 2:5, 2:6, 2:7] = 1.0
+    data[0, 3, 3:5, 3:6] = 0.0          # sealed cavity
+    got = filled_nonzero_mask(data)
+    np.testing.assert_array_equal(got, _brute_force_fill(np.any(data != 0, axis=0)))
+    assert got[3, 3, 3]
+
+
+def test_zscore_normalize_closed_form():
+    from oracle.preprocess import zscore_normalize
+
+    rng = np.random.default_rng(5)
+    x = (rng.standard_normal((6, 7, 8)) * 30 + 100).astype(np.float32)
+    mask = rng.random(x.shape) < 0.6
+    got = zscore_normalize(x, mask)
+    sel = x[mask].astype(np.float64)
+    want = (x.astype(np.float64) - sel.mean()) / sel.std()
+    np.testing.assert_allclose(got[mask], want[mask], rtol=0, atol=2e-5)
+    np.testing.assert_array_equal(got[~mask], x[~mask])
+    const = zscore_normalize(np.full((3, 3, 3), 7.0, dtype=np.float32))
+    np.testing.assert_array_equal(const, np.zeros((3, 3, 3), dtype=np.float32))
