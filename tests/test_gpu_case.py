@@ -160,3 +160,51 @@ def test_cli_predicts_an_upstream_folder(tmp_path, monkeypatch):
     # the second call reuses the conversion and skips the finished case
     assert main(["predict", "-i", str(tmp_path / "in"), "-o", str(tmp_path / "out"), "-d", "1",
                  "-c", "3d_fullres", "-f", "0", "--continue_prediction"]) == 0
+
+
+def test_brats_style_mri_case(tmp_path):
+    """Four MRI channels, z-score normalisation inside the filled nonzero mask, isotropic
+    1 mm plans, the five-fold ensemble the named BraTS entry runs: against the oracle chain."""
+    from nnunet_mlx.named_models import brats
+
+    spec = PlainConvUNetSpec(4, 5, (8, 16), ((3, 3, 3),) * 2, ((1, 1, 1), (2, 2, 2)), (2, 2), (2,))
+    folder = write_random_model_folder(tmp_path / "model", spec, patch_size=(16, 24, 24),
+                                       seeds=tuple(range(5)),
+                                       labels=("edema", "nonenh", "empty", "enh"))
+    plans = json.loads((folder / "plans.json").read_text())
+    cfg = plans["configurations"]["3d_fullres"]
+    cfg["use_mask_for_norm"] = [True] * 4
+    cfg["spacing"] = [1.0, 1.0, 1.0]
+    (folder / "plans.json").write_text(json.dumps(plans))
+    rng = np.random.default_rng(12)
+    z, y, x = np.mgrid[0:20, 0:30, 0:28]
+    head = ((z - 10) / 8.0) ** 2 + ((y - 15) / 12.0) ** 2 + ((x - 14) / 11.0) ** 2 < 1
+    ventricle = ((z - 10) / 2.0) ** 2 + ((y - 15) / 3.0) ** 2 + ((x - 14) / 3.0) ** 2 < 1
+    images, channels = {}, []
+    for c, name in enumerate(brats.CHANNELS):
+        vol = np.zeros((20, 30, 28), dtype=np.float32)
+        vol[head] = (rng.standard_normal(int(head.sum())) * 100 + 400 + 50 * c).astype(np.float32)
+        vol[ventricle] = 0.0                       # a sealed zero cavity: inside the mask
+        nifti.write_nifti(tmp_path / f"{name}.nii.gz", vol, (1.0, 1.0, 1.0))
+        images[name] = tmp_path / f"{name}.nii.gz"
+        channels.append(vol)
+    print("raw case: BraTS-style 4-channel MRI, masked z-score", flush=True)
+    result = brats.run(image_paths=images, output_dir=tmp_path / "out", weights_path=folder)
+    mask = nifti.read_nifti(result["outputs"]["mask"]).array
+    raw = np.stack(channels)
+    bbox = op.nonzero_bbox(raw)
+    sl = tuple(slice(a, b) for a, b in bbox)
+    filled = op.filled_nonzero_mask(raw)[sl]
+    assert filled.sum() > np.any(raw != 0, axis=0)[sl].sum()   # the cavity is filled
+    data = np.stack([op.zscore_normalize(raw[c][sl], filled) for c in range(4)])
+    nets = [OracleNetwork(spec, random_weights(spec, s)) for s in range(5)]
+    logits, _ = osw.predict(nets, data, (16, 24, 24), num_classes=5, axes=(0, 1, 2),
+                            step_fraction=0.5, accumulation="nnunet-fp16")
+    labels = np.argmax(logits, axis=-1)
+    want = np.zeros(raw.shape[1:], dtype=np.uint16)
+    want[sl] = labels
+    agree = (mask == want).mean()
+    print(f"label agreement {agree:.6f}, classes {np.bincount(want.ravel(), minlength=5)}",
+          flush=True)
+    assert agree >= 0.999
+    assert result["details"]["folds"] == [0, 1, 2, 3, 4]
