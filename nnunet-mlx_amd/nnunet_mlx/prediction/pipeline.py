@@ -179,16 +179,47 @@ class ModelFolderPredictor:
                        overwrite: bool = False, continue_prediction: bool = False
                        ) -> list[CasePrediction]:
         """Predict every case of an nnU-Net input folder (``<case>_<XXXX><ending>`` per
-        channel) into ``<output>/<case><ending>`` (src/nnunet_mlx/prediction/pipeline.py:389-449)."""
+        channel) into ``<output>/<case><ending>`` (src/nnunet_mlx/prediction/pipeline.py:389-449).
+
+        Host I/O overlaps the GPU: one reader thread loads (and decompresses) the next case
+        while the current one runs, and one writer thread compresses and writes the
+        previous label image; every GPU call stays on the calling thread."""
+        from concurrent.futures import ThreadPoolExecutor
+
+        from nnunet_mlx.storage.nifti import read_images, write_segmentation
+
         cases = case_files(input_folder, self.bundle.file_ending, self.bundle.image_channels)
         out = Path(output_folder)
         out.mkdir(parents=True, exist_ok=True)
-        results = []
+        todo = []
         for case, files in cases.items():
             target = out / f"{case}{self.bundle.file_ending}"
             if continue_prediction and target.is_file():
                 continue
-            results.append(self.predict_case(files, target, overwrite=overwrite))
+            if target.exists() and not overwrite:
+                raise ContractError(f"segmentation output already exists: {target}")
+            todo.append((files, target))
+        results: list[CasePrediction] = []
+        with ThreadPoolExecutor(1) as reader, ThreadPoolExecutor(1) as writer:
+            pending_read = reader.submit(read_images, todo[0][0]) if todo else None
+            pending_write = None
+            for index, (files, target) in enumerate(todo):
+                start = perf_counter()
+                data, properties = pending_read.result()
+                read_wait = perf_counter() - start
+                if index + 1 < len(todo):
+                    pending_read = reader.submit(read_images, todo[index + 1][0])
+                segmentation, details = self.predict_raw(data, properties)
+                del data
+                if pending_write is not None:
+                    pending_write.result()
+                pending_write = writer.submit(write_segmentation, segmentation, target,
+                                              properties, overwrite=True)
+                metrics = {"read_wait_s": read_wait, **details["metrics"]}
+                results.append(CasePrediction((target,), segmentation,
+                                              details["preprocessed_shape"], metrics))
+            if pending_write is not None:
+                pending_write.result()
         return results
 
 

@@ -148,15 +148,17 @@ def test_cli_predicts_an_upstream_folder(tmp_path, monkeypatch):
                upstream / "fold_0" / "checkpoint_final.pth")
     (tmp_path / "in").mkdir()
     synthetic_ct(tmp_path / "in" / "c1_0000.nii.gz", seed=6)
+    synthetic_ct(tmp_path / "in" / "c2_0000.nii.gz", seed=7)
     monkeypatch.setenv("NNUNET_MLX_CACHE", str(tmp_path / "cache"))
     print("raw case: CLI predict -d over an upstream results folder", flush=True)
     monkeypatch.setenv("nnUNet_results", str(tmp_path / "results"))
     assert main(["predict", "-i", str(tmp_path / "in"), "-o", str(tmp_path / "out"), "-d", "1",
                  "-c", "3d_fullres", "-f", "0"]) == 0
-    got = nifti.read_nifti(tmp_path / "out" / "c1.nii.gz").array
-    ref = medmlx.run(weights_path=folder, image_paths=[tmp_path / "in" / "c1_0000.nii.gz"],
-                     output_dir=tmp_path / "ref")
-    np.testing.assert_array_equal(got, nifti.read_nifti(ref["outputs"]["mask"]).array)
+    for case in ("c1", "c2"):   # cases read, predicted and written in overlapped order
+        got = nifti.read_nifti(tmp_path / "out" / f"{case}.nii.gz").array
+        ref = medmlx.run(weights_path=folder, image_paths=[tmp_path / "in" / f"{case}_0000.nii.gz"],
+                         output_dir=tmp_path / f"ref_{case}")
+        np.testing.assert_array_equal(got, nifti.read_nifti(ref["outputs"]["mask"]).array)
     # the second call reuses the conversion and skips the finished case
     assert main(["predict", "-i", str(tmp_path / "in"), "-o", str(tmp_path / "out"), "-d", "1",
                  "-c", "3d_fullres", "-f", "0", "--continue_prediction"]) == 0
