@@ -27,10 +27,16 @@ Restates, in numpy:
     per plane) and then the coarse axis with half-pixel nearest indices (order 0),
     rounding to float32 once.
 
+  * ``filled_nonzero_mask`` / ``zscore_normalize``: the filled nonzero mask of
+    ``crop_to_nonzero`` (SciPy's ``binary_fill_holes``, the reference's own call) and the
+    ZScoreNormalization branch in numpy float32.
+
 Pinned by tests/test_oracle_preprocess.py against ``scipy.ndimage.spline_filter1d``
 (prefilter coefficients), ``scipy.ndimage.zoom`` (whole resize, float64 and float32, orders
 1 and 3, 2-D and 3-D, up- and down-sampling), closed forms (constant and linear volumes
-are reproduced), and numpy for crop bounds and normalisation.
+are reproduced), numpy for crop bounds and normalisation, a breadth-first flood fill from
+the border for the filled mask, and the float64 closed form of the z-score (constant
+channel -> zeros).
 """
 
 from __future__ import annotations

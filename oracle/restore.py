@@ -18,6 +18,13 @@ Restates, in numpy float64:
     class (src/nnunet_mlx/kernels/metal_restore.py:119-137;
     src/nnunet_mlx/prediction/restore.py:195-215).
 
+``restore_labels_spline`` is the reference's host restoration for spline plans
+(src/nnunet_mlx/prediction/restore.py:28-158): each class resampled by
+``preprocess.resample_data`` (separate axis or whole volume, float16 logits rounded once to
+float16), then numpy's first-maximum argmax.  Its order-1 whole-volume route is pinned
+against ``restore_labels`` (the same interpolation reached independently) and its
+separate-axis route per plane against ``scipy.ndimage.zoom``.
+
 Pinned by tests/test_oracle_restore.py against: scipy.ndimage.zoom(order=1,
 mode="nearest", grid_mode=True) in float64 (the host resampler's order-1 half-pixel
 interpolation with edge extension; values to 1e-12, labels exactly), a per-voxel
