@@ -129,6 +129,7 @@ struct IgemmArgs {
   int tz, ty, tx;
   int ntn, nwg;
   float4* stats;  // optional per-tile InstanceNorm partials [b][tile][cout] (mean, M2, n, 0)
+  int vstore;     // epilogue through LDS with 16-byte stores (every column block full)
   const uint4* w16;   // split-fp16 packed weights (x3 kernel)
   int ntg;            // tap groups of 4 (x3 kernel)
   float out_scale;    // 1 / weight scale (x3 kernel)
@@ -212,7 +213,9 @@ __device__ __forceinline__ HaloSource halo_source(const IgemmArgs& a, int chunk)
 // (nbk0+nb)*16 + row.  Values are first multiplied by out_scale (a power of two undoing a
 // weight scale, exact; skipped when 1), then the bias is added as a separate float32
 // addition; optional fused InstanceNorm partials, then the stores.
-template <int MB, int NB, int WM, int WN>
+// VST: with a.vstore set, the tile is transposed through LDS (rows padded by 4 floats) and
+// written as whole 16-byte words per lane, each voxel's channel run contiguous
+template <int MB, int NB, int WM, int WN, bool VST = false>
 __device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB][NB], float* lds,
                                                int wm, int wn, int slot, int row, int nbk0, int b,
                                                int tzi, int tyi, int txi, int oz0, int oy0, int ox0,
@@ -319,6 +322,38 @@ __device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB]
         if (n < a.cout)
           a.stats[((int64_t)b * spt + tile_s) * a.cout + n] = make_float4(mean[nb], t, cnt, 0.f);
       }
+    }
+  }
+  if constexpr (VST) {
+    if (a.vstore) {
+      constexpr int NCOL = 16 * NB * WN;
+      constexpr int LDW = NCOL + 4;
+      constexpr int MT = 16 * MB * WM;
+      constexpr int NT = 64 * WM * WN;
+      constexpr int Q = NCOL / 4;
+      float* tile_out = lds;
+      __syncthreads();  // every wave is past its last halo, weight and partial-sum read
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int v = 16 * (wm * MB + mb) + 4 * slot + r;
+#pragma unroll
+          for (int nb = 0; nb < NB; ++nb)
+            tile_out[v * LDW + (wn * NB + nb) * 16 + row] =
+                has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+        }
+      __syncthreads();
+      const int n0 = (nbk0 - wn * NB) * 16;
+      for (int i = threadIdx.x; i < MT * Q; i += NT) {
+        const int v = i / Q, q = i - v * Q;
+        const int z = oz0 + (v >> a.lbxy), yy = oy0 + ((v >> a.lbx) & (a.by - 1)),
+                  xx = ox0 + (v & (a.bx - 1));
+        if (z < a.od && yy < a.oh && xx < a.ow)
+          *reinterpret_cast<f4*>(a.y + ((((int64_t)b * a.od + z) * a.oh + yy) * a.ow + xx) * a.cout +
+                                 n0 + 4 * q) = *reinterpret_cast<const f4*>(tile_out + v * LDW + 4 * q);
+      }
+      return;
     }
   }
 #pragma unroll
@@ -957,8 +992,8 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
       mma_products<AR>(acc, A[cur], B[cur]);
     }
   }
-  igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
-                                 ox0, a.out_scale);
+  igemm_epilogue<MB, NB, WM, WN, true>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi,
+                                       oz0, oy0, ox0, a.out_scale);
 }
 
 // Split-fp16 weight packing: 16-byte words packed[((chunk * groups + g) * nblk + nb) * 128 +
@@ -1170,6 +1205,10 @@ void launch_x3s(const IgemmArgs& a, bool vec, int arith, hipStream_t st, double 
   const size_t red_bytes = (size_t)WM * 16 * NB * WN * sizeof(float);
   size_t lds_bytes = x3s_lds_bytes((int64_t)a.hz * a.hy * a.hx, a.ntg, WN * NB);
   if (lds_bytes < red_bytes) lds_bytes = red_bytes;
+  if (a.vstore) {
+    const size_t tile_bytes = (size_t)16 * MB * WM * (16 * NB * WN + 4) * sizeof(float);
+    if (lds_bytes < tile_bytes) lds_bytes = tile_bytes;
+  }
   ProfScope prof(names[arith == kBf16].c_str(), flops, bytes, st);
   if (a.ntg == 7)
     launch_x3s_ntg<MB, NB, WM, WN, 7>(a, vec, arith, lds_bytes, st);
@@ -2366,6 +2405,8 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
   igemm_work(g, c1, c2, cout, &flops, &bytes);
   const bool vec = c1 % kChunk == 0 && c2 % kChunk == 0;
   if (plan.staged) {
+    // whole 32-column blocks and 16-byte aligned rows: the epilogue writes float4 words
+    a.vstore = cout % 32 == 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0;
     launch_x3s<4, 2, 4, 1>(a, vec, arith, st, flops, bytes);
     return;
   }
