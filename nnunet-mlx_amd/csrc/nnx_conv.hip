@@ -246,81 +246,152 @@ __device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB]
     return *z < a.od && *yy < a.oh && *xx < a.ow;
   };
   if (a.stats) {
-    // InstanceNorm partials of this tile, two-pass over the registers: the tile mean of
-    // every channel (lane sums, xor-shuffles over the 4 row slots, then the WM waves
-    // through LDS), then the centred sum of squares about it.
-    constexpr int NWG = 16 * NB * WN;
-    float* red = lds;  // WM * NWG floats; the halo is no longer read
-    const float cnt = (float)((a.od - oz0 < a.bz ? a.od - oz0 : a.bz) *
-                              (a.oh - oy0 < a.by ? a.oh - oy0 : a.by) *
-                              (a.ow - ox0 < a.bx ? a.ow - ox0 : a.bx));
-    float part[NB], mean[NB];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) part[nb] = 0.f;
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int z, yy, xx;
-        if (voxel_ok(mb, r, &z, &yy, &xx)) {
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb)
-            part[nb] += has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
-        }
-      }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      part[nb] += __shfl_xor(part[nb], 16);
-      part[nb] += __shfl_xor(part[nb], 32);
-    }
-    __syncthreads();
-    if (slot == 0) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      float t = 0.f;
-      for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
-      mean[nb] = t / cnt;
-      part[nb] = 0.f;
-    }
-#pragma unroll
-    for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        int z, yy, xx;
-        if (voxel_ok(mb, r, &z, &yy, &xx)) {
-#pragma unroll
-          for (int nb = 0; nb < NB; ++nb) {
-            const float v = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
-            const float d = v - mean[nb];
-            part[nb] = fmaf(d, d, part[nb]);
-          }
-        }
-      }
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      part[nb] += __shfl_xor(part[nb], 16);
-      part[nb] += __shfl_xor(part[nb], 32);
-    }
-    __syncthreads();
-    if (slot == 0) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
-    }
-    __syncthreads();
-    if (wm == 0 && slot == 0) {
-      const int tile_s = (tzi * a.ty + tyi) * a.tx + txi;
-      const int spt = a.tz * a.ty * a.tx;
+    if constexpr (VST) {
+      // InstanceNorm partials of this tile in one pass: per wave, sums of d = v - s and d^2
+      // about a shift s (the wave's first voxel, finite), over the valid voxels; the WM
+      // waves' (n, mean, M2) are then merged (Chan) through LDS.
+      float4* red4 = reinterpret_cast<float4*>(lds);  // WM * 16 * NB * WN entries
+      constexpr int NWG = 16 * NB * WN;
+      float sd[NB], sq[NB], sh[NB];
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) {
-        const int n = (nbk0 + nb) * 16 + row;
+        const float v0 = has_bias ? acc[0][nb][0] + bias_n[nb] : acc[0][nb][0];
+        sh[nb] = __shfl(v0, row);  // lane `row` holds voxel 16 * wm * MB of column row
+        sd[nb] = 0.f;
+        sq[nb] = 0.f;
+      }
+      float nv = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          int z, yy, xx;
+          if (voxel_ok(mb, r, &z, &yy, &xx)) {
+            nv += 1.f;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              const float d = (has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r]) - sh[nb];
+              sd[nb] += d;
+              sq[nb] = fmaf(d, d, sq[nb]);
+            }
+          }
+        }
+      nv += __shfl_xor(nv, 16);
+      nv += __shfl_xor(nv, 32);
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        sd[nb] += __shfl_xor(sd[nb], 16);
+        sd[nb] += __shfl_xor(sd[nb], 32);
+        sq[nb] += __shfl_xor(sq[nb], 16);
+        sq[nb] += __shfl_xor(sq[nb], 32);
+      }
+      __syncthreads();  // every wave is past its last halo and weight read
+      if (slot == 0) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+          red4[wm * NWG + (wn * NB + nb) * 16 + row] = make_float4(sd[nb], sq[nb], sh[nb], nv);
+      }
+      __syncthreads();
+      if (wm == 0 && slot == 0) {
+        const int tile_s = (tzi * a.ty + tyi) * a.tx + txi;
+        const int spt = a.tz * a.ty * a.tx;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int n = (nbk0 + nb) * 16 + row;
+          float cnt = 0.f, mean = 0.f, m2 = 0.f;
+          for (int w = 0; w < WM; ++w) {
+            const float4 e = red4[w * NWG + (wn * NB + nb) * 16 + row];
+            if (e.w > 0.f) {
+              const float mw = e.z + e.x / e.w;
+              const float m2w = fmaxf(e.y - e.x * (e.x / e.w), 0.f);
+              const float tot = cnt + e.w;
+              const float delta = mw - mean;
+              mean += delta * (e.w / tot);
+              m2 += m2w + delta * delta * (cnt * e.w / tot);
+              cnt = tot;
+            }
+          }
+          if (n < a.cout)
+            a.stats[((int64_t)b * spt + tile_s) * a.cout + n] = make_float4(mean, m2, cnt, 0.f);
+        }
+      }
+    } else {
+      // InstanceNorm partials of this tile, two-pass over the registers: the tile mean of
+      // every channel (lane sums, xor-shuffles over the 4 row slots, then the WM waves
+      // through LDS), then the centred sum of squares about it.
+      constexpr int NWG = 16 * NB * WN;
+      float* red = lds;  // WM * NWG floats; the halo is no longer read
+      const float cnt = (float)((a.od - oz0 < a.bz ? a.od - oz0 : a.bz) *
+                                (a.oh - oy0 < a.by ? a.oh - oy0 : a.by) *
+                                (a.ow - ox0 < a.bx ? a.ow - ox0 : a.bx));
+      float part[NB], mean[NB];
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) part[nb] = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          int z, yy, xx;
+          if (voxel_ok(mb, r, &z, &yy, &xx)) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb)
+              part[nb] += has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+          }
+        }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        part[nb] += __shfl_xor(part[nb], 16);
+        part[nb] += __shfl_xor(part[nb], 32);
+      }
+      __syncthreads();
+      if (slot == 0) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
         float t = 0.f;
         for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
-        if (n < a.cout)
-          a.stats[((int64_t)b * spt + tile_s) * a.cout + n] = make_float4(mean[nb], t, cnt, 0.f);
+        mean[nb] = t / cnt;
+        part[nb] = 0.f;
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          int z, yy, xx;
+          if (voxel_ok(mb, r, &z, &yy, &xx)) {
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+              const float v = has_bias ? acc[mb][nb][r] + bias_n[nb] : acc[mb][nb][r];
+              const float d = v - mean[nb];
+              part[nb] = fmaf(d, d, part[nb]);
+            }
+          }
+        }
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        part[nb] += __shfl_xor(part[nb], 16);
+        part[nb] += __shfl_xor(part[nb], 32);
+      }
+      __syncthreads();
+      if (slot == 0) {
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) red[wm * NWG + (wn * NB + nb) * 16 + row] = part[nb];
+      }
+      __syncthreads();
+      if (wm == 0 && slot == 0) {
+        const int tile_s = (tzi * a.ty + tyi) * a.tx + txi;
+        const int spt = a.tz * a.ty * a.tx;
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          const int n = (nbk0 + nb) * 16 + row;
+          float t = 0.f;
+          for (int w = 0; w < WM; ++w) t += red[w * NWG + (wn * NB + nb) * 16 + row];
+          if (n < a.cout)
+            a.stats[((int64_t)b * spt + tile_s) * a.cout + n] = make_float4(mean[nb], t, cnt, 0.f);
+        }
       }
     }
   }
