@@ -320,7 +320,7 @@ int nnx_crop_normalize(const float* d_data, int channels, const int64_t* size,
                        const int* transpose, const int64_t* start, const int64_t* out_size,
                        const int* schemes, const float* norm, float* d_out, void* stream);
 /* Z-score normalisation (ZScoreNormalization of _normalize_channel,
- * src/nnunet_mlx/data/preprocessing.py:286-296, with the filled nonzero mask of
+ * src/nnunet_mlx/data/preprocessing.py:298-307, with the filled nonzero mask of
  * crop_to_nonzero, :166-214).
  *
  * nnx_nonzero_mask_filled: d_mask (extent[0], extent[1], extent[2]) uint8 over the raw box
@@ -344,6 +344,14 @@ size_t nnx_zscore_stats_workspace(void);
 int nnx_zscore_stats(const float* d_data, int channels, const int64_t* size, int channel,
                      const int64_t* start, const int64_t* extent, const uint8_t* d_mask,
                      float* d_stats, void* d_work, void* stream);
+/* d_minmax[0..1] = (min, max) of channel `channel` over the raw box (start, extent);
+ * d_work: nnx_zscore_stats_workspace bytes.  The extrema of RescaleTo01Normalization and the
+ * range check of RGBTo01Normalization (src/nnunet_mlx/data/preprocessing.py:310-319); both
+ * then normalise as NNX_NORM_ZSCORE with (mean, std) = (min, max(max - min, 1e-8)) and
+ * (0, 255). */
+int nnx_channel_minmax(const float* d_data, int channels, const int64_t* size, int channel,
+                       const int64_t* start, const int64_t* extent, float* d_minmax,
+                       void* d_work, void* stream);
 int nnx_crop_normalize_masked(const float* d_data, int channels, const int64_t* size,
                               const int* transpose, const int64_t* start,
                               const int64_t* out_size, const int* schemes, const float* norm,

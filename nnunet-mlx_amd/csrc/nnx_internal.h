@@ -191,6 +191,9 @@ void crop_normalize_masked(const float* x, int channels, const int64_t* size,
 int nonzero_mask_filled(const float* x, int channels, const int64_t* size, const int64_t* start,
                         const int64_t* extent, uint8_t* mask, void* work, hipStream_t st);
 size_t zscore_stats_workspace();
+void box_minmax(const float* x, int channels, const int64_t* size, int channel,
+                const int64_t* start, const int64_t* extent, float* minmax, void* work,
+                hipStream_t st);
 void zscore_stats(const float* x, int channels, const int64_t* size, int channel,
                   const int64_t* start, const int64_t* extent, const uint8_t* mask, float* stats,
                   void* work, hipStream_t st);

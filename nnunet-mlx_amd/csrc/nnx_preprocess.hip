@@ -184,6 +184,55 @@ __global__ __launch_bounds__(256) void mask_finish_kernel(uint8_t* __restrict__ 
     cell[e] = cell[e] != 1;
 }
 
+// ---- channel extrema over the crop box ----------------------------------------------------
+
+__global__ __launch_bounds__(256) void box_minmax_partial_kernel(
+    const float* __restrict__ xc, int64_t Y, int64_t Z, int64_t b0, int64_t b1, int64_t b2,
+    int64_t E0, int64_t E1, int64_t E2, float2* __restrict__ partial) {
+  __shared__ float smin[4], smax[4];
+  const int64_t total = E0 * E1 * E2;
+  float lo = INFINITY, hi = -INFINITY;
+  for (int64_t e = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; e < total;
+       e += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t i2 = e % E2, i1 = (e / E2) % E1, i0 = e / (E1 * E2);
+    const float v = xc[((b0 + i0) * Y + (b1 + i1)) * Z + (b2 + i2)];
+    lo = fminf(lo, v);
+    hi = fmaxf(hi, v);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o));
+    hi = fmaxf(hi, __shfl_xor(hi, o));
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    smin[wave] = lo;
+    smax[wave] = hi;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0)
+    partial[blockIdx.x] = make_float2(fminf(fminf(smin[0], smin[1]), fminf(smin[2], smin[3])),
+                                      fmaxf(fmaxf(smax[0], smax[1]), fmaxf(smax[2], smax[3])));
+}
+
+__global__ __launch_bounds__(64) void box_minmax_final_kernel(const float2* __restrict__ partial,
+                                                             int parts, float* __restrict__ out) {
+  float lo = INFINITY, hi = -INFINITY;
+  for (int i = threadIdx.x; i < parts; i += 64) {
+    lo = fminf(lo, partial[i].x);
+    hi = fmaxf(hi, partial[i].y);
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    lo = fminf(lo, __shfl_xor(lo, o));
+    hi = fmaxf(hi, __shfl_xor(hi, o));
+  }
+  if (threadIdx.x == 0) {
+    out[0] = lo;
+    out[1] = hi;
+  }
+}
+
 // ---- z-score statistics -----------------------------------------------------------------
 // Per block: float64 sums over the crop box of channel c (mask cells only when `mask`),
 // pass 0: (sum x, count), pass 1: (sum (x - mean32)^2, count) with mean32 = stats[2c].
@@ -684,6 +733,26 @@ void zscore_stats(const float* x, int channels, const int64_t* size, int channel
                        stats);
   }
   launch_check("zscore_stats");
+}
+
+void box_minmax(const float* x, int channels, const int64_t* size, int channel,
+                const int64_t* start, const int64_t* extent, float* minmax, void* work,
+                hipStream_t st) {
+  require(x && size && start && extent && minmax && work, "extrema pointers must not be null");
+  require(channel >= 0 && channel < channels, "extrema channel out of range");
+  for (int a = 0; a < 3; ++a)
+    require(extent[a] >= 1 && start[a] >= 0 && start[a] + extent[a] <= size[a],
+            "extrema box outside the volume");
+  const int64_t total = extent[0] * extent[1] * extent[2];
+  const float* xc = x + (int64_t)channel * size[0] * size[1] * size[2];
+  float2* partial = static_cast<float2*>(work);  // zscore_stats_workspace() bytes suffice
+  const int blocks = (int)std::min<int64_t>(kStatBlocks, ceil_div(total, 256));
+  ProfScope prof("preprocess_minmax", 0.0, 4.0 * (double)total, st);
+  hipLaunchKernelGGL(box_minmax_partial_kernel, dim3(blocks), dim3(256), 0, st, xc, size[1],
+                     size[2], start[0], start[1], start[2], extent[0], extent[1], extent[2],
+                     partial);
+  hipLaunchKernelGGL(box_minmax_final_kernel, dim3(1), dim3(64), 0, st, partial, blocks, minmax);
+  launch_check("box_minmax");
 }
 
 void crop_normalize(const float* x, int channels, const int64_t* size, const int* transpose,

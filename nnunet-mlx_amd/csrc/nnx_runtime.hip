@@ -1188,6 +1188,15 @@ int nnx_nonzero_mask_filled(const float* d_data, int channels, const int64_t* si
 
 size_t nnx_zscore_stats_workspace(void) { return zscore_stats_workspace(); }
 
+int nnx_channel_minmax(const float* d_data, int channels, const int64_t* size, int channel,
+                       const int64_t* start, const int64_t* extent, float* d_minmax,
+                       void* d_work, void* stream) {
+  return guarded([&] {
+    box_minmax(d_data, channels, size, channel, start, extent, d_minmax, d_work,
+               as_stream(stream));
+  });
+}
+
 int nnx_zscore_stats(const float* d_data, int channels, const int64_t* size, int channel,
                      const int64_t* start, const int64_t* extent, const uint8_t* d_mask,
                      float* d_stats, void* d_work, void* stream) {

@@ -197,6 +197,11 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         ctypes.c_int, [c_void_p, ctypes.c_int, c_i64_p, c_i64_p, c_i64_p, c_void_p, c_void_p, c_void_p]
     ),
     "nnx_zscore_stats_workspace": (ctypes.c_size_t, []),
+    "nnx_channel_minmax": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_i64_p, ctypes.c_int, c_i64_p, c_i64_p, c_void_p, c_void_p,
+         c_void_p],
+    ),
     "nnx_zscore_stats": (
         ctypes.c_int,
         [c_void_p, ctypes.c_int, c_i64_p, ctypes.c_int, c_i64_p, c_i64_p, c_void_p, c_void_p,

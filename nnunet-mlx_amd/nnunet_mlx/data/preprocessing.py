@@ -15,8 +15,10 @@ computes shapes and reads back the six crop bounds and the z-score statistics.  
 path covers CTNormalization, NoNormalization and ZScoreNormalization (with or without the
 filled nonzero mask; mean and std accumulated in float64 and rounded to float32, within a
 few float32 steps of numpy's float32 statistics) and spline plans
-(``resample_data_or_seg_to_shape``; orders 1 and 3, order_z 0); RescaleTo01/RGBTo01, the
-Torch-grid resampler and cascade inputs raise ``ContractError`` rather than run elsewhere.
+(``resample_data_or_seg_to_shape``; orders 1 and 3, order_z 0); RescaleTo01 and RGBTo01 run
+as the z-score form with host-computed (min, max - min) and (0, 255) after a device min/max
+(``nnx_channel_minmax``).  The Torch-grid resampler and cascade inputs raise
+``ContractError`` rather than run elsewhere.
 """
 
 from __future__ import annotations
@@ -33,7 +35,11 @@ from nnunet_mlx.errors import ContractError
 from nnunet_mlx.plans import ResamplingContract, resolve_configuration
 
 DEVICE_SCHEMES = {"NoNormalization": _native.NNX_NORM_NONE, "CTNormalization": _native.NNX_NORM_CT,
-                  "ZScoreNormalization": _native.NNX_NORM_ZSCORE}
+                  "ZScoreNormalization": _native.NNX_NORM_ZSCORE,
+                  # (x - min) / max(max - min, 1e-8) and x / 255: the z-score form with
+                  # host-computed (mean, std)
+                  "RescaleTo01Normalization": _native.NNX_NORM_ZSCORE,
+                  "RGBTo01Normalization": _native.NNX_NORM_ZSCORE}
 
 
 @dataclass(frozen=True)
@@ -224,8 +230,26 @@ def preprocess_raw_case(data, properties: Mapping[str, object], plan: Preprocess
                 stat_work.data_ptr(), st))
             if use_mask:
                 schemes[c] = _native.NNX_NORM_ZSCORE_MASKED
+        elif scheme in ("RescaleTo01Normalization", "RGBTo01Normalization"):
+            if stat_work is None:
+                stat_work = torch.empty(lib.nnx_zscore_stats_workspace(), dtype=torch.uint8,
+                                        device=device)
+            _native.check(lib.nnx_channel_minmax(
+                values.data_ptr(), channels, _native.i64s(raw_shape), c,
+                _native.i64s(raw_start), _native.i64s(raw_extent), stats[c].data_ptr(),
+                stat_work.data_ptr(), st))
     if stat_work is not None:
         host_stats = stats.cpu().numpy()
+        for c, scheme in enumerate(plan.normalization_schemes):
+            if scheme == "RescaleTo01Normalization":
+                low, high = (np.float32(v) for v in host_stats[c])
+                # the float32 operations of _normalize_channel: x - min, then / max(x - min)
+                norm[c, :2] = (low, max(float(np.float32(high - low)), 1e-8))
+            elif scheme == "RGBTo01Normalization":
+                low, high = (float(v) for v in host_stats[c])
+                if low < 0 or high > 255:
+                    raise ContractError("RGB normalization requires values in [0, 255]")
+                norm[c, :2] = (0.0, 255.0)
         for c, scheme in enumerate(plan.normalization_schemes):
             if scheme == "ZScoreNormalization":
                 mean, std = (float(v) for v in host_stats[c])

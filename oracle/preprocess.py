@@ -72,7 +72,7 @@ def filled_nonzero_mask(data: np.ndarray) -> np.ndarray:
 
 def zscore_normalize(values: np.ndarray, mask: np.ndarray | None = None) -> np.ndarray:
     """ZScoreNormalization of ``_normalize_channel`` (src/nnunet_mlx/data/preprocessing.py:
-    286-296): numpy float32 mean and std of the selected voxels, then (x - mean) /
+    298-307): numpy float32 mean and std of the selected voxels, then (x - mean) /
     max(std, 1e-8) in float32 on the selection; other voxels unchanged."""
     result = np.asarray(values, dtype=np.float32).copy()
     selection = np.ones(result.shape, dtype=bool) if mask is None else np.asarray(mask, bool)
@@ -80,6 +80,23 @@ def zscore_normalize(values: np.ndarray, mask: np.ndarray | None = None) -> np.n
     mean = float(selected.mean())
     std = float(selected.std())
     result[selection] = (result[selection] - mean) / max(std, 1e-8)
+    return result
+
+
+def rescale01_normalize(values: np.ndarray) -> np.ndarray:
+    """RescaleTo01Normalization (src/nnunet_mlx/data/preprocessing.py:310-313), numpy float32."""
+    result = np.asarray(values, dtype=np.float32).copy()
+    result -= float(result.min())
+    result /= max(float(result.max()), 1e-8)
+    return result
+
+
+def rgb01_normalize(values: np.ndarray) -> np.ndarray:
+    """RGBTo01Normalization (src/nnunet_mlx/data/preprocessing.py:314-318), numpy float32."""
+    result = np.asarray(values, dtype=np.float32).copy()
+    if float(result.min()) < 0 or float(result.max()) > 255:
+        raise ValueError("RGB normalization requires values in [0, 255]")
+    result /= 255
     return result
 
 

@@ -201,7 +201,7 @@ def test_preprocess_rejects_unsupported():
     plan = ct_plan((1.0, 1.0, 1.0))
     with pytest.raises(ContractError):
         preprocess_raw_case(np.zeros((1, 4, 4, 4), dtype=np.float32), {"spacing": [1, 1, 1]}, plan)
-    zplan = PreprocessPlan(plan.transpose_forward, plan.spacing, ("RescaleTo01Normalization",),
+    zplan = PreprocessPlan(plan.transpose_forward, plan.spacing, ("MyOwnNormalization",),
                            (False,), plan.intensity_properties, plan.data_resampling)
     with pytest.raises(ContractError):
         preprocess_raw_case(np.ones((1, 4, 4, 4), dtype=np.float32), {"spacing": [1, 1, 1]}, zplan)
@@ -310,3 +310,31 @@ def test_preprocess_zscore_case_matches_oracle(use_mask):
     got = out.data.cpu().numpy()
     assert got.shape == want.shape
     np.testing.assert_allclose(got, want, rtol=2e-5, atol=2e-5)
+
+
+def test_preprocess_rescale_and_rgb_match_oracle():
+    print("rescale01 / rgb01 case", flush=True)
+    rng = np.random.default_rng(31)
+    raw = np.zeros((2, 14, 18, 16), dtype=np.float32)
+    raw[0, 2:12, 3:15, 1:14] = rng.standard_normal((10, 12, 13)).astype(np.float32) * 70 + 20
+    raw[1, 2:12, 3:15, 1:14] = rng.integers(0, 256, (10, 12, 13)).astype(np.float32)
+    plans = {
+        "transpose_forward": [0, 1, 2], "transpose_backward": [0, 1, 2],
+        "configurations": {"3d_fullres": {
+            "spacing": [1.0, 1.0, 1.0],
+            "normalization_schemes": ["RescaleTo01Normalization", "RGBTo01Normalization"],
+            "use_mask_for_norm": [False, False], "patch_size": [16, 16, 16],
+            "resampling_fn_data": "resample_data_or_seg_to_shape",
+            "resampling_fn_data_kwargs": {"is_seg": False, "order": 3, "order_z": 0,
+                                          "force_separate_z": None}}},
+    }
+    plan = PreprocessPlan.from_plans(plans, "3d_fullres")
+    out = preprocess_raw_case(raw, {"spacing": [1.0, 1.0, 1.0]}, plan)
+    bbox = op.nonzero_bbox(raw)
+    crop = raw[(slice(None), *(slice(a, b) for a, b in bbox))]
+    want = np.stack([op.rescale01_normalize(crop[0]), op.rgb01_normalize(crop[1])])
+    np.testing.assert_array_equal(out.data.cpu().numpy(), want)
+    bad = raw.copy()
+    bad[1, 5, 5, 5] = 300.0
+    with pytest.raises(ContractError, match="RGB"):
+        preprocess_raw_case(bad, {"spacing": [1.0, 1.0, 1.0]}, plan)

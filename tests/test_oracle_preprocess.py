@@ -152,3 +152,17 @@ def test_zscore_normalize_closed_form():
     np.testing.assert_array_equal(got[~mask], x[~mask])
     const = zscore_normalize(np.full((3, 3, 3), 7.0, dtype=np.float32))
     np.testing.assert_array_equal(const, np.zeros((3, 3, 3), dtype=np.float32))
+
+
+def test_rescale_and_rgb_closed_forms():
+    from oracle.preprocess import rescale01_normalize, rgb01_normalize
+
+    x = np.array([[[3.0, 7.0], [5.0, 11.0]]], dtype=np.float32)
+    np.testing.assert_allclose(rescale01_normalize(x), (x - 3.0) / 8.0, rtol=0, atol=1e-7)
+    assert rescale01_normalize(x).min() == 0.0 and rescale01_normalize(x).max() == 1.0
+    np.testing.assert_array_equal(rescale01_normalize(np.full((2, 2, 2), 4.0, np.float32)),
+                                  np.zeros((2, 2, 2), np.float32))
+    np.testing.assert_array_equal(rgb01_normalize(np.array([0.0, 255.0, 51.0], np.float32)),
+                                  np.array([0.0, 1.0, 0.2], np.float32))
+    with pytest.raises(ValueError):
+        rgb01_normalize(np.array([-1.0, 3.0], np.float32))
