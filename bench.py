@@ -349,6 +349,125 @@ def cpu_baseline(spec, weights) -> dict:
     }
 
 
+def ensemble_volume(name: str, seed: int = 7):
+    """Synthetic volumes of the multi-channel configurations: BraTS (4 x 155 x 240 x 240,
+    N(0, 1) inside a random ellipsoid brain mask, 0 outside) and AutoPET (2 x 284 x 400 x 400:
+    z-scored CT with ellipsoid regions; PET log-normal(0, 1) clipped to [0, 30] with 0.1 % of
+    voxels at SUV 5-20)."""
+    import numpy as np
+
+    rng = np.random.default_rng(seed)
+    if name == "brats-sw":
+        c, shape = 4, (155, 240, 240)
+        zz, yy, xx = np.ogrid[:shape[0], :shape[1], :shape[2]]
+        vol = np.zeros((c, *shape), dtype=np.float32)
+        for ch in range(c):
+            cz, cy, cx = (s / 2 + rng.uniform(-8, 8) for s in shape)
+            az, ay, ax = rng.uniform(55, 70), rng.uniform(80, 100), rng.uniform(65, 85)
+            brain = ((zz - cz) / az) ** 2 + ((yy - cy) / ay) ** 2 + ((xx - cx) / ax) ** 2 <= 1
+            vol[ch][brain] = rng.standard_normal(int(brain.sum()), dtype=np.float32)
+        return vol
+    shape = (284, 400, 400)
+    ct = rng.standard_normal(shape, dtype=np.float32)
+    zz, yy, xx = np.ogrid[:shape[0], :shape[1], :shape[2]]
+    for _ in range(12):
+        cz, cy, cx = (rng.uniform(0, s) for s in shape)
+        az, ay, ax = rng.uniform(10, 60), rng.uniform(20, 100), rng.uniform(20, 100)
+        inside = ((zz - cz) / az) ** 2 + ((yy - cy) / ay) ** 2 + ((xx - cx) / ax) ** 2 <= 1
+        ct[inside] += np.float32(rng.uniform(-1.0, 1.5))
+    pet = np.clip(rng.lognormal(0.0, 1.0, shape).astype(np.float32), 0, 30)
+    hot = rng.random(shape) < 1e-3
+    pet[hot] = rng.uniform(5, 20, int(hot.sum())).astype(np.float32)
+    return np.stack([ct, pet])
+
+
+def ensemble_workload(args) -> int:
+    """The multi-fold and bf16 configurations as whole cases resident in HBM: BraTS (5 folds,
+    4 -> 5 classes, 8x mirroring), AutoPET (5 folds, 2 -> 2 classes, patch 112 x 160 x 128,
+    8x mirroring) and pancreas (ResEnc-L, bf16, patch 128 x 160 x 160, no mirroring); labels of
+    the fold-averaged logits.  value = volume voxels per second."""
+    import numpy as np
+    import torch
+
+    from nnunet_mlx import _native
+    from nnunet_mlx.model.network import build_network
+    from nnunet_mlx.model.topology import PlainConvUNetSpec, ResidualEncoderUNetSpec
+    from nnunet_mlx.prediction import sliding_window as sw
+    from nnunet_mlx.storage.synthetic import random_weights
+
+    torch.cuda.set_device(0)
+    k3 = ((3, 3, 3),)
+    if args.workload == "brats-sw":
+        spec = PlainConvUNetSpec(4, 5, (32, 64, 128, 256, 320, 320), k3 * 6,
+                                 ((1, 1, 1),) + ((2, 2, 2),) * 5, (2,) * 6, (2,) * 5)
+        patch, seeds, axes, precision = (128, 128, 128), range(5), (0, 1, 2), args.precision
+        volume = ensemble_volume("brats-sw")
+    elif args.workload == "autopet-sw":
+        spec = PlainConvUNetSpec(2, 2, (32, 64, 128, 256, 320, 320), k3 * 6,
+                                 ((1, 1, 1),) + ((2, 2, 2),) * 4 + ((1, 2, 2),), (2,) * 6, (2,) * 5)
+        patch, seeds, axes, precision = (112, 160, 128), range(5), (0, 1, 2), args.precision
+        volume = ensemble_volume("autopet-sw")
+    else:
+        spec = ResidualEncoderUNetSpec(1, 3, (32, 64, 128, 256, 320, 320, 320), k3 * 7,
+                                       ((1, 1, 1),) + ((2, 2, 2),) * 5 + ((2, 1, 1),),
+                                       (1, 3, 4, 6, 6, 6, 6), (1,) * 6)
+        patch, seeds, axes, precision = (128, 160, 160), (4,), (), "bf16"
+        volume = synthetic_ct()
+    nets = []
+    for seed in seeds:
+        net = build_network(spec, precision=precision)
+        net.load_weights(random_weights(spec, seed=seed))
+        if nets:
+            net.share_workspace(nets[0])
+        nets.append(net)
+    d_volume = torch.from_numpy(volume).cuda()
+    kwargs = dict(patch_size=patch, num_outputs=spec.num_classes, mirroring_axes=axes,
+                  step_fraction=0.5, accumulation="float32", tiles_per_batch=args.tiles_per_batch)
+    for i in range(max(args.warmup, 1)):
+        print(f"[bench] {args.workload} warmup {i + 1}", file=sys.stderr, flush=True)
+        sw.average_fold_labels(nets, d_volume, return_device=True, **kwargs)
+    torch.cuda.synchronize()
+    with _native.KernelProfile() as prof:
+        t0 = time.perf_counter()
+        for i in range(args.steps):
+            print(f"[bench] {args.workload} step {i + 1}/{args.steps}", file=sys.stderr, flush=True)
+            labels = sw.average_fold_labels(nets, d_volume, return_device=True, **kwargs)
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / args.steps
+    kernels = {}
+    for name, c in sorted(prof.classes.items(), key=lambda kv: -kv[1]["ms"]):
+        entry = {"launches": c["launches"] // args.steps, "ms": round(c["ms"] / args.steps, 3)}
+        if c["flops"]:
+            entry["tflops"] = round(c["flops"] / (c["ms"] * 1e-3) / 1e12, 2)
+        elif c["bytes"]:
+            entry["gbs"] = round(c["bytes"] / (c["ms"] * 1e-3) / 1e9, 1)
+        kernels[name] = entry
+    steps = [len(s) for s in sw.compute_steps([max(a, b) for a, b in zip(volume.shape[1:], patch)],
+                                              patch, step_fraction=0.5)]
+    tiles = int(np.prod(steps))
+    voxels = int(np.prod(volume.shape[1:]))
+    line = {
+        "metric": f"sliding-window voxels/s, {args.workload} configuration",
+        "value": round(voxels / step_s, 1), "unit": "voxels/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": max(args.warmup, 1), "ms_per_step": round(step_s * 1e3, 1),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "bf16 products, f32 accumulate" if precision == "bf16" else
+                 "f32 (fp16-split products, f32 accumulate)",
+        "data": "synthetic",
+        "config": {"workload": f"{args.workload}: volume {list(volume.shape)} fp32 resident in HBM, "
+                               f"{len(nets)} fold(s), patch {list(patch)}, step 0.5, "
+                               f"mirror axes {list(axes)}, {tiles} tiles, "
+                               f"{tiles * len(nets) * 2 ** len(axes)} forwards",
+                   "label_counts": torch.bincount(labels.reshape(-1).to(torch.int64),
+                                                  minlength=spec.num_classes).tolist()},
+        "kernels": kernels, "roofline": None, "cpu_baseline": None,
+    }
+    for net in nets:
+        net.close()
+    print(json.dumps(line), flush=True)
+    return 0
+
+
 def raw_case_workload(args) -> int:
     """Raw liver CT resident in HBM -> uint16 labels on the raw grid on the host: GPU
     preprocessing, the 8x-mirrored sliding window with float16 accumulation (what the
@@ -437,11 +556,14 @@ def main() -> int:
                         help="skip the one-step measurement of the other precision")
     parser.add_argument("--shape", type=int, nargs=3, default=VOLUME_SHAPE[1:],
                         help="volume size (Z Y X); the default is the liver case")
-    parser.add_argument("--workload", choices=("liver-sw", "preprocess-ct", "liver-raw-case"),
+    parser.add_argument("--workload", choices=("liver-sw", "preprocess-ct", "liver-raw-case",
+                                               "brats-sw", "autopet-sw", "pancreas-sw"),
                         default="liver-sw",
                         help="liver-sw: the sliding-window case (default); preprocess-ct: raw "
                              "CT preprocessing on the GPU; liver-raw-case: raw CT to labels on "
-                             "the raw grid (preprocessing, sliding window, restoration)")
+                             "the raw grid (preprocessing, sliding window, restoration); "
+                             "brats-sw / autopet-sw / pancreas-sw: the multi-fold and bf16 "
+                             "configurations")
     args = parser.parse_args()
     if args.summarize_profiles:
         summarize_profiles(args.summarize_profiles)
@@ -455,6 +577,8 @@ def main() -> int:
         return preprocess_workload(args)
     if args.workload == "liver-raw-case":
         return raw_case_workload(args)
+    if args.workload in ("brats-sw", "autopet-sw", "pancreas-sw"):
+        return ensemble_workload(args)
 
     import numpy as np
     import torch

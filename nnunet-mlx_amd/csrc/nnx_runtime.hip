@@ -383,6 +383,11 @@ struct Planner {
   Workspace* ws = nullptr;
   float* take(size_t floats) {
     if (planning) {
+      // kernels address an activation with 32-bit element offsets inside a batch item and
+      // have been validated up to 2^31 elements per buffer
+      require(floats <= ((size_t)1 << 31),
+              "a network activation of this batch exceeds 2^31 elements; forward fewer views "
+              "or tiles per batch");
       sizes.push_back(floats * sizeof(float));
       return nullptr;
     }

@@ -151,11 +151,32 @@ def _device_volume(data, device: torch.device) -> torch.Tensor:
     return volume
 
 
+# Largest activation a forward batch may create (elements); the library rejects more.
+ACTIVATION_ELEMENT_LIMIT = 1 << 31
+
+
+def _activation_elements_per_view(models, patch) -> int:
+    """Largest activation (elements) one view of ``patch`` creates in any of the networks:
+    the full-resolution stage or a deeper stage (stride-2 sizes round up)."""
+    worst = 0
+    for model in models:
+        spec = getattr(model, "spec", None)
+        if spec is None:
+            continue
+        size = [int(v) for v in patch]
+        first = max(spec.features[0], getattr(spec, "stem_channels", None) or 0)
+        worst = max(worst, int(np.prod(size)) * first)
+        for features, stride in zip(spec.features, spec.strides):
+            size = [-(-n // int(st)) for n, st in zip(size, stride)]
+            worst = max(worst, int(np.prod(size)) * int(features))
+    return worst
+
+
 class _Request:
     """Everything the HIP pipeline needs for one volume, kept alive across the call."""
 
     def __init__(self, data, *, patch_size, num_classes, mirroring_axes, step_fraction,
-                 accumulation, device, tiles_per_batch):
+                 accumulation, device, tiles_per_batch, models=()):
         self.patch, self.axes = _validate_request(
             data, patch_size, num_classes, mirroring_axes, accumulation)
         self.accumulation = accumulation
@@ -172,8 +193,12 @@ class _Request:
         self.gaussian = torch.from_numpy(np.array(gaussian, copy=True)).to(device)
         self.device = device
         if tiles_per_batch is None:
-            # about 32 views per forward: enough workgroups for the 8^3 and 4^3 stages
+            # about 32 views per forward: enough workgroups for the 8^3 and 4^3 stages,
+            # within the library's activation size limit
             tiles_per_batch = max(1, 32 // len(self.flips))
+            per_tile = _activation_elements_per_view(models, self.patch) * len(self.flips)
+            while tiles_per_batch > 1 and tiles_per_batch * per_tile > ACTIVATION_ELEMENT_LIMIT:
+                tiles_per_batch -= 1
         self.tiles_per_batch = int(tiles_per_batch)
         self._offsets_c = _native.ints([v for o in self.offsets for v in o])
         self._flips_c = _native.ints(self.flips)
@@ -303,7 +328,7 @@ def average_fold_device_logits(
     request = _Request(
         data_channels_first, patch_size=patch_size, num_classes=num_outputs,
         mirroring_axes=mirroring_axes, step_fraction=step_fraction, accumulation=accumulation,
-        device=_device(models), tiles_per_batch=tiles_per_batch,
+        device=_device(models), tiles_per_batch=tiles_per_batch, models=tuple(models),
     )
     logits, _ = _run(tuple(models), request, want_logits=True, want_labels=False)
     return logits
@@ -359,7 +384,7 @@ def average_fold_labels(
     request = _Request(
         data_channels_first, patch_size=patch_size, num_classes=num_outputs,
         mirroring_axes=mirroring_axes, step_fraction=step_fraction, accumulation=accumulation,
-        device=_device(models), tiles_per_batch=tiles_per_batch,
+        device=_device(models), tiles_per_batch=tiles_per_batch, models=tuple(models),
     )
     _, labels = _run(tuple(models), request, want_logits=False, want_labels=True)
     if return_device:

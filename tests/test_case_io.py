@@ -180,3 +180,29 @@ def test_cli_argument_errors(tmp_path, capsys):
     assert main(["predict", "-i", str(tmp_path), "-o", str(tmp_path / "o"), "-m", str(tmp_path),
                  "-f", "x"]) == 2
     assert "invalid fold" in capsys.readouterr().err
+
+
+def test_default_batch_respects_the_activation_limit():
+    """Largest activation per view from the spec, and the default tiles per batch capped so
+    a forward batch stays within 2^31 elements (liver: 4 tiles x 8 views = exactly 2^31)."""
+    from types import SimpleNamespace
+
+    from nnunet_mlx.model.topology import PlainConvUNetSpec, ResidualEncoderUNetSpec
+    from nnunet_mlx.prediction.sliding_window import (ACTIVATION_ELEMENT_LIMIT,
+                                                       _activation_elements_per_view)
+
+    k3 = ((3, 3, 3),)
+    liver = PlainConvUNetSpec(1, 3, (32, 64, 128, 256, 320, 320), k3 * 6,
+                              ((1, 1, 1),) + ((2, 2, 2),) * 5, (2,) * 6, (2,) * 5)
+    resenc = ResidualEncoderUNetSpec(1, 3, (32, 64, 128, 256, 320, 320, 320), k3 * 7,
+                                     ((1, 1, 1),) + ((2, 2, 2),) * 5 + ((2, 1, 1),),
+                                     (1, 3, 4, 6, 6, 6, 6), (1,) * 6)
+    per = _activation_elements_per_view([SimpleNamespace(spec=liver)], (128, 128, 128))
+    assert per == 128 ** 3 * 32 and 4 * 8 * per == ACTIVATION_ELEMENT_LIMIT
+    per = _activation_elements_per_view([SimpleNamespace(spec=resenc)], (128, 160, 160))
+    assert per == 128 * 160 * 160 * 32
+    tiles = 32
+    while tiles > 1 and tiles * per > ACTIVATION_ELEMENT_LIMIT:
+        tiles -= 1
+    assert tiles == 20
+    assert _activation_elements_per_view([object()], (8, 8, 8)) == 0
