@@ -120,3 +120,18 @@ def test_forward_rejects_bad_input(device):
     with pytest.raises(ContractError):
         # odd sizes: the stride-2 conv rounds up, the shortcut's average pool rounds down
         res(torch.zeros((1, 9, 8, 8, 1), device=device))
+
+
+def test_forward_rejects_batches_beyond_the_activation_limit(device):
+    """A batch whose full-resolution activation exceeds 2^31 elements is refused while the
+    workspace is planned, before any kernel runs."""
+    from nnunet_mlx.errors import ContractError
+
+    spec = liver_spec()
+    net = build_network(spec)
+    net.load_weights(random_weights(spec, seed=0))
+    x = torch.zeros((33, 128, 128, 128, 1), device=device)   # 33 * 128^3 * 32 > 2^31
+    print("activation-limit case: batch 33 of 128^3", flush=True)
+    with pytest.raises(ContractError, match="2\\^31"):
+        net(x)
+    net.close()
