@@ -1450,7 +1450,7 @@ __device__ __forceinline__ float split_scale_of(float max_abs) {
 // holds 4 consecutive channels of one voxel, stored as one 16-byte word; the tile's
 // InstanceNorm partials reduce the accumulators across lanes and waves (mean, then the
 // centred M2), so the outputs never pass through LDS.
-template <int COUT>
+template <int COUT, int CIN>
 __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __restrict__ x,
                                                              const float* __restrict__ w,
                                                              float wscale,
@@ -1464,7 +1464,8 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
   constexpr int MB = 4;
   constexpr int TZ = kDirX3Tz, TY = kDirX3Ty, TX = kDirX3Tx;
   constexpr int HY = TY + 2, HX = TX + 2;
-  constexpr int kHalo = (TZ + 2) * HY * HX;
+  constexpr int kHalo = (TZ + 2) * HY * HX * CIN;  // voxel-major, CIN channels a voxel
+  constexpr int K = 27 * CIN, KS = (K + 31) / 32;    // taps x channels, 32 per MFMA step
   constexpr int kLoads = (kHalo + 255) / 256;
   __shared__ float halo[kHalo];
   __shared__ float red[4][NB * 16];
@@ -1475,22 +1476,25 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
   const int64_t item = (int64_t)blockIdx.y * D * H * W;
   const bool has_bias = bias != nullptr;
 
-  // A fragments: lane (n = 16 nb + row, k = 8 slot + q) holds wscale * W[n][k] split; bias
-  // of the lane's 4 output channels 16 nb + 4 slot + r
-  h8 A[NB][2];
+  // A fragments: lane (n = 16 nb + row, k = 32 s + 8 slot + q) holds wscale * W[n][k] split,
+  // k = tap * CIN + channel (the (C_out, kD, kH, kW, C_in) layout); bias of the lane's 4
+  // output channels 16 nb + 4 slot + r
+  h8 A[NB][KS][2];
   f4 bn[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int n = nb * 16 + row;
 #pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int k = slot * 8 + q;
-      const float v = (n < cout && k < 27) ? w[n * 27 + k] * wscale : 0.f;
-      _Float16 hh, ll;
-      to_operand<kSplit3>(v, hh, ll);
-      A[nb][0][q] = hh;
-      A[nb][1][q] = ll;
-    }
+    for (int st = 0; st < KS; ++st)
+#pragma unroll
+      for (int q = 0; q < 8; ++q) {
+        const int k = st * 32 + slot * 8 + q;
+        const float v = (n < cout && k < K) ? w[n * K + k] * wscale : 0.f;
+        _Float16 hh, ll;
+        to_operand<kSplit3>(v, hh, ll);
+        A[nb][st][0][q] = hh;
+        A[nb][st][1][q] = ll;
+      }
     const int n0 = nb * 16 + slot * 4;
     bn[nb] = f4{0.f, 0.f, 0.f, 0.f};
     if (has_bias && n0 < cout) bn[nb] = f4{bias[n0], bias[n0 + 1], bias[n0 + 2], bias[n0 + 3]};
@@ -1508,11 +1512,12 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
 #pragma unroll
     for (int j = 0; j < kLoads; ++j) {
       const int i = tid + 256 * j;
-      const int hz = i / (HY * HX), hy = (i / HX) % HY, hx = i % HX;
+      const int hvox = i / CIN, hc = i - hvox * CIN;
+      const int hz = hvox / (HY * HX), hy = (hvox / HX) % HY, hx = hvox % HX;
       const int z = z0 + hz - 1, yy = y0 + hy - 1, xx = x0 + hx - 1;
       const bool inside = i < kHalo && (unsigned)z < (unsigned)D && (unsigned)yy < (unsigned)H &&
                           (unsigned)xx < (unsigned)W;
-      hv[j] = inside ? x[item + ((int64_t)z * H + yy) * W + xx] : 0.f;
+      hv[j] = inside ? x[(item + ((int64_t)z * H + yy) * W + xx) * CIN + hc] : 0.f;
     }
   };
   if (t_begin < t_end) load_halo(t_begin);
@@ -1549,22 +1554,26 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
       // B fragment: lane (voxel v = 64 wave + 16 mb + row, taps 8 slot + q)
       const int v = wave * 64 + mb * 16 + row;
       const int base = ((v / (TX * TY)) * HY + (v / TX) % TY) * HX + v % TX;
-      h8 B[2];
 #pragma unroll
-      for (int q = 0; q < 8; ++q) {
-        const int k = slot * 8 + q;
-        const int off = k < 27 ? ((k / 9) * HY + (k / 3) % 3) * HX + k % 3 : 0;
-        const float hvq = k < 27 ? halo[base + off] * xscale : 0.f;
-        _Float16 hh, ll;
-        to_operand<kSplit3>(hvq, hh, ll);
-        B[0][q] = hh;
-        B[1][q] = ll;
-      }
+      for (int st = 0; st < KS; ++st) {
+        h8 B[2];
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) {
-        acc[mb][nb] = mfma16x16x32h(A[nb][0], B[0], acc[mb][nb]);
-        acc[mb][nb] = mfma16x16x32h(A[nb][0], B[1], acc[mb][nb]);
-        acc[mb][nb] = mfma16x16x32h(A[nb][1], B[0], acc[mb][nb]);
+        for (int q = 0; q < 8; ++q) {
+          const int k = st * 32 + slot * 8 + q;
+          const int tap = k / CIN, hc = k - tap * CIN;
+          const int off = k < K ? ((tap / 9) * HY + (tap / 3) % 3) * HX + tap % 3 : 0;
+          const float hvq = k < K ? halo[(base + off) * CIN + hc] * xscale : 0.f;
+          _Float16 hh, ll;
+          to_operand<kSplit3>(hvq, hh, ll);
+          B[0][q] = hh;
+          B[1][q] = ll;
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) {
+          acc[mb][nb] = mfma16x16x32h(A[nb][st][0], B[0], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(A[nb][st][0], B[1], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(A[nb][st][1], B[0], acc[mb][nb]);
+        }
       }
     }
 
@@ -2495,8 +2504,11 @@ int conv_direct_stats_tiles(const int* size, bool split) {
 }
 
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
-                        const int* size, int cout, hipStream_t st, float4* stats, float wscale) {
+                        const int* size, int cout, hipStream_t st, float4* stats, float wscale,
+                        int cin) {
   require(x && w && y, "convolution pointers must not be null");
+  require(cin == 1 || (wscale > 0.f && (cin == 2 || cin == 4)),
+          "the direct convolution takes 1 input channel, or 2 or 4 with split products");
   require(cout >= 4 && cout <= 64 && cout % 4 == 0,
           "one-channel direct convolution supports 4..64 outputs in steps of 4");
   require(batch >= 1 && batch <= 65535, "invalid convolution batch");
@@ -2512,7 +2524,7 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
   require(tiles < (1LL << 31), "convolution volume too large");
   const dim3 grid((unsigned)tiles, (unsigned)batch);
   const size_t lds = (size_t)256 * (cout + 1) * sizeof(float);
-  const double bytes = 4.0 * (double)nvox * (1 + cout);
+  const double bytes = 4.0 * (double)nvox * (cin + cout);
   if (split) {
     // split products on MFMA: the output write bounds it (reported against HBM).  Each
     // block takes kDirX3TilesPerBlock consecutive tiles (weights split once per block).
@@ -2522,9 +2534,18 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
     switch (cout / 4) {
 #define NNX_DIRECT_X3_CASE(Q)                                                                  \
   case Q:                                                                                      \
-    hipLaunchKernelGGL(direct_cin1_x3_kernel<4 * Q>, grid_x3, dim3(256), 0, st, x, w, wscale,  \
-                       bias, y, size[0], size[1], size[2], tiles_y, tiles_x, (int)tiles, tpb,  \
-                       stats);                                                                 \
+    if (cin == 1)                                                                              \
+      hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 1>), grid_x3, dim3(256), 0, st, x, w,    \
+                         wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
+                         (int)tiles, tpb, stats);                                               \
+    else if (cin == 2)                                                                         \
+      hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 2>), grid_x3, dim3(256), 0, st, x, w,    \
+                         wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
+                         (int)tiles, tpb, stats);                                               \
+    else                                                                                       \
+      hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 4>), grid_x3, dim3(256), 0, st, x, w,    \
+                         wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
+                         (int)tiles, tpb, stats);                                               \
     break;
       NNX_DIRECT_X3_CASE(1) NNX_DIRECT_X3_CASE(2) NNX_DIRECT_X3_CASE(3) NNX_DIRECT_X3_CASE(4)
       NNX_DIRECT_X3_CASE(5) NNX_DIRECT_X3_CASE(6) NNX_DIRECT_X3_CASE(7) NNX_DIRECT_X3_CASE(8)

@@ -153,10 +153,11 @@ int conv_x3_stats_tiles(const ConvGeom& g, int cout);
 bool conv_x3_supported(const int* ksize, const int* stride, int cout);
 // With `stats`: per-block InstanceNorm partials, conv_direct_stats_tiles(size) per item.
 // wscale 0: float32 fma products; wscale > 0 (split_weight_scale of max |w|): split-fp16
-// products on MFMA, each tile's input scaled by a power of two from its own max |x|.
+// products on MFMA, each tile's input scaled by a power of two from its own max |x|; with
+// split products the input may have 1, 2 or 4 channels (NDHWC, weights (C_out, 3, 3, 3, cin)).
 void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float* y, int batch,
                         const int* size, int cout, hipStream_t st, float4* stats = nullptr,
-                        float wscale = 0.f);
+                        float wscale = 0.f, int cin = 1);
 int conv_direct_stats_tiles(const int* size, bool split = false);
 
 int64_t tconv_packed_floats(int cout, const int* ksize, int cin);

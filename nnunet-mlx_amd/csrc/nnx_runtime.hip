@@ -144,6 +144,7 @@ struct ConvNorm {
   bool act = true;
   int pw = -1, pb = -1, pg = -1, pbeta = -1;
   bool direct = false;
+  bool direct_multi = false;  // 2 input channels: direct with split products if first
   bool first = false;   // reads the network input (kept in exact float32 products)
   bool split = false;   // packed for the split-fp16 kernel
   float scale = 1.f;    // power-of-two weight scale of the split packing
@@ -238,8 +239,14 @@ void declare_convnorm(nnx_model* m, ConvNorm& c, const std::string& prefix, int 
     c.pg = add_param(m, prefix + ".norm.weight", {cout});
     c.pbeta = add_param(m, prefix + ".norm.bias", {cout});
   }
-  c.direct = cin1 == 1 && cin2 == 0 && k[0] == 3 && k[1] == 3 && k[2] == 3 && s[0] == 1 &&
-             s[1] == 1 && s[2] == 1 && cout % 4 == 0 && cout <= 64;
+  const bool shape_ok = cin2 == 0 && k[0] == 3 && k[1] == 3 && k[2] == 3 && s[0] == 1 &&
+                        s[1] == 1 && s[2] == 1 && cout % 4 == 0 && cout <= 64;
+  c.direct = cin1 == 1 && shape_ok;
+  // 2 input channels: the direct kernel with split products, for the network's first
+  // convolution only (decided when packing, once the first convolution is known).  With 4
+  // channels its four MFMA steps per voxel tile made it slower than the float32-product
+  // implicit GEMM (247 against 230 ms per 4 x 155 x 240 x 240 five-fold case).
+  c.direct_multi = cin1 == 2 && shape_ok;
 }
 
 const int kUnit[3] = {1, 1, 1};
@@ -341,6 +348,7 @@ bool uses_split_kernels(const nnx_model* m) {
 }
 
 void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
+  if (c.first && c.direct_multi && m->precision == NNX_PRECISION_FP32_SPLIT) c.direct = true;
   if (c.direct) {
     // the direct kernel reads the reference layout; split products in the fp32-split
     // precision (the bf16 precision keeps float32 products for the first convolution)
@@ -434,7 +442,7 @@ struct Runner {
       }
       float4* stats = plan->ws->stats.as<float4>();
       conv3d_direct_cin1(x1.data, pdev(m, c.pw), pdev(m, c.pb), out, n, in.d, c.cout, st, stats,
-                         c.split ? c.scale : 0.f);
+                         c.split ? c.scale : 0.f, c.cin1);
       instnorm_merge_partials(stats, tiles, n, vox, c.cout, pdev(m, c.pg), pdev(m, c.pbeta),
                               m->eps, params, st);
       if (!defer)
