@@ -181,7 +181,9 @@ __global__ __launch_bounds__(256) void norm_merge_kernel(const float2* __restric
 
 // Same merge for partials that carry their own counts (per-tile partials written by the
 // convolution epilogue: (mean, M2, n, 0) at partial[(b * nparts + i) * C + c]), in two passes.
-// Pass 1: block (j, b) merges rows [j * per, (j + 1) * per) of item b; a thread takes
+// Pass 1: block (j, b) merges rows [j * per, (j + 1) * per) of item b, the last block
+// (j = gridDim.x - 1) every row from (gridDim.x - 1) * per to nparts, so with per >= 2 every
+// slice has at least two rows to hold its result; a thread takes
 // channel cb + t % CB of every G-th row (CB = min(C, 256) channels a pass, G = 256 / CB
 // row groups), so each row is read as one contiguous run; the groups are merged through
 // LDS, and the slice's (mean, M2) in float64 and its count are written over the slice's
@@ -195,7 +197,7 @@ __global__ __launch_bounds__(256) void norm_merge_slices_kernel(float4* __restri
   const int G = 256 / CB;
   const int g = t / CB;
   const int r0 = j * per;
-  const int r1 = r0 + per < nparts ? r0 + per : nparts;
+  const int r1 = j + 1 == (int)gridDim.x ? nparts : r0 + per;
   float4* rows = partial + (int64_t)b * nparts * C;
   // (mean, M2) as a double pair and the count, per channel of this pass
   double res_m[2], res_2[2];
@@ -513,11 +515,10 @@ void instnorm_merge_partials(float4* partials, int nparts, int batch, int64_t sp
     launch_check("instnorm merge partials");
     return;
   }
-  // slices of >= 2 rows (a slice's result takes its first two rows), ~2048 blocks in all
-  int nslices = (int)std::min<int64_t>(ceil_div(2048, batch), nparts / 2);
-  if (nslices < 1) nslices = 1;
-  const int per = (int)ceil_div(nparts, nslices);
-  nslices = (int)ceil_div(nparts, per);
+  // ~2048 blocks in all; slices of per = floor(nparts / nslices) >= 2 rows (a slice's result
+  // takes its first two rows), the last slice also taking the remainder
+  const int nslices = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(2048, batch), nparts / 2));
+  const int per = nparts / nslices;
   hipLaunchKernelGGL(norm_merge_slices_kernel, dim3(nslices, batch), dim3(256), 0, st, partials,
                      channels, nparts, per);
   launch_check("instnorm merge slices");

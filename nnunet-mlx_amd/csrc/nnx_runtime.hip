@@ -4,6 +4,7 @@
 // every extern "C" entry point of include/nnx.h.
 #include <algorithm>
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -357,8 +358,11 @@ void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
     return;
   }
   // Split-fp16 (or bf16) products for the hidden convolutions with >= 8 taps (a tap group
-  // holds 4 taps; 1x1x1 convolutions would waste 3/4 of it).  The first convolution reads
-  // the raw network input, whose range is not normalised, so it keeps float32 products.
+  // holds 4 taps; 1x1x1 convolutions would waste 3/4 of it).  A first convolution that
+  // reaches this point (more than 2 input channels, or any first convolution in bf16) reads
+  // the raw network input, whose range is not normalised, so it keeps float32 products;
+  // first convolutions with 1 or 2 input channels took the direct kernel above (split
+  // products with a per-tile input scale in the fp32-split precision).
   const int taps = c.k[0] * c.k[1] * c.k[2];
   c.split = uses_split_kernels(m) && !c.first && taps >= 8 && conv_x3_supported(c.k, c.s, c.cout);
   if (c.split) {
@@ -382,6 +386,32 @@ Shape3 conv_out(const Shape3& in, const ConvNorm& c) {
   return o;
 }
 
+// Layer checks (NNX_CHECK_LAYERS=1 in the environment): after every convolution, transposed
+// convolution and head the stream is synchronised and the layer's output is scanned for
+// non-finite values; the first such layer fails the forward with its parameter name and the
+// batch geometry.  A diagnostic for wrong results; off by default (it serialises the forward).
+bool layer_checks_enabled() {
+  static const bool on = [] {
+    const char* v = std::getenv("NNX_CHECK_LAYERS");
+    return v != nullptr && v[0] == '1';
+  }();
+  return on;
+}
+
+void check_layer(const std::string& name, const float* buf, int64_t n, int batch, hipStream_t st) {
+  static DevBuf* counter = new DevBuf();  // lives until process exit
+  counter->ensure(sizeof(unsigned int));
+  count_nonfinite(buf, n, counter->as<unsigned int>(), st);
+  unsigned int bad = 0;
+  hip_check(hipMemcpyAsync(&bad, counter->ptr, sizeof(bad), hipMemcpyDeviceToHost, st),
+            "layer check copy");
+  hip_check(hipStreamSynchronize(st), "layer check synchronize");
+  if (bad)
+    fail(NNX_ERR_NONFINITE, "layer check: " + std::to_string(bad) + " non-finite values of " +
+                                std::to_string(n) + " in the output of " + name + " (batch " +
+                                std::to_string(batch) + ")");
+}
+
 struct Planner {
   // During planning, records buffer sizes; during execution, hands out the same buffers.
   std::vector<size_t> sizes;
@@ -389,13 +419,13 @@ struct Planner {
   size_t next = 0;
   bool planning = true;
   Workspace* ws = nullptr;
+  int batch = 1;
   float* take(size_t floats) {
     if (planning) {
-      // kernels address an activation with 32-bit element offsets inside a batch item and
-      // have been validated up to 2^31 elements per buffer
-      require(floats <= ((size_t)1 << 31),
-              "a network activation of this batch exceeds 2^31 elements; forward fewer views "
-              "or tiles per batch");
+      // kernels address a batch item's voxels with 32-bit offsets (whole-batch offsets are
+      // 64-bit), so one item of an activation stays below 2^31 elements
+      require(floats / (size_t)batch < ((size_t)1 << 31),
+              "a network activation exceeds 2^31 elements per batch item; use a smaller patch");
       sizes.push_back(floats * sizeof(float));
       return nullptr;
     }
@@ -410,6 +440,7 @@ struct Act {
   const float* data = nullptr;
   PendingNorm norm;
 };
+
 
 struct Runner {
   nnx_model* m;
@@ -448,6 +479,8 @@ struct Runner {
       if (!defer)
         instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, act, m->slope, residual,
                               st);
+      if (layer_checks_enabled())
+        check_layer(m->params[c.pw].name, out, (int64_t)n * vox * c.cout, n, st);
       return result;
     }
     // Implicit GEMM: the epilogue writes per-tile statistics, so the norm never re-reads the
@@ -471,6 +504,8 @@ struct Runner {
     if (!defer)
       instnorm_apply_params(out, out, n, vox, c.cout, params, nullptr, act, m->slope, residual,
                             st);
+    if (layer_checks_enabled())
+      check_layer(m->params[c.pw].name, out, (int64_t)n * vox * c.cout, n, st);
     return result;
   }
 
@@ -503,6 +538,8 @@ struct Runner {
         else
           tconv3d_gemm(hidden.data, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d,
                        u.cout, u.k, st);
+        if (layer_checks_enabled())
+          check_layer(m->params[u.pw].name, upbuf, (int64_t)n * us.vox() * u.cout, n, st);
       }
       if (!(us == ss)) {
         // patch not divisible by the total stride: centre crop / zero pad the upsampled
@@ -525,9 +562,12 @@ struct Runner {
       hs = cur;
     }
     const SegHead& sh = m->seg[S - 2];
-    if (!plan->planning)
+    if (!plan->planning) {
       conv1x1(hidden.data, sh.cin, pdev(m, sh.pw), pdev(m, sh.pb), d_out, (int64_t)n * hs.vox(),
               sh.cout, st, hidden.norm, hs.vox());
+      if (layer_checks_enabled())
+        check_layer(m->params[sh.pw].name, d_out, (int64_t)n * hs.vox() * sh.cout, n, st);
+    }
   }
 
   void forward_plain(const float* x, const Shape3& in, float* d_out) {
@@ -575,7 +615,12 @@ struct Runner {
             rs.d[i] = cur.d[i] / rb.pool_k[i];
           }
           float* pooled = plan->take((size_t)n * rs.vox() * cin);
-          if (!plan->planning) avgpool3d(h.data, pooled, n, cur.d, cin, rb.pool_k, st);
+          if (!plan->planning) {
+            avgpool3d(h.data, pooled, n, cur.d, cin, rb.pool_k, st);
+            if (layer_checks_enabled())
+              check_layer(m->params[rb.convs[0].pw].name + " (shortcut pool)", pooled,
+                          (int64_t)n * rs.vox() * cin, n, st);
+          }
           residual = pooled;
         }
         if (rb.proj) {
@@ -620,6 +665,7 @@ void ensure_workspace(nnx_model* m, int n, const Shape3& in) {
   Workspace& ws = *m->ws;
   Planner plan;
   plan.planning = true;
+  plan.batch = n;
   Runner r{m, &plan, nullptr, n};
   r.forward(nullptr, in, nullptr);
   // grow every slot to the largest need seen so far (folds sharing one workspace may
@@ -1048,14 +1094,15 @@ int nnx_conv3d_direct_small_cin(const float* d_x, const float* d_weight, const f
   });
 }
 
-int nnx_conv3d_direct_small_cin_split(const float* d_x, const float* d_weight, float scale,
-                                      const float* d_bias, float* d_y, int batch, const int* size,
-                                      int cout, void* stream) {
+int nnx_conv3d_direct_small_cin_split(const float* d_x, int cin, const float* d_weight,
+                                      float scale, const float* d_bias, float* d_y, int batch,
+                                      const int* size, int cout, void* stream) {
   return guarded([&] {
     require(size != nullptr, "null argument");
+    require(cin == 1 || cin == 2, "the split direct convolution takes 1 or 2 input channels");
     require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
     conv3d_direct_cin1(d_x, d_weight, d_bias, d_y, batch, size, cout, as_stream(stream), nullptr,
-                       scale);
+                       scale, cin);
   });
 }
 

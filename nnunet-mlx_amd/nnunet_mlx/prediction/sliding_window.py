@@ -151,25 +151,46 @@ def _device_volume(data, device: torch.device) -> torch.Tensor:
     return volume
 
 
-# Largest activation a forward batch may create (elements); the library rejects more.
+# Default memory budget of one forward batch: its largest single activation (elements).
+# The network workspace keeps every activation of the batch resident (about 4 x the
+# largest one for a plain network, more for residual encoders), so 2^31 float32 elements
+# (8 GiB) keeps a default batch within a few tens of GB of HBM.  A memory budget only: the
+# library handles batches of any size whose items stay below 2^31 elements.
 ACTIVATION_ELEMENT_LIMIT = 1 << 31
+# Views per forward batch the default aims at: enough workgroups for the 8^3 and 4^3 stages.
+DEFAULT_VIEWS_PER_BATCH = 32
 
 
-def _activation_elements_per_view(models, patch) -> int:
-    """Largest activation (elements) one view of ``patch`` creates in any of the networks:
-    the full-resolution stage or a deeper stage (stride-2 sizes round up)."""
-    worst = 0
+def _activation_elements_per_view(models, patch, *, channels: int = 1, num_classes: int = 1) -> int:
+    """Largest tensor (elements) one view of ``patch`` creates in any of the networks: the
+    input tile, the logits, the full-resolution stage or a deeper stage (stride-2 sizes
+    round up)."""
+    voxels = int(np.prod([int(v) for v in patch]))
+    worst = voxels * max(int(channels), int(num_classes))
     for model in models:
         spec = getattr(model, "spec", None)
         if spec is None:
             continue
         size = [int(v) for v in patch]
         first = max(spec.features[0], getattr(spec, "stem_channels", None) or 0)
-        worst = max(worst, int(np.prod(size)) * first)
+        worst = max(worst, voxels * first)
         for features, stride in zip(spec.features, spec.strides):
             size = [-(-n // int(st)) for n, st in zip(size, stride)]
             worst = max(worst, int(np.prod(size)) * int(features))
     return worst
+
+
+def default_tiles_per_batch(models, patch, nviews: int, *, channels: int = 1,
+                            num_classes: int = 1) -> int:
+    """Tiles per forward batch when the caller does not choose: about
+    ``DEFAULT_VIEWS_PER_BATCH`` views, fewer while the batch's largest activation exceeds
+    ``ACTIVATION_ELEMENT_LIMIT``, at least one tile."""
+    tiles = max(1, DEFAULT_VIEWS_PER_BATCH // max(1, int(nviews)))
+    per_tile = _activation_elements_per_view(models, patch, channels=channels,
+                                             num_classes=num_classes) * max(1, int(nviews))
+    while tiles > 1 and tiles * per_tile > ACTIVATION_ELEMENT_LIMIT:
+        tiles -= 1
+    return tiles
 
 
 class _Request:
@@ -193,12 +214,9 @@ class _Request:
         self.gaussian = torch.from_numpy(np.array(gaussian, copy=True)).to(device)
         self.device = device
         if tiles_per_batch is None:
-            # about 32 views per forward: enough workgroups for the 8^3 and 4^3 stages,
-            # within the library's activation size limit
-            tiles_per_batch = max(1, 32 // len(self.flips))
-            per_tile = _activation_elements_per_view(models, self.patch) * len(self.flips)
-            while tiles_per_batch > 1 and tiles_per_batch * per_tile > ACTIVATION_ELEMENT_LIMIT:
-                tiles_per_batch -= 1
+            tiles_per_batch = default_tiles_per_batch(models, self.patch, len(self.flips),
+                                                      channels=self.channels,
+                                                      num_classes=self.num_classes)
         self.tiles_per_batch = int(tiles_per_batch)
         self._offsets_c = _native.ints([v for o in self.offsets for v in o])
         self._flips_c = _native.ints(self.flips)

@@ -183,13 +183,16 @@ def test_cli_argument_errors(tmp_path, capsys):
 
 
 def test_default_batch_respects_the_activation_limit():
-    """Largest activation per view from the spec, and the default tiles per batch capped so
-    a forward batch stays within 2^31 elements (liver: 4 tiles x 8 views = exactly 2^31)."""
+    """Largest activation per view from the spec (input channels and classes included), and
+    the default tiles per batch of the sliding window's own request: about 32 views, capped
+    so a forward batch's largest activation stays within 2^31 elements (liver: 4 tiles x 8
+    views = exactly 2^31; ResEnc-L 128x160x160 without mirroring: 20 tiles)."""
     from types import SimpleNamespace
 
+    import torch
+
     from nnunet_mlx.model.topology import PlainConvUNetSpec, ResidualEncoderUNetSpec
-    from nnunet_mlx.prediction.sliding_window import (ACTIVATION_ELEMENT_LIMIT,
-                                                       _activation_elements_per_view)
+    from nnunet_mlx.prediction import sliding_window as sw
 
     k3 = ((3, 3, 3),)
     liver = PlainConvUNetSpec(1, 3, (32, 64, 128, 256, 320, 320), k3 * 6,
@@ -197,12 +200,18 @@ def test_default_batch_respects_the_activation_limit():
     resenc = ResidualEncoderUNetSpec(1, 3, (32, 64, 128, 256, 320, 320, 320), k3 * 7,
                                      ((1, 1, 1),) + ((2, 2, 2),) * 5 + ((2, 1, 1),),
                                      (1, 3, 4, 6, 6, 6, 6), (1,) * 6)
-    per = _activation_elements_per_view([SimpleNamespace(spec=liver)], (128, 128, 128))
-    assert per == 128 ** 3 * 32 and 4 * 8 * per == ACTIVATION_ELEMENT_LIMIT
-    per = _activation_elements_per_view([SimpleNamespace(spec=resenc)], (128, 160, 160))
-    assert per == 128 * 160 * 160 * 32
-    tiles = 32
-    while tiles > 1 and tiles * per > ACTIVATION_ELEMENT_LIMIT:
-        tiles -= 1
-    assert tiles == 20
-    assert _activation_elements_per_view([object()], (8, 8, 8)) == 0
+    per = sw._activation_elements_per_view([SimpleNamespace(spec=liver)], (128, 128, 128))
+    assert per == 128 ** 3 * 32 and 4 * 8 * per == sw.ACTIVATION_ELEMENT_LIMIT
+    assert sw._activation_elements_per_view([object()], (8, 8, 8)) == 8 ** 3
+    # classes (or input channels) wider than the first stage set the per-view size
+    wide = sw._activation_elements_per_view([SimpleNamespace(spec=liver)], (8, 8, 8),
+                                            num_classes=40)
+    assert wide == 8 ** 3 * 40
+
+    # the helper the sliding-window request calls when tiles_per_batch is None
+    assert sw.default_tiles_per_batch([SimpleNamespace(spec=liver)], (128, 128, 128), 8) == 4
+    assert sw.default_tiles_per_batch([SimpleNamespace(spec=resenc)], (128, 160, 160), 1) == 20
+    assert sw.default_tiles_per_batch([SimpleNamespace(spec=liver)], (16, 16, 16), 1) == 32
+    assert sw.default_tiles_per_batch([SimpleNamespace(spec=liver)], (16, 16, 16), 8) == 4
+    # at least one tile, however large the patch
+    assert sw.default_tiles_per_batch([SimpleNamespace(spec=liver)], (512, 512, 512), 8) == 1

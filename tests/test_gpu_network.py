@@ -122,16 +122,18 @@ def test_forward_rejects_bad_input(device):
         res(torch.zeros((1, 9, 8, 8, 1), device=device))
 
 
-def test_forward_rejects_batches_beyond_the_activation_limit(device):
-    """A batch whose full-resolution activation exceeds 2^31 elements is refused while the
-    workspace is planned, before any kernel runs."""
+def test_forward_rejects_items_beyond_the_activation_limit(device):
+    """A batch item whose full-resolution activation exceeds 2^31 elements (the kernels'
+    per-item offsets are 32-bit) is refused while the workspace is planned, before any
+    allocation or kernel; a batch of many items beyond 2^31 elements in total is fine (the
+    real-shape workload tests run such batches)."""
     from nnunet_mlx.errors import ContractError
 
     spec = liver_spec()
     net = build_network(spec)
     net.load_weights(random_weights(spec, seed=0))
-    x = torch.zeros((33, 128, 128, 128, 1), device=device)   # 33 * 128^3 * 32 > 2^31
-    print("activation-limit case: batch 33 of 128^3", flush=True)
+    x = torch.zeros((1, 288, 512, 512, 1), device=device)   # 288 * 512^2 * 32 > 2^31
+    print("activation-limit case: one item of 288x512x512", flush=True)
     with pytest.raises(ContractError, match="2\\^31"):
         net(x)
     net.close()
