@@ -231,3 +231,100 @@ def test_bf16_oracle_rounding_points():
     emulated = net(xs)
     rel = np.linalg.norm(emulated - full) / np.linalg.norm(full)
     assert 1e-5 < rel < 3e-2
+
+
+def _pool64(h, stride):
+    """float64 average pooling with kernel = stride (sizes divisible), channels-last."""
+    n, d, hh, w, c = h.shape
+    a, b, e = stride
+    return h.reshape(n, d // a, a, hh // b, b, w // e, e, c).mean(axis=(2, 4, 6))
+
+
+def _leaky64(v, slope=0.01):
+    return np.maximum(slope * v, v)
+
+
+def _residual_reference(spec, w, x, variant=None):
+    """float64 composition of a ResidualEncoderUNet from brute-force pieces, written from
+    the block definitions (src/nnunet_mlx/model/network.py:467-602): the shortcut is the
+    input, average-pooled by the block's stride when it is not 1, then a bias-free 1x1
+    ConvNorm when the channel count changes; the branch is ConvNormAct(stride) then ConvNorm
+    (BasicBlockD) or 1x1 ConvNormAct, kxk ConvNormAct(stride), 1x1 ConvNorm (BottleneckD);
+    the block output is LeakyReLU(branch + shortcut).  ``variant`` builds a deliberately
+    wrong block ("act_before_add": LeakyReLU(LeakyReLU(branch) + shortcut);
+    "pool_after_projection": the projection at full resolution, then the pooling)."""
+
+    def cn(prefix, h, stride, act, bias=True):
+        y = brute_force_conv3d(h, w[f"{prefix}.conv.weight"], stride)
+        b = w[f"{prefix}.conv.bias"] if bias else np.zeros(y.shape[-1])
+        return _norm64(y, b, w[f"{prefix}.norm.weight"], w[f"{prefix}.norm.bias"],
+                       0.01 if act else None)
+
+    h = cn("stem", x.astype(np.float64), (1, 1, 1), True)
+    skips = []
+    for s in range(len(spec.features)):
+        for b in range(spec.encoder_blocks[s]):
+            stride = tuple(spec.strides[s]) if b == 0 else (1, 1, 1)
+            pre = f"res{s}.block{b}"
+            pool_first = variant != "pool_after_projection"
+            shortcut = h if stride == (1, 1, 1) or not pool_first else _pool64(h, stride)
+            if f"{pre}.proj.conv.weight" in w:
+                shortcut = cn(f"{pre}.proj", shortcut, (1, 1, 1), False, bias=False)
+            if stride != (1, 1, 1) and not pool_first:
+                shortcut = _pool64(shortcut, stride)
+            if spec.bottleneck_channels is None:
+                branch = cn(f"{pre}.conv2", cn(f"{pre}.conv1", h, stride, True), (1, 1, 1),
+                            variant == "act_before_add")
+            else:
+                t = cn(f"{pre}.conv1", h, (1, 1, 1), True)
+                t = cn(f"{pre}.conv2", t, stride, True)
+                branch = cn(f"{pre}.conv3", t, (1, 1, 1), variant == "act_before_add")
+            h = _leaky64(branch + shortcut)
+        skips.append(h)
+    h = skips.pop()
+    for d in range(len(spec.features) - 1):
+        skip = skips.pop()
+        up = brute_force_tconv3d(h, w[f"up{d}.weight"]) + w[f"up{d}.bias"]
+        h = np.concatenate([up, skip], axis=-1)
+        for j in range(spec.decoder_convs[d]):
+            h = cn(f"dec{d}.block{j}", h, (1, 1, 1), True)
+    last = len(spec.features) - 2
+    return (np.einsum("nzyxc,oc->nzyxo", h, w[f"seg{last}.weight"][:, 0, 0, 0, :].astype(np.float64))
+            + w[f"seg{last}.bias"])
+
+
+RESIDUAL_CASES = {
+    # BasicBlockD: stride-1 first stage with a stem of its own width (projection without
+    # pooling), strided stages with pooling + projection, two blocks in a stage
+    "basic": ResidualEncoderUNetSpec(2, 3, (4, 8, 8), ((3, 3, 3),) * 3,
+                                     ((1, 1, 1), (2, 2, 2), (1, 2, 2)), (1, 2, 1), (1, 2),
+                                     stem_channels=6),
+    # BottleneckD: 1x1 / kxk (stride) / 1x1 branch
+    "bottleneck": ResidualEncoderUNetSpec(1, 2, (4, 8), ((3, 3, 3),) * 2, ((1, 1, 1), (2, 2, 2)),
+                                          (2, 1), (1,), bottleneck_channels=(2, 3)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(RESIDUAL_CASES))
+def test_residual_network_composition_against_float64(name):
+    """Tiny ResidualEncoderUNets: the oracle's residual path vs the float64 composition."""
+    spec = RESIDUAL_CASES[name]
+    w = random_weights(spec, seed=7, random_affine=True)
+    x = np.random.default_rng(8).standard_normal((1, 8, 8, 8, spec.input_channels)).astype(np.float32)
+    got = OracleNetwork(spec, w, residual=True)(x)
+    ref = _residual_reference(spec, w, x)
+    np.testing.assert_allclose(got, ref, rtol=1e-4, atol=1e-4)
+
+
+def test_residual_composition_detects_misplaced_operations():
+    """The composition tells the block variants apart: with LeakyReLU applied to the branch
+    before the residual addition, or with the shortcut pooled after its projection, the
+    logits move far beyond the tolerance the oracle is held to above, so an oracle with
+    either mistake fails test_residual_network_composition_against_float64."""
+    spec = RESIDUAL_CASES["basic"]
+    w = random_weights(spec, seed=7, random_affine=True)
+    x = np.random.default_rng(8).standard_normal((1, 8, 8, 8, spec.input_channels)).astype(np.float32)
+    got = OracleNetwork(spec, w, residual=True)(x)
+    for variant in ("act_before_add", "pool_after_projection"):
+        wrong = _residual_reference(spec, w, x, variant=variant)
+        assert np.abs(wrong - got).max() > 50 * 1e-4, variant
