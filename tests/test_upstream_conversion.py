@@ -251,6 +251,131 @@ def test_converted_weights_compute_what_the_upstream_modules_compute():
     np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
 
 
+class _ConvNormOnly(torch.nn.Module):
+    """Upstream ConvDropoutNormReLU without its nonlinearity (conv, norm)."""
+
+    def __init__(self, cin, cout, kernel, stride, spec, bias):
+        super().__init__()
+        self.conv = torch.nn.Conv3d(cin, cout, kernel, stride, tuple(k // 2 for k in kernel),
+                                    bias=bias)
+        self.norm = torch.nn.InstanceNorm3d(cout, eps=spec.norm_eps, affine=spec.norm_affine)
+
+    def forward(self, x):
+        return self.norm(self.conv(x))
+
+
+class _UpstreamResidualBlock(torch.nn.Module):
+    """Upstream BasicBlockD / BottleneckD: the branch, and ``skip`` = Sequential(AvgPool of
+    the stride when it is not 1, bias-free 1x1 conv + norm when the channels change);
+    LeakyReLU after the sum."""
+
+    def __init__(self, cin, cout, kernel, stride, spec, bottleneck=None):
+        super().__init__()
+        stride = tuple(stride)
+        self.slope = spec.leaky_slope
+        if bottleneck is None:
+            self.conv1 = _ConvNorm(cin, cout, kernel, stride, spec)
+            self.conv2 = _ConvNormOnly(cout, cout, kernel, 1, spec, spec.conv_bias)
+            self.branch = (self.conv1, self.conv2)
+        else:
+            self.conv1 = _ConvNorm(cin, bottleneck, (1, 1, 1), 1, spec)
+            self.conv2 = _ConvNorm(bottleneck, bottleneck, kernel, stride, spec)
+            self.conv3 = _ConvNormOnly(bottleneck, cout, (1, 1, 1), 1, spec, spec.conv_bias)
+            self.branch = (self.conv1, self.conv2, self.conv3)
+        ops = []
+        if stride != (1, 1, 1):
+            ops.append(torch.nn.AvgPool3d(stride, stride))
+        if cin != cout:
+            ops.append(_ConvNormOnly(cin, cout, (1, 1, 1), 1, spec, False))
+        self.skip = torch.nn.Sequential(*ops) if ops else None
+
+    def forward(self, x):
+        residual = x if self.skip is None else self.skip(x)
+        out = x
+        for module in self.branch:
+            out = module(out)
+        return torch.nn.functional.leaky_relu(out + residual, self.slope)
+
+
+class UpstreamResidualUNet(torch.nn.Module):
+    """torch.nn modules named and laid out as upstream's ResidualEncoderUNet (stem,
+    ``encoder.stages.<s>.blocks.<b>``, the plain decoder)."""
+
+    def __init__(self, spec):
+        super().__init__()
+        f, k, s = spec.features, spec.kernel_sizes, spec.strides
+        self.encoder = torch.nn.Module()
+        stem_ch = spec.effective_stem_channels
+        self.encoder.stem = _Stage([_ConvNorm(spec.input_channels, stem_ch, k[0], 1, spec)])
+        cin, stages = stem_ch, []
+        for i in range(len(f)):
+            bottleneck = None if spec.bottleneck_channels is None else spec.bottleneck_channels[i]
+            stage = torch.nn.Module()
+            stage.blocks = torch.nn.Sequential(*[
+                _UpstreamResidualBlock(cin if b == 0 else f[i], f[i], k[i],
+                                       s[i] if b == 0 else (1, 1, 1), spec, bottleneck)
+                for b in range(spec.encoder_blocks[i])])
+            stages.append(stage)
+            cin = f[i]
+        self.encoder.stages = torch.nn.ModuleList(stages)
+        self.decoder = torch.nn.Module()
+        up, dec, seg = [], [], []
+        for d in range(len(f) - 1):
+            src, dst = len(f) - 1 - d, len(f) - 2 - d
+            up.append(torch.nn.ConvTranspose3d(f[src], f[dst], s[src], s[src], bias=spec.conv_bias))
+            dec.append(_Stage([_ConvNorm(2 * f[dst] if b == 0 else f[dst], f[dst], k[dst], 1, spec)
+                               for b in range(spec.decoder_convs[d])]))
+            seg.append(torch.nn.Conv3d(f[dst], spec.num_classes, 1, 1, 0, bias=True))
+        self.decoder.transpconvs = torch.nn.ModuleList(up)
+        self.decoder.stages = torch.nn.ModuleList(dec)
+        self.decoder.seg_layers = torch.nn.ModuleList(seg)
+
+    def forward(self, x):
+        x = self.encoder.stem(x)
+        skips = []
+        for stage in self.encoder.stages:
+            x = stage.blocks(x)
+            skips.append(x)
+        x = skips.pop()
+        for d in range(len(self.decoder.stages)):
+            x = torch.cat((self.decoder.transpconvs[d](x), skips.pop()), 1)
+            x = self.decoder.stages[d](x)
+        return self.decoder.seg_layers[-1](x)
+
+
+RESIDUAL_NETS = {
+    "basic": ResidualEncoderUNetSpec(2, 3, (4, 8, 16), K3 * 3, ((1, 1, 1), (2, 2, 2), (1, 2, 2)),
+                                     (1, 2, 2), (1, 1), stem_channels=6),
+    "bottleneck": ResidualEncoderUNetSpec(1, 2, (4, 8, 8), K3 * 3,
+                                          ((1, 1, 1), (2, 2, 2), (2, 2, 2)), (2, 1, 2), (1, 1),
+                                          bottleneck_channels=(2, 3, 4)),
+}
+
+
+@pytest.mark.parametrize("name", sorted(RESIDUAL_NETS))
+def test_converted_residual_weights_compute_what_the_upstream_modules_compute(name):
+    """An upstream residual-encoder state dict (stem, blocks with conv1/conv2[/conv3] and
+    skip.<i>), converted, gives the oracle's residual path the upstream modules' forward."""
+    from oracle.network import OracleNetwork
+
+    spec = RESIDUAL_NETS[name]
+    torch.manual_seed(11)
+    upstream_net = UpstreamResidualUNet(spec).eval()
+    with torch.no_grad():
+        for p in upstream_net.parameters():
+            p.copy_(torch.randn_like(p) * 0.3)
+    state = upstream_net.state_dict()
+    assert any(".skip.1.conv.weight" in key for key in state) or name == "bottleneck"
+    converted = upstream.convert_state_dict(state)
+    assert set(converted.weights) == set(random_weights(spec, seed=0))
+    x = torch.randn(1, spec.input_channels, 8, 16, 12)
+    with torch.no_grad():
+        want = upstream_net(x).permute(0, 2, 3, 4, 1).numpy()
+    got = OracleNetwork(spec, converted.weights, residual=True)(x.permute(0, 2, 3, 4, 1).numpy())
+    assert got.shape == want.shape
+    np.testing.assert_allclose(got, want, rtol=1e-4, atol=1e-4)
+
+
 @pytest.mark.gpu
 def test_converted_folder_runs_on_the_device(tmp_path):
     """A converted folder loads through the model-folder path and its resident fold gives
