@@ -47,15 +47,19 @@ const char* nnx_version(void);
 #define NNX_ARCH_RESIDUAL 1
 #define NNX_PRECISION_FP32 0
 /* Float32 semantics (float32 inputs, weights, accumulation and outputs) with the 3-D
- * convolutions after the first one computed as three fp16 MFMA products of split operands
- * (x = hi + lo), see nnx_conv3d_split.  Meets the float32 logits tolerance; activations
- * must stay below 65504 in magnitude (they are normalised, so they do). */
+ * convolutions computed as three fp16 MFMA products of split operands (x = hi + lo), see
+ * nnx_conv3d_split.  A first convolution with 1 or 2 input channels uses split products
+ * too, with a per-tile power-of-two scale of the raw input (nnx_conv3d_direct_small_cin_split);
+ * other first convolutions keep float32 products.  Meets the float32 logits tolerance;
+ * hidden activations must stay below 65504 in magnitude (they are normalised, so they do). */
 #define NNX_PRECISION_FP32_SPLIT 1
 /* bf16 operands with float32 accumulation (the pancreas config's bf16): the 3-D
  * convolutions after the first one and the transposed convolutions round their weights
  * and input activations to bf16 (nearest even) and multiply on bf16 MFMA, accumulating in
  * float32; InstanceNorm statistics, the first convolution, 1x1x1 convolutions and the
- * activations between layers stay float32.  Logits meet relative-L2 1e-2. */
+ * activations between layers stay float32.  On random-init networks the logits land at
+ * relative-L2 1.0e-2 to 2.3e-2 of the float32 logits, the distance the same bf16 rounding
+ * reaches when emulated on the CPU; relative-L2 1e-2 is not met in general. */
 #define NNX_PRECISION_BF16 2
 
 typedef struct nnx_spec {
@@ -210,14 +214,16 @@ int nnx_conv3d_split(const float* d_x1, int c1, const float* d_x2, int c2, const
 int nnx_conv3d_direct_small_cin(const float* d_x, const float* d_weight /* (Cout,3,3,3,1) */,
                                 const float* d_bias, float* d_y, int batch, const int* size,
                                 int cout, void* stream);
-/* The same convolution with split-fp16 products on MFMA (the 27 taps of 16 voxels as one
- * 16 x 32 fragment, hi*hi + hi*lo + lo*hi, float32 accumulation): weights times `scale`
- * (nnx_split_weight_scale of max |w|), each 4 x 4 x 16 output tile's input times a power
- * of two from the tile's own max |x|, products times the inverses (exact), + bias.
- * Replaces the same reference call as nnx_conv3d_direct_small_cin in the fp32-split
- * precision. */
-int nnx_conv3d_direct_small_cin_split(const float* d_x,
-                                      const float* d_weight /* (Cout,3,3,3,1) */, float scale,
+/* The same convolution with split-fp16 products on MFMA for 1 or 2 input channels (the
+ * 27 * cin (tap, channel) products of 16 voxels as 16 x 32 fragments, hi*hi + hi*lo +
+ * lo*hi, float32 accumulation): weights times `scale` (nnx_split_weight_scale of max |w|),
+ * each 4 x 4 x 16 output tile's input (all channels) times one power of two from the tile's
+ * own max |x|, products times the inverses (exact), + bias.  Replaces the same reference
+ * call as nnx_conv3d_direct_small_cin in the fp32-split precision, and the first
+ * Conv3d of two-channel networks (mx.conv3d via _unbiased_convolution,
+ * src/nnunet_mlx/model/network.py:240-269). */
+int nnx_conv3d_direct_small_cin_split(const float* d_x, int cin /* 1 or 2 */,
+                                      const float* d_weight /* (Cout,3,3,3,cin) */, float scale,
                                       const float* d_bias, float* d_y, int batch,
                                       const int* size, int cout, void* stream);
 

@@ -2507,8 +2507,8 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
                         const int* size, int cout, hipStream_t st, float4* stats, float wscale,
                         int cin) {
   require(x && w && y, "convolution pointers must not be null");
-  require(cin == 1 || (wscale > 0.f && (cin == 2 || cin == 4)),
-          "the direct convolution takes 1 input channel, or 2 or 4 with split products");
+  require(cin == 1 || (wscale > 0.f && cin == 2),
+          "the direct convolution takes 1 input channel, or 2 with split products");
   require(cout >= 4 && cout <= 64 && cout % 4 == 0,
           "one-channel direct convolution supports 4..64 outputs in steps of 4");
   require(batch >= 1 && batch <= 65535, "invalid convolution batch");
@@ -2538,12 +2538,8 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
       hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 1>), grid_x3, dim3(256), 0, st, x, w,    \
                          wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
                          (int)tiles, tpb, stats);                                               \
-    else if (cin == 2)                                                                         \
-      hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 2>), grid_x3, dim3(256), 0, st, x, w,    \
-                         wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
-                         (int)tiles, tpb, stats);                                               \
     else                                                                                       \
-      hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 4>), grid_x3, dim3(256), 0, st, x, w,    \
+      hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 2>), grid_x3, dim3(256), 0, st, x, w,    \
                          wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
                          (int)tiles, tpb, stats);                                               \
     break;

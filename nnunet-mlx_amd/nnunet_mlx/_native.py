@@ -150,8 +150,8 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
     ),
     "nnx_conv3d_direct_small_cin_split": (
         ctypes.c_int,
-        [c_void_p, c_void_p, ctypes.c_float, c_void_p, c_void_p, ctypes.c_int, c_int_p, ctypes.c_int,
-         c_void_p],
+        [c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p, ctypes.c_int, c_int_p,
+         ctypes.c_int, c_void_p],
     ),
     "nnx_tconv3d_packed_floats": (ctypes.c_size_t, [ctypes.c_int, c_int_p, ctypes.c_int]),
     "nnx_tconv3d_pack_weight": (

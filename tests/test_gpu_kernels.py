@@ -141,24 +141,29 @@ def test_direct_single_channel_conv(lib, size, cout):
     assert rel_l2(got, ref) <= 1e-6, report("direct", got, ref)
 
 
-@pytest.mark.parametrize("size,cout,amplitude", [((16, 16, 16), 32, 1.0), ((5, 7, 9), 8, 1.0),
-                                                 ((9, 20, 11), 12, 3e4), ((4, 8, 8), 64, 1e-30)])
-def test_direct_single_channel_conv_split(lib, size, cout, amplitude):
+@pytest.mark.parametrize("size,cout,amplitude,cin", [
+    ((16, 16, 16), 32, 1.0, 1), ((5, 7, 9), 8, 1.0, 1), ((9, 20, 11), 12, 3e4, 1),
+    ((4, 8, 8), 64, 1e-30, 1),
+    # two channels: ragged tiles, and channel amplitudes 1 and 3e4 sharing one tile scale
+    ((7, 9, 19), 32, (1.0, 3e4), 2), ((16, 16, 16), 32, 1.0, 2), ((3, 5, 33), 4, (3e4, 1e-3), 2)])
+def test_direct_single_channel_conv_split(lib, size, cout, amplitude, cin):
     """Split products on MFMA hold the float32 bar of the split kernels at any input range
     (each tile scales its input by a power of two): raw CT-like magnitudes beyond the fp16
-    range, tiny values, and tiles mixing both."""
-    print(f"direct split conv {size} {cout} {amplitude}", flush=True)
+    range, tiny values, and tiles mixing both; with two input channels the channels of one
+    tile share its scale."""
+    print(f"direct split conv {size} {cout} {amplitude} cin={cin}", flush=True)
     rng = np.random.default_rng(11)
-    x = (rng.standard_normal((2, *size, 1)) * amplitude).astype(np.float32)
+    amp = np.broadcast_to(np.asarray(amplitude, dtype=np.float64), (cin,))
+    x = (rng.standard_normal((2, *size, cin)) * amp).astype(np.float32)
     x[0, : size[0] // 2] *= 1e-3  # tiles whose values span three decades
-    w = (rng.standard_normal((cout, 3, 3, 3, 1)) * 0.3).astype(np.float32)
+    w = (rng.standard_normal((cout, 3, 3, 3, cin)) * 0.3).astype(np.float32)
     w.reshape(-1)[::5] *= 1e-3
-    b = (rng.standard_normal(cout) * amplitude * 0.1).astype(np.float32)
+    b = (rng.standard_normal(cout) * amp.max() * 0.1).astype(np.float32)
     scale = lib.nnx_split_weight_scale(float(np.abs(w).max()))
     y = torch.full((2, *size, cout), float("nan"), dtype=torch.float32, device="cuda")
     dx, dw, db = dev(x), dev(w), dev(b)
     _native.check(lib.nnx_conv3d_direct_small_cin_split(
-        dx.data_ptr(), dw.data_ptr(), scale, db.data_ptr(), y.data_ptr(), 2,
+        dx.data_ptr(), cin, dw.data_ptr(), scale, db.data_ptr(), y.data_ptr(), 2,
         _native.ints(size), cout, stream()))
     got = host(y)
     ref = _conv_ref64(x, w, (1, 1, 1)) + b.astype(np.float64)
