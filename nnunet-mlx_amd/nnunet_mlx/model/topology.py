@@ -3,156 +3,201 @@
 Same public surface as the reference's ``nnunet_mlx.model.topology``
 (src/nnunet_mlx/model/topology.py:132-430): ``PlainConvUNetSpec`` and
 ``ResidualEncoderUNetSpec`` frozen dataclasses with ``from_plans``, ``spatial_dims``
-and ``to_payload``.  Only Conv/InstanceNorm/LeakyReLU networks without dropout or
-running statistics are admitted; anything else raises ``ContractError``.
+and ``to_payload``.  A plans file describes the network in
+``configurations.<name>.architecture`` as ``network_class_name`` plus ``arch_kwargs``
+(upstream dynamic_network_architectures constructor arguments).  Only networks this
+package computes exactly are admitted: Conv + InstanceNorm + LeakyReLU, activation after
+the norm, no active dropout, no running statistics.  Anything else raises
+``ContractError`` naming the offending ``arch_kwargs`` entry.
 """
 
 from __future__ import annotations
 
+import math
 from collections.abc import Mapping, Sequence
 from dataclasses import dataclass
-from numbers import Real
 
 from nnunet_mlx.errors import ContractError
 
 SpatialShape = tuple[int, ...]
 
-
-def _mapping(value: object, *, name: str) -> Mapping[str, object]:
-    if not isinstance(value, Mapping):
-        raise ContractError(f"{name} must be a mapping")
-    return value
-
-
-def _sequence(value: object, *, name: str) -> Sequence[object]:
-    if isinstance(value, (str, bytes)) or not isinstance(value, Sequence):
-        raise ContractError(f"{name} must be a sequence")
-    return value
-
-
-def _boolean(value: object, *, name: str) -> bool:
-    if not isinstance(value, bool):
-        raise ContractError(f"{name} must be a boolean")
-    return value
+# Operation class paths must end with these names (torch registers the classes under
+# several module paths, e.g. torch.nn.Conv3d and torch.nn.modules.conv.Conv3d).
+_OPERATION_SUFFIXES = {"conv_op": "Conv{d}d", "norm_op": "InstanceNorm{d}d", "nonlin": "LeakyReLU"}
+# Option keys of the norm, activation and dropout that carry no arithmetic of their own,
+# or whose values are checked below.
+_NORM_OPTIONS = frozenset({"eps", "affine", "momentum", "track_running_stats"})
+_NONLIN_OPTIONS = frozenset({"negative_slope", "inplace"})
+_DROPOUT_OPTIONS = frozenset({"p", "inplace"})
+_DROPOUT_CLASSES = frozenset(
+    f"torch.nn.{module}Dropout{suffix}" for module in ("", "modules.dropout.")
+    for suffix in ("", "2d", "3d"))
 
 
-def _number(value: object, *, name: str) -> float:
-    if isinstance(value, bool) or not isinstance(value, Real):
-        raise ContractError(f"{name} must be a number")
-    number = float(value)
-    if number != number or number in (float("inf"), float("-inf")):
-        raise ContractError(f"{name} must be finite")
-    return number
+class _ArchKwargs:
+    """Typed access to one ``arch_kwargs`` mapping; every failure names its key."""
+
+    def __init__(self, raw: object, where: str) -> None:
+        if not isinstance(raw, Mapping):
+            raise ContractError(f"{where}.arch_kwargs is not a mapping")
+        self.raw = raw
+        self.where = f"{where}.arch_kwargs"
+
+    def error(self, key: str, problem: str) -> ContractError:
+        return ContractError(f"plans {self.where}.{key} {problem}")
+
+    def has(self, key: str) -> bool:
+        return key in self.raw
+
+    def section(self, key: str) -> Mapping[str, object]:
+        value = self.raw.get(key)
+        if value is None:
+            return {}
+        if not isinstance(value, Mapping):
+            raise self.error(key, "is not a mapping")
+        return value
+
+    def flag(self, key: str, default: bool, source: Mapping[str, object] | None = None) -> bool:
+        value = (self.raw if source is None else source).get(key, default)
+        if type(value) is not bool:
+            raise self.error(key, f"must be true or false, not {value!r}")
+        return value
+
+    def real(self, key: str, default: float, source: Mapping[str, object] | None = None) -> float:
+        value = (self.raw if source is None else source).get(key, default)
+        if type(value) is bool or not isinstance(value, (int, float)) or not math.isfinite(value):
+            raise self.error(key, f"must be a finite number, not {value!r}")
+        return float(value)
+
+    def count(self, key: str, value: object = None) -> int:
+        value = self.raw.get(key) if value is None else value
+        if type(value) is not int or value < 1:
+            raise self.error(key, f"must hold positive integers, found {value!r}")
+        return value
+
+    def counts(self, key: str) -> tuple[int, ...]:
+        value = self.raw.get(key)
+        if isinstance(value, (str, bytes)) or not isinstance(value, Sequence) or not value:
+            raise self.error(key, "must be a non-empty list of positive integers")
+        return tuple(self.count(key, item) for item in value)
+
+    def per_stage(self, key: str, stages: int) -> tuple[int, ...]:
+        """One positive count per stage; a single integer stands for every stage."""
+        value = self.raw.get(key)
+        if type(value) is int:
+            return (self.count(key, value),) * stages
+        values = self.counts(key)
+        if len(values) != stages:
+            raise self.error(key, f"has {len(values)} entries for {stages} encoder stages")
+        return values
+
+    def rows(self, key: str) -> tuple[SpatialShape, ...]:
+        """Per-stage spatial rows (kernel sizes, strides): 2 or 3 positive integers each,
+        the same number in every row."""
+        value = self.raw.get(key)
+        if isinstance(value, (str, bytes)) or not isinstance(value, Sequence) or not value:
+            raise self.error(key, "must be a non-empty list of spatial rows")
+        rows = []
+        for row in value:
+            if isinstance(row, (str, bytes)) or not isinstance(row, Sequence):
+                raise self.error(key, f"row {row!r} is not a list")
+            rows.append(tuple(self.count(key, v) for v in row))
+        lengths = {len(r) for r in rows}
+        if len(lengths) != 1 or lengths.pop() not in (2, 3):
+            raise self.error(key, "rows must all hold 2 or all hold 3 integers")
+        return tuple(rows)
 
 
-def _positive_int(value: object, *, name: str) -> int:
-    if isinstance(value, bool) or not isinstance(value, int) or value < 1:
-        raise ContractError(f"{name} must be a positive integer")
-    return value
+def _read_architecture(plans: Mapping[str, object], configuration: str,
+                       class_suffix: str) -> tuple[_ArchKwargs, int]:
+    """The configuration's ``arch_kwargs`` after the checks every admitted network
+    shares, and the number of spatial dimensions."""
+    configurations = plans.get("configurations") if isinstance(plans, Mapping) else None
+    if not isinstance(configurations, Mapping) or configuration not in configurations:
+        raise ContractError(f"nnU-Net plans have no configuration {configuration!r}")
+    entry = configurations[configuration]
+    architecture = entry.get("architecture") if isinstance(entry, Mapping) else None
+    if not isinstance(architecture, Mapping):
+        raise ContractError(f"plans configuration {configuration!r} has no architecture")
+    name = architecture.get("network_class_name")
+    if not isinstance(name, str) or not name.endswith(class_suffix):
+        raise ContractError(f"unsupported nnU-Net architecture {name!r}")
+    args = _ArchKwargs(architecture.get("arch_kwargs"), f"configurations.{configuration}")
+    dims = len(args.rows("kernel_sizes")[0])
 
+    for key, suffix in _OPERATION_SUFFIXES.items():
+        op = args.raw.get(key)
+        wanted = suffix.format(d=dims)
+        if not isinstance(op, str) or not op.endswith("." + wanted):
+            raise ContractError(f"{dims}-D nnU-Net requires {wanted} for {key}, got {op!r}")
 
-def _positive_ints(value: object, *, name: str) -> tuple[int, ...]:
-    result = tuple(_positive_int(item, name=name) for item in _sequence(value, name=name))
-    if not result:
-        raise ContractError(f"{name} must not be empty")
-    return result
+    # the activation must follow the norm
+    if args.flag("nonlin_first", False):
+        raise args.error("nonlin_first", "asks for the activation before the norm, which is "
+                                         "not supported")
+    stages = len(args.counts("features_per_stage"))
+    if args.has("n_stages") and args.count("n_stages") != stages:
+        raise args.error("n_stages", f"is {args.raw['n_stages']} but features_per_stage has "
+                                     f"{stages} entries")
 
+    norm = args.section("norm_op_kwargs")
+    if set(norm) - _NORM_OPTIONS:
+        raise args.error("norm_op_kwargs", f"has unsupported options {sorted(set(norm) - _NORM_OPTIONS)}")
+    if args.flag("track_running_stats", False, norm):
+        raise args.error("norm_op_kwargs", "uses running statistics, which are not supported")
+    if norm.get("momentum") is not None and not 0.0 <= args.real("momentum", 0.1, norm) <= 1.0:
+        raise args.error("norm_op_kwargs", "momentum lies outside [0, 1]")
 
-def _spatial_rows(value: object, *, name: str) -> tuple[SpatialShape, ...]:
-    rows = []
-    for raw in _sequence(value, name=name):
-        row = _positive_ints(raw, name=name)
-        if len(row) not in (2, 3):
-            raise ContractError(f"{name} rows must contain two or three integers")
-        rows.append(row)
-    if len({len(row) for row in rows}) != 1:
-        raise ContractError(f"{name} rows must use one spatial dimensionality")
-    return tuple(rows)
+    nonlin = args.section("nonlin_kwargs")
+    if set(nonlin) - _NONLIN_OPTIONS:
+        raise args.error("nonlin_kwargs", f"has unsupported options {sorted(set(nonlin) - _NONLIN_OPTIONS)}")
 
-
-def _validate_ops(kwargs: Mapping[str, object], *, spatial_dims: int) -> None:
-    conv, norm, nonlin = kwargs.get("conv_op"), kwargs.get("norm_op"), kwargs.get("nonlin")
-    if not isinstance(conv, str) or not conv.endswith(f".Conv{spatial_dims}d"):
-        raise ContractError(f"{spatial_dims}-D nnU-Net requires Conv{spatial_dims}d, got {conv!r}")
-    if not isinstance(norm, str) or not norm.endswith(f".InstanceNorm{spatial_dims}d"):
-        raise ContractError(
-            f"{spatial_dims}-D nnU-Net requires InstanceNorm{spatial_dims}d, got {norm!r}"
-        )
-    if not isinstance(nonlin, str) or not nonlin.endswith(".LeakyReLU"):
-        raise ContractError(f"{spatial_dims}-D nnU-Net requires LeakyReLU, got {nonlin!r}")
-
-
-_DROPOUT = {
-    "torch.nn.Dropout", "torch.nn.Dropout2d", "torch.nn.Dropout3d",
-    "torch.nn.modules.dropout.Dropout", "torch.nn.modules.dropout.Dropout2d",
-    "torch.nn.modules.dropout.Dropout3d",
-}
-
-
-def _validate_semantics(kwargs: Mapping[str, object]) -> None:
-    if _boolean(kwargs.get("nonlin_first", False), name="nonlin_first"):
-        raise ContractError("unsupported nonlin_first activation ordering")
-    stages = len(_sequence(kwargs.get("features_per_stage"), name="features_per_stage"))
-    if "n_stages" in kwargs and _positive_int(kwargs["n_stages"], name="n_stages") != stages:
-        raise ContractError("n_stages does not match features_per_stage")
-    dropout = kwargs.get("dropout_op")
+    dropout = args.raw.get("dropout_op")
     if dropout is not None:
-        if dropout not in _DROPOUT:
-            raise ContractError("unsupported dropout_op")
-        options = _mapping(kwargs.get("dropout_op_kwargs"), name="dropout_op_kwargs")
-        if _number(options.get("p", 0.5), name="dropout p") != 0:
-            raise ContractError("unsupported nonzero dropout")
-        if set(options) - {"p", "inplace"}:
-            raise ContractError("unsupported dropout options")
-    norm = _mapping(kwargs.get("norm_op_kwargs", {}), name="norm_op_kwargs")
-    if set(norm) - {"eps", "affine", "momentum", "track_running_stats"}:
-        raise ContractError("unsupported normalization options")
-    if _boolean(norm.get("track_running_stats", False), name="track_running_stats"):
-        raise ContractError("unsupported normalization running statistics")
-    if norm.get("momentum") is not None:
-        momentum = _number(norm["momentum"], name="normalization momentum")
-        if not 0 <= momentum <= 1:
-            raise ContractError("normalization momentum must be in [0, 1]")
-    nonlin = _mapping(kwargs.get("nonlin_kwargs", {}), name="nonlin_kwargs")
-    if set(nonlin) - {"negative_slope", "inplace"}:
-        raise ContractError("unsupported activation options")
+        if dropout not in _DROPOUT_CLASSES:
+            raise args.error("dropout_op", f"{dropout!r} is not a torch dropout class")
+        options = args.section("dropout_op_kwargs")
+        if set(options) - _DROPOUT_OPTIONS:
+            raise args.error("dropout_op_kwargs", "has unsupported options")
+        if args.real("p", 0.5, options) != 0.0:
+            raise args.error("dropout_op_kwargs", "enables dropout at inference (p != 0)")
+    return args, dims
 
 
-def _architecture(plans: Mapping[str, object], configuration: str, suffix: str):
-    configurations = _mapping(plans.get("configurations"), name="configurations")
-    raw = configurations.get(configuration)
-    if raw is None:
-        raise ContractError(f"nnU-Net plans lack configuration {configuration!r}")
-    architecture = _mapping(_mapping(raw, name=configuration).get("architecture"), name="architecture")
-    class_name = architecture.get("network_class_name")
-    if not isinstance(class_name, str) or not class_name.endswith(suffix):
-        raise ContractError(f"unsupported nnU-Net architecture {class_name!r}")
-    kwargs = _mapping(architecture.get("arch_kwargs"), name="arch_kwargs")
-    _validate_semantics(kwargs)
-    kernel_sizes = _spatial_rows(kwargs.get("kernel_sizes"), name="kernel_sizes")
-    _validate_ops(kwargs, spatial_dims=len(kernel_sizes[0]))
-    return kwargs, kernel_sizes
+def _norm_and_activation(args: _ArchKwargs) -> dict[str, object]:
+    norm = args.section("norm_op_kwargs")
+    nonlin = args.section("nonlin_kwargs")
+    return dict(
+        conv_bias=args.flag("conv_bias", False),
+        norm_eps=args.real("eps", 1e-5, norm),
+        norm_affine=args.flag("affine", False, norm),
+        leaky_slope=args.real("negative_slope", 0.01, nonlin),
+    )
 
 
-def _common_checks(spec, stages_field: tuple[int, ...], name: str) -> None:
-    stages = len(spec.features)
+def _validate_topology(spec, per_stage: tuple[int, ...], kind: str) -> None:
+    """Shape rules both specs share, whether built from plans or directly."""
+    n = len(spec.features)
+    problems = []
     if spec.input_channels < 1 or spec.num_classes < 1:
-        raise ContractError(f"{name} needs input channels and at least one output")
-    if stages < 2:
-        raise ContractError(f"{name} needs at least two stages")
-    if any(len(v) != stages for v in (spec.kernel_sizes, spec.strides, stages_field)):
-        raise ContractError("encoder topology lengths do not match")
-    if len(spec.decoder_convs) != stages - 1:
-        raise ContractError("decoder topology must have one entry per skip connection")
-    dims = {len(row) for row in (*spec.kernel_sizes, *spec.strides)}
-    if len(dims) != 1 or next(iter(dims)) not in (2, 3):
-        raise ContractError(f"{name} requires consistent 2-D or 3-D spatial rows")
-    if any(v < 1 or v % 2 == 0 for row in spec.kernel_sizes for v in row):
-        raise ContractError("only positive odd convolution kernels are supported")
-    if spec.norm_eps <= 0:
-        raise ContractError("normalization epsilon must be positive")
+        problems.append("needs input channels and at least one output")
+    if n < 2:
+        problems.append("needs at least two stages")
+    if {len(spec.kernel_sizes), len(spec.strides), len(per_stage)} != {n}:
+        problems.append("kernel sizes, strides and per-stage counts must have one entry per stage")
+    if len(spec.decoder_convs) != n - 1:
+        problems.append("needs one decoder entry per skip connection")
+    widths = {len(row) for row in spec.kernel_sizes} | {len(row) for row in spec.strides}
+    if len(widths) != 1 or not widths <= {2, 3}:
+        problems.append("kernel and stride rows must all be 2-D or all 3-D")
+    if any(k < 1 or k % 2 == 0 for row in spec.kernel_sizes for k in row):
+        problems.append("convolution kernels must be positive and odd")
+    if not spec.norm_eps > 0:
+        problems.append("normalization epsilon must be positive")
     if not 0 <= spec.leaky_slope <= 1:
-        raise ContractError("LeakyReLU negative_slope must be in [0, 1]")
+        problems.append("LeakyReLU negative_slope must lie in [0, 1]")
+    if problems:
+        raise ContractError(f"{kind}: " + "; ".join(problems))
 
 
 @dataclass(frozen=True)
@@ -173,7 +218,7 @@ class PlainConvUNetSpec:
     leaky_slope: float = 0.01
 
     def __post_init__(self) -> None:
-        _common_checks(self, self.encoder_convs, "PlainConvUNet")
+        _validate_topology(self, self.encoder_convs, "PlainConvUNet")
 
     @property
     def spatial_dims(self) -> int:
@@ -182,22 +227,13 @@ class PlainConvUNetSpec:
     @classmethod
     def from_plans(cls, plans: Mapping[str, object], *, configuration: str, input_channels: int,
                    num_classes: int) -> PlainConvUNetSpec:
-        kwargs, kernel_sizes = _architecture(plans, configuration, ".PlainConvUNet")
-        norm = _mapping(kwargs.get("norm_op_kwargs", {}), name="norm_op_kwargs")
-        nonlin = _mapping(kwargs.get("nonlin_kwargs", {}), name="nonlin_kwargs")
-        return cls(
-            input_channels=input_channels,
-            num_classes=num_classes,
-            features=_positive_ints(kwargs.get("features_per_stage"), name="features"),
-            kernel_sizes=kernel_sizes,
-            strides=_spatial_rows(kwargs.get("strides"), name="strides"),
-            encoder_convs=_positive_ints(kwargs.get("n_conv_per_stage"), name="encoder"),
-            decoder_convs=_positive_ints(kwargs.get("n_conv_per_stage_decoder"), name="decoder"),
-            conv_bias=_boolean(kwargs.get("conv_bias", False), name="conv_bias"),
-            norm_eps=_number(norm.get("eps", 1e-5), name="norm eps"),
-            norm_affine=_boolean(norm.get("affine", False), name="norm affine"),
-            leaky_slope=_number(nonlin.get("negative_slope", 0.01), name="leaky slope"),
-        )
+        args, _ = _read_architecture(plans, configuration, ".PlainConvUNet")
+        features = args.counts("features_per_stage")
+        return cls(input_channels=input_channels, num_classes=num_classes, features=features,
+                   kernel_sizes=args.rows("kernel_sizes"), strides=args.rows("strides"),
+                   encoder_convs=args.per_stage("n_conv_per_stage", len(features)),
+                   decoder_convs=args.counts("n_conv_per_stage_decoder"),
+                   **_norm_and_activation(args))
 
     def to_payload(self) -> dict[str, object]:
         return {
@@ -229,14 +265,14 @@ class ResidualEncoderUNetSpec:
     bottleneck_channels: tuple[int, ...] | None = None
 
     def __post_init__(self) -> None:
-        _common_checks(self, self.encoder_blocks, "ResidualEncoderUNet")
+        _validate_topology(self, self.encoder_blocks, "ResidualEncoderUNet")
         if self.stem_channels is not None and self.stem_channels < 1:
-            raise ContractError("stem channels must be positive")
-        if self.bottleneck_channels is not None:
-            if len(self.bottleneck_channels) != len(self.features):
-                raise ContractError("bottleneck channels must have one entry per encoder stage")
-            if any(c < 1 for c in self.bottleneck_channels):
-                raise ContractError("bottleneck channels must be positive")
+            raise ContractError("ResidualEncoderUNet: stem channels must be positive")
+        if self.bottleneck_channels is not None and (
+                len(self.bottleneck_channels) != len(self.features)
+                or min(self.bottleneck_channels) < 1):
+            raise ContractError("ResidualEncoderUNet: bottleneck channels need one positive "
+                                "entry per encoder stage")
 
     @property
     def spatial_dims(self) -> int:
@@ -249,43 +285,28 @@ class ResidualEncoderUNetSpec:
     @classmethod
     def from_plans(cls, plans: Mapping[str, object], *, configuration: str, input_channels: int,
                    num_classes: int) -> ResidualEncoderUNetSpec:
-        kwargs, kernel_sizes = _architecture(plans, configuration, ".ResidualEncoderUNet")
-        features = _positive_ints(kwargs.get("features_per_stage"), name="features")
-        block = kwargs.get("block")
-        raw_bottleneck = kwargs.get("bottleneck_channels")
+        args, _ = _read_architecture(plans, configuration, ".ResidualEncoderUNet")
+        features = args.counts("features_per_stage")
+        block = args.raw.get("block")
+        # BasicBlockD (the default block) has no bottleneck width; BottleneckD needs one,
+        # given once for every stage or per stage
         if block is None or (isinstance(block, str) and block.endswith(".BasicBlockD")):
-            if raw_bottleneck is not None:
-                raise ContractError("BasicBlockD plans must not define bottleneck channels")
+            if args.raw.get("bottleneck_channels") is not None:
+                raise args.error("bottleneck_channels", "is set for BasicBlockD blocks")
             bottleneck = None
         elif isinstance(block, str) and block.endswith(".BottleneckD"):
-            if raw_bottleneck is None:
-                raise ContractError("BottleneckD requires bottleneck channels")
-            if isinstance(raw_bottleneck, int) and not isinstance(raw_bottleneck, bool):
-                bottleneck = (_positive_int(raw_bottleneck, name="bottleneck channels"),) * len(features)
-            else:
-                bottleneck = _positive_ints(raw_bottleneck, name="bottleneck channels")
-                if len(bottleneck) != len(features):
-                    raise ContractError("bottleneck channels must have one entry per encoder stage")
+            if args.raw.get("bottleneck_channels") is None:
+                raise args.error("bottleneck_channels", "is required for BottleneckD blocks")
+            bottleneck = args.per_stage("bottleneck_channels", len(features))
         else:
-            raise ContractError(f"unsupported residual block {block!r}")
-        norm = _mapping(kwargs.get("norm_op_kwargs", {}), name="norm_op_kwargs")
-        nonlin = _mapping(kwargs.get("nonlin_kwargs", {}), name="nonlin_kwargs")
-        raw_stem = kwargs.get("stem_channels")
-        return cls(
-            input_channels=input_channels,
-            num_classes=num_classes,
-            features=features,
-            kernel_sizes=kernel_sizes,
-            strides=_spatial_rows(kwargs.get("strides"), name="strides"),
-            encoder_blocks=_positive_ints(kwargs.get("n_blocks_per_stage"), name="encoder blocks"),
-            decoder_convs=_positive_ints(kwargs.get("n_conv_per_stage_decoder"), name="decoder"),
-            conv_bias=_boolean(kwargs.get("conv_bias", False), name="conv_bias"),
-            norm_eps=_number(norm.get("eps", 1e-5), name="norm eps"),
-            norm_affine=_boolean(norm.get("affine", False), name="norm affine"),
-            leaky_slope=_number(nonlin.get("negative_slope", 0.01), name="leaky slope"),
-            stem_channels=None if raw_stem is None else _positive_int(raw_stem, name="stem channels"),
-            bottleneck_channels=bottleneck,
-        )
+            raise args.error("block", f"{block!r} is not BasicBlockD or BottleneckD")
+        stem = args.raw.get("stem_channels")
+        return cls(input_channels=input_channels, num_classes=num_classes, features=features,
+                   kernel_sizes=args.rows("kernel_sizes"), strides=args.rows("strides"),
+                   encoder_blocks=args.per_stage("n_blocks_per_stage", len(features)),
+                   decoder_convs=args.counts("n_conv_per_stage_decoder"),
+                   stem_channels=None if stem is None else args.count("stem_channels"),
+                   bottleneck_channels=bottleneck, **_norm_and_activation(args))
 
     def to_payload(self) -> dict[str, object]:
         return {

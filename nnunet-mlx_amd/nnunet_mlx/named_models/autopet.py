@@ -1,4 +1,5 @@
-"""nnU-Net AutoPET II whole-body PET/CT lesion segmentation (``nnunet-autopet``).
+"""Named model ``nnunet-autopet``: nnU-Net lesion segmentation of whole-body PET/CT
+(AutoPET II).
 
 Reference: src/nnunet_mlx/named_models/autopet.py:14-57.
 """
@@ -24,8 +25,9 @@ CHANNELS = ("ct", "pet")
 def run(*, image_paths: Mapping[str, PathLike], output_dir: PathLike,
         weights_path: PathLike | None = None, overwrite: bool = False,
         use_mirroring: bool = True, step_fraction: float = 0.5) -> dict:
-    """Segment tumor lesions from ``{"ct", "pet"}`` with every fold of the
-    ``3d_fullres_resenc_bs80`` configuration."""
+    """Label tumour lesions from the mapping ``{"ct": ..., "pet": ...}`` (co-registered CT
+    and SUV PET, NIfTI), averaging all folds of the ``3d_fullres_resenc_bs80``
+    configuration."""
     channels = input_channels(image_paths, CHANNELS)
     images, _ = medmlx.check_request(list(channels.values()), output_dir=output_dir,
                                      overwrite=overwrite, use_mirroring=use_mirroring,

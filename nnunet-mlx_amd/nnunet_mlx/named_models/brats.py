@@ -1,4 +1,5 @@
-"""nnU-Net BraTS brain-tumor MRI segmentation (``nnunet-brats2021``).
+"""Named model ``nnunet-brats2021``: nnU-Net brain-tumour segmentation of four MRI
+sequences.
 
 Reference: src/nnunet_mlx/named_models/brats.py:15-62.
 """
@@ -25,8 +26,9 @@ CHANNELS = ("t1", "t1ce", "t2", "flair")
 def run(*, image_paths: Mapping[str, PathLike], output_dir: PathLike,
         weights_path: PathLike | None = None, overwrite: bool = False, fold: int | None = None,
         use_mirroring: bool = True) -> dict:
-    """Segment four co-registered MRI sequences ``{"t1", "t1ce", "t2", "flair"}``; all five
-    folds are ensembled unless ``fold`` (0..4) selects one."""
+    """Label a brain tumour from the mapping ``{"t1": ..., "t1ce": ..., "t2": ..., "flair":
+    ...}`` of co-registered NIfTI volumes.  The five trained folds are averaged; an integer
+    ``fold`` between 0 and 4 uses that fold alone."""
     if fold is not None and (isinstance(fold, bool) or fold not in range(5)):
         raise ContractError("BraTS fold must be between 0 and 4")
     channels = input_channels(image_paths, CHANNELS)

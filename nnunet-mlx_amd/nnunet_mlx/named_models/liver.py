@@ -1,4 +1,4 @@
-"""nnU-Net liver and liver-cancer CT segmentation (``nnunet-liver``).
+"""Named model ``nnunet-liver``: nnU-Net segmentation of the liver and its tumours in CT.
 
 Reference: src/nnunet_mlx/named_models/liver.py:12-99.
 """
@@ -19,9 +19,10 @@ MODEL = {
 
 def run(*, image_path: PathLike, output_dir: PathLike, weights_path: PathLike | None = None,
         overwrite: bool = False, use_mirroring: bool = True, step_fraction: float = 0.5) -> dict:
-    """Segment liver (1) and liver cancer (2) in one CT (NIfTI, Hounsfield units), on the
-    CT's grid; ``mask.nii.gz`` goes to ``output_dir``.  Three-axis mirroring (8 network
-    passes per tile) and a 0.5 step by default."""
+    """Label one Hounsfield-unit CT volume (NIfTI): 1 = liver, 2 = tumour, 0 elsewhere.
+    The label map keeps the input's voxel grid and is written as ``mask.nii.gz`` in
+    ``output_dir``.  Defaults reproduce the published setup: every test-time flip of the
+    three axes (8 forwards per tile) and tiles half a patch apart."""
     images, _ = medmlx.check_request([image_path], output_dir=output_dir, overwrite=overwrite,
                                      use_mirroring=use_mirroring, step_fraction=step_fraction)
     folder = model_folder("nnunet-liver", weights_path)
@@ -31,7 +32,8 @@ def run(*, image_path: PathLike, output_dir: PathLike, weights_path: PathLike | 
 
 
 class LiverModel:
-    """The liver model loaded once; :meth:`run` takes the per-CT arguments."""
+    """A resident liver model: weights go to the GPU once, then :meth:`run` labels one CT
+    per call with the options given to :func:`load_model`."""
 
     def __init__(self, model: medmlx.NnUNetModel) -> None:
         self._model = model
@@ -52,7 +54,7 @@ class LiverModel:
 
 def load_model(*, weights_path: PathLike | None = None, use_mirroring: bool = True,
                step_fraction: float = 0.5) -> LiverModel:
-    """Load the liver model once to segment several CTs."""
+    """Put the liver model on the GPU for repeated :meth:`LiverModel.run` calls."""
     folder = model_folder("nnunet-liver", weights_path)
     return LiverModel(medmlx.load_model(weights_path=folder, configuration="3d_fullres",
                                         use_mirroring=use_mirroring,

@@ -1,4 +1,4 @@
-"""Pancreas and pancreatic-cancer CT segmentation (``nnunet-pancreas``).
+"""Named model ``nnunet-pancreas``: segmentation of the pancreas and its tumours in CT.
 
 Reference: src/nnunet_mlx/named_models/pancreas.py:12-49.
 """
@@ -18,8 +18,9 @@ MODEL = {
 
 def run(*, image_path: PathLike, output_dir: PathLike, weights_path: PathLike | None = None,
         overwrite: bool = False, fold: int = 0, use_mirroring: bool = True) -> dict:
-    """Segment pancreas (1) and cancer (2) in one CT with the ``3d_fullres_bs4``
-    configuration; ``fold`` is the converted checkpoint slot (fold_all staged in 0)."""
+    """Label one CT volume (NIfTI): 1 = pancreas, 2 = tumour.  Runs the ``3d_fullres_bs4``
+    configuration from converted checkpoint slot ``fold`` (slot 0 holds the network
+    trained on all data)."""
     images, _ = medmlx.check_request([image_path], output_dir=output_dir, overwrite=overwrite,
                                      folds=[fold], use_mirroring=use_mirroring)
     folder = model_folder("nnunet-pancreas", weights_path)
