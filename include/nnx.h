@@ -181,6 +181,19 @@ int nnx_instnorm_lrelu(const float* d_x, float* d_y, int batch, int64_t spatial,
                        float eps, int apply_act, float slope, const float* d_residual,
                        void* d_workspace, size_t workspace_bytes, void* stream);
 
+/* nnx_instnorm_lrelu without a workspace and without any allocation: the partials and
+ * parameters live in a file-scope device array of nnx_instnorm_noalloc_max_bytes() bytes
+ * (16 MiB; each GPU keeps its own copy until the process ends).  No counterpart in the
+ * reference: for callers that cannot allocate device memory (code under HIP graph capture,
+ * tight serving loops, harnesses that forbid hipMalloc).  Sizes whose
+ * nnx_instnorm_workspace_bytes() exceeds the scratch return NNX_ERR_INVALID.  Calls that
+ * overlap on one GPU share the scratch and race; the caller serialises them. */
+size_t nnx_instnorm_noalloc_max_bytes(void);
+int nnx_instnorm_lrelu_noalloc(const float* d_x, float* d_y, int batch, int64_t spatial,
+                               int channels, const float* d_input_bias, const float* d_gamma,
+                               const float* d_beta, float eps, int apply_act, float slope,
+                               const float* d_residual, void* stream);
+
 /* Implicit-GEMM 3-D convolution on fp32 MFMA, NDHWC.  Two input pointers implement the
  * concat-free decoder convolution conv(concat(x1, x2)) (x2 may be NULL, c2 = 0).
  * Padding is k//2 per axis; the bias (may be NULL) is added to each output.

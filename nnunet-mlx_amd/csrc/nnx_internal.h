@@ -215,6 +215,11 @@ void conv1x1(const float* x, int cin, const float* w, const float* bias, float* 
              int64_t item_voxels = 0);
 
 size_t instnorm_workspace_bytes(int batch, int64_t spatial, int channels);
+size_t instnorm_noalloc_max_bytes();
+void instnorm_lrelu_noalloc(const float* x, float* y, int batch, int64_t spatial, int channels,
+                            const float* input_bias, const float* gamma, const float* beta,
+                            float eps, bool act, float slope, const float* residual,
+                            hipStream_t st);
 void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int channels,
                     const float* input_bias, const float* gamma, const float* beta, float eps,
                     bool act, float slope, const float* residual, void* ws, size_t ws_bytes,

@@ -9,6 +9,8 @@
 //      update in float64, giving mean and biased variance of x + input_bias.
 //   3. norm_apply: y = max(slope*r, r), r = fma(x + b - mean, gamma*rsqrt(var+eps), beta)
 //      (+ residual before the activation), vectorised float4, in place allowed.
+#include <mutex>
+
 #include "nnx_internal.h"
 
 namespace nnx {
@@ -499,6 +501,56 @@ void instnorm_lrelu(const float* x, float* y, int batch, int64_t spatial, int ch
                                                          ((partial_bytes + 255) / 256) * 256);
   instnorm_apply_params(x, y, batch, spatial, channels, params, input_bias, act, slope, residual,
                         st);
+}
+
+// ---- allocation-free InstanceNorm + LeakyReLU ---------------------------------------
+// `scratch` replaces the caller's workspace of instnorm_lrelu: per-chunk partials and the
+// per-(b, c) parameters, instnorm_workspace_bytes() of it.  Every device the library runs on
+// holds its own copy until the process ends.  Nothing in it needs clearing between calls
+// (the statistics pass writes every partial the merge reads, the merge every parameter the
+// apply pass reads), but two calls in flight on one device share it and race.
+constexpr size_t kNoAllocScratchBytes = (size_t)16 << 20;
+__device__ __align__(256) unsigned char scratch[kNoAllocScratchBytes];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of the current device's `scratch`, looked up on the first call on that
+// device (the array's name is only a host-side handle, not a device address).
+void* scratch_address() {
+  int device = -1;
+  hip_check(hipGetDevice(&device), "hipGetDevice");
+  require(device >= 0 && device < kMaxScratchDevices, "device index out of range");
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[device]) {
+    void* ptr = nullptr;
+    hip_check(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)), "hipGetSymbolAddress(scratch)");
+    require(ptr != nullptr, "scratch symbol has no device address");
+    g_scratch_ptr[device] = ptr;
+  }
+  return g_scratch_ptr[device];
+}
+}  // namespace
+
+size_t instnorm_noalloc_max_bytes() { return kNoAllocScratchBytes; }
+
+void instnorm_lrelu_noalloc(const float* x, float* y, int batch, int64_t spatial, int channels,
+                            const float* input_bias, const float* gamma, const float* beta,
+                            float eps, bool act, float slope, const float* residual,
+                            hipStream_t st) {
+  require(x && y, "instance normalisation pointers must not be null");
+  require(batch >= 1 && spatial >= 1 && channels >= 1,
+          "instance normalisation needs a non-empty tensor");
+  const size_t need = instnorm_workspace_bytes(batch, spatial, channels);
+  if (need > kNoAllocScratchBytes)
+    fail(NNX_ERR_INVALID, "instance normalisation of this size needs " + std::to_string(need) +
+                              " bytes of workspace, more than the allocation-free entry's " +
+                              std::to_string(kNoAllocScratchBytes) +
+                              "-byte scratch; use nnx_instnorm_lrelu with a workspace");
+  instnorm_lrelu(x, y, batch, spatial, channels, input_bias, gamma, beta, eps, act, slope,
+                 residual, scratch_address(), kNoAllocScratchBytes, st);
 }
 
 void instnorm_merge_partials(float4* partials, int nparts, int batch, int64_t spatial,

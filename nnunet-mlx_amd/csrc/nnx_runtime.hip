@@ -1032,6 +1032,18 @@ int nnx_instnorm_lrelu(const float* d_x, float* d_y, int batch, int64_t spatial,
   });
 }
 
+size_t nnx_instnorm_noalloc_max_bytes(void) { return instnorm_noalloc_max_bytes(); }
+
+int nnx_instnorm_lrelu_noalloc(const float* d_x, float* d_y, int batch, int64_t spatial,
+                               int channels, const float* d_input_bias, const float* d_gamma,
+                               const float* d_beta, float eps, int apply_act, float slope,
+                               const float* d_residual, void* stream) {
+  return guarded([&] {
+    instnorm_lrelu_noalloc(d_x, d_y, batch, spatial, channels, d_input_bias, d_gamma, d_beta,
+                           eps, apply_act != 0, slope, d_residual, as_stream(stream));
+  });
+}
+
 size_t nnx_conv3d_packed_floats(int cout, const int* ksize, int c1, int c2) {
   if (!ksize || cout < 1 || c1 < 1 || c2 < 0) return 0;
   return (size_t)conv_packed_floats(cout, ksize, c1, c2);

@@ -125,6 +125,12 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int, c_void_p, c_void_p, c_void_p,
          ctypes.c_float, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p, ctypes.c_size_t, c_void_p],
     ),
+    "nnx_instnorm_noalloc_max_bytes": (ctypes.c_size_t, []),
+    "nnx_instnorm_lrelu_noalloc": (
+        ctypes.c_int,
+        [c_void_p, c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_int, c_void_p, c_void_p, c_void_p,
+         ctypes.c_float, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p],
+    ),
     "nnx_conv3d_packed_floats": (ctypes.c_size_t, [ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_int]),
     "nnx_conv3d_pack_weight": (
         ctypes.c_int, [c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, ctypes.c_int, c_void_p, c_void_p]
