@@ -214,6 +214,21 @@ def kernel_class_of(short: str) -> str | None:
 
 
 TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic_liver_case.md"
+SOURCES_LINE = "Kernel sources sha256: "
+
+
+def kernel_sources_digest() -> str:
+    """SHA-256 (16 hex digits) of the HIP sources and the C-ABI header: a counter summary
+    describes the kernels built from exactly these sources."""
+    import hashlib
+
+    h = hashlib.sha256()
+    files = sorted((ROOT / "nnunet-mlx_amd" / "csrc").glob("*.hip"))
+    files += sorted((ROOT / "nnunet-mlx_amd" / "csrc").glob("*.h")) + [ROOT / "include" / "nnx.h"]
+    for f in files:
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
 
 
 def summarize_profiles(directory: str) -> None:
@@ -276,6 +291,9 @@ def summarize_profiles(directory: str) -> None:
         f"{neg['FETCH_SIZE']:.0f} KiB and WRITE_SIZE = {neg['WRITE_SIZE']:.0f} KiB, so FETCH_SIZE is "
         f"scaled by {fetch_factor:.4f} and WRITE_SIZE by {write_factor:.4f}.",
         "",
+        f"{SOURCES_LINE}{kernel_sources_digest()} (bench.py reports this traffic only while the "
+        "sources are unchanged).",
+        "",
         "| kernel | launches | fetch bytes/launch | write bytes/launch | traffic bytes/launch |",
         "|---|---:|---:|---:|---:|",
     ]
@@ -289,10 +307,16 @@ def summarize_profiles(directory: str) -> None:
 
 
 def measured_traffic(kernel_class: str) -> float | None:
-    """HBM bytes per launch of `kernel_class` from the committed counter summary."""
+    """HBM bytes per launch of `kernel_class` from the committed counter summary, or None
+    when the summary is missing or was measured on other kernel sources than these."""
     if not TRAFFIC_FILE.is_file():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    text = TRAFFIC_FILE.read_text()
+    if f"{SOURCES_LINE}{kernel_sources_digest()}" not in text:
+        print("[bench] the HBM traffic summary describes other kernel sources: traffic omitted",
+              file=sys.stderr, flush=True)
+        return None
+    for line in text.splitlines():
         cells = [c.strip().strip("`") for c in line.strip("|").split("|")]
         if len(cells) == 5 and cells[0] == kernel_class:
             return float(cells[4])
@@ -300,8 +324,12 @@ def measured_traffic(kernel_class: str) -> float | None:
 
 
 def cpu_baseline(spec, weights) -> dict:
-    """Oracle forward of one 128^3 view on the host cores + one tile's accumulation,
-    extrapolated to the case (968 forwards, 121 accumulations)."""
+    """The CPU oracle on a bounded sample of the liver case: one 128^3 forward (median of 3
+    after one warm-up) and one tile's mirrored average + Gaussian accumulation with the
+    oracle's own flips (8 views: flip, forward output, flip back, sum, divide, accumulate;
+    median of 3), extrapolated to the case's 968 forwards and 121 tiles."""
+    import statistics
+
     import numpy as np
     import torch
 
@@ -311,22 +339,26 @@ def cpu_baseline(spec, weights) -> dict:
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
     net = OracleNetwork(spec, weights)
-    x = np.random.default_rng(0).standard_normal((1, *PATCH, 1)).astype(np.float32)
-    t0 = time.perf_counter()
-    pred = net(x)
-    forward_s = time.perf_counter() - t0
+    x = synthetic_ct((1, *PATCH), seed=3)[0][None, ..., None]
+    pred = net(x)                                          # warm-up
+    forward_times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        pred = net(x)
+        forward_times.append(time.perf_counter() - t0)
+    forward_s = statistics.median(forward_times)
     g = osw.gaussian_importance(PATCH)[..., None]
     acc = np.zeros((*PATCH, 3), dtype=np.float32)
     norm = np.zeros((*PATCH, 1), dtype=np.float32)
-    views = [pred[0]] * 8
-    t0 = time.perf_counter()
-    s = views[0].copy()
-    for v in views[1:]:
-        s = s + v
-    s = s / np.float32(8)
-    acc += s * g
-    norm += g
-    accumulate_s = time.perf_counter() - t0
+    cached = pred  # the network's output stands in for each view's forward
+    accumulate_times = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        p = osw.mirrored_prediction(lambda tile: cached, x, (0, 1, 2))[0]
+        acc += p * g
+        norm += g
+        accumulate_times.append(time.perf_counter() - t0)
+    accumulate_s = statistics.median(accumulate_times)
     case_s = 968 * forward_s + 121 * accumulate_s
     voxels = int(np.prod(VOLUME_SHAPE[1:]))
     cpu_model = ""
@@ -342,10 +374,11 @@ def cpu_baseline(spec, weights) -> dict:
         "unit": "voxels/s",
         "cores": cores,
         "kind": "port",
-        "sample": (f"one 128^3 forward ({forward_s:.2f} s) + one tile accumulation "
-                   f"({accumulate_s:.3f} s) of the CPU oracle (torch-CPU fp32 network, numpy "
-                   f"accumulation), extrapolated to 968 forwards + 121 accumulations "
-                   f"= {case_s:.0f} s per case; {cores} threads on {cpu_model or 'host CPU'}"),
+        "sample": (f"CPU oracle (torch-CPU fp32 network, numpy sliding window) on {cores} "
+                   f"threads of {cpu_model or 'the host CPU'}: one 128^3 forward "
+                   f"{forward_s:.2f} s (median of 3 after a warm-up) and one tile's 8-view "
+                   f"mirrored average + Gaussian accumulation {accumulate_s:.3f} s (median of "
+                   f"3), extrapolated to 968 forwards + 121 tiles = {case_s:.0f} s per case"),
     }
 
 

@@ -30,3 +30,17 @@ def rel_l2(actual: np.ndarray, expected: np.ndarray) -> float:
 def report(name: str, actual: np.ndarray, expected: np.ndarray) -> str:
     diff = np.abs(np.asarray(actual, np.float64) - np.asarray(expected, np.float64))
     return f"{name}: max_abs={diff.max():.3e} rel_l2={rel_l2(actual, expected):.3e}"
+
+
+def install_package(target) -> "Path":
+    """pip-install this repository (offline, no dependencies) into ``target``; returns the
+    directory holding the console scripts."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parents[1]
+    subprocess.run([sys.executable, "-m", "pip", "install", "--quiet", "--no-deps", "--no-index",
+                    "--no-build-isolation", "--target", str(target), str(root)],
+                   check=True, capture_output=True, text=True)
+    return Path(target) / "bin"

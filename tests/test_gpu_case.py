@@ -159,9 +159,29 @@ def test_cli_predicts_an_upstream_folder(tmp_path, monkeypatch):
         ref = medmlx.run(weights_path=folder, image_paths=[tmp_path / "in" / f"{case}_0000.nii.gz"],
                          output_dir=tmp_path / f"ref_{case}")
         np.testing.assert_array_equal(got, nifti.read_nifti(ref["outputs"]["mask"]).array)
-    # the second call reuses the conversion and skips the finished case
-    assert main(["predict", "-i", str(tmp_path / "in"), "-o", str(tmp_path / "out"), "-d", "1",
-                 "-c", "3d_fullres", "-f", "0", "--continue_prediction"]) == 0
+    # the installed console script, as a separate process: it reuses the conversion and
+    # skips the finished case, then predicts a third case to another folder
+    import os
+    import subprocess
+
+    from tests.helpers import install_package
+
+    bin_dir = install_package(tmp_path / "site")
+    env = dict(os.environ, PYTHONPATH=str(tmp_path / "site"))
+    synthetic_ct(tmp_path / "in" / "c3_0000.nii.gz", seed=8)
+    print("raw case: installed nnunet-mlx predict as a subprocess", flush=True)
+    out = subprocess.run([str(bin_dir / "nnunet-mlx"), "predict", "-i", str(tmp_path / "in"),
+                          "-o", str(tmp_path / "out"), "-d", "1", "-c", "3d_fullres", "-f", "0",
+                          "--continue_prediction", "--json"], env=env, capture_output=True,
+                         text=True, timeout=300)
+    assert out.returncode == 0, out.stderr
+    predicted = json.loads(out.stdout.strip().splitlines()[-1])["predicted"]
+    assert any(p.endswith("c3.nii.gz") for p in predicted), predicted
+    assert not any(p.endswith(("c1.nii.gz", "c2.nii.gz")) for p in predicted), predicted
+    got = nifti.read_nifti(tmp_path / "out" / "c3.nii.gz").array
+    ref = medmlx.run(weights_path=folder, image_paths=[tmp_path / "in" / "c3_0000.nii.gz"],
+                     output_dir=tmp_path / "ref_c3")
+    np.testing.assert_array_equal(got, nifti.read_nifti(ref["outputs"]["mask"]).array)
 
 
 def test_brats_style_mri_case(tmp_path):
