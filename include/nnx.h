@@ -222,6 +222,25 @@ int nnx_conv3d_split(const float* d_x1, int c1, const float* d_x2, int c2, const
                      float scale, const float* d_bias, float* d_y, int batch, const int* in_size,
                      int cout, const int* ksize, const int* stride, void* stream);
 
+/* The same convolution in Winograd form F(2x2x2, 3x3x3) for stride-1 3x3x3 layers with
+ * C_out % 32 == 0 and c1, c2 multiples of 16: per 2x2x2 output tile the 4x4x4 input patch
+ * and each 3x3x3 filter are transformed (additions, and halves for the filter: exact in
+ * float32 / float64), the 64 transform positions are multiplied as split-fp16 products
+ * (hi*hi + hi*lo + lo*hi, float32 accumulation) on fp16 MFMA, and the output transform
+ * returns the tile; 64 products per 8 outputs instead of 216.  Filters are transformed in
+ * float64, multiplied by `scale` (nnx_winograd_weight_scale(max |w|)) and split when
+ * packed; outputs are multiplied by 1/scale (exact), + bias.  Replaces the same reference
+ * calls as nnx_conv3d_igemm (mx.conv3d via _unbiased_convolution,
+ * src/nnunet_mlx/model/network.py:240-269, and the split concat convolution,
+ * src/nnunet_mlx/model/network.py:305-322). */
+float nnx_winograd_weight_scale(float max_abs); /* 0 for a negative or non-finite argument */
+size_t nnx_conv3d_winograd_packed_bytes(int cout, int c1, int c2);
+int nnx_conv3d_winograd_pack_weight(const float* d_weight /* (Cout,3,3,3,c1+c2) */, int cout,
+                                    int c1, int c2, float scale, void* d_packed, void* stream);
+int nnx_conv3d_winograd(const float* d_x1, int c1, const float* d_x2, int c2,
+                        const void* d_packed, float scale, const float* d_bias, float* d_y,
+                        int batch, const int* in_size, int cout, void* stream);
+
 /* One-input-channel 3x3x3 stride-1 pad-1 convolution, fma over taps in (kd,kh,kw) order.
  * Replaces single_channel_conv3d (src/nnunet_mlx/kernels/metal_single_channel_conv.py:32-97). */
 int nnx_conv3d_direct_small_cin(const float* d_x, const float* d_weight /* (Cout,3,3,3,1) */,

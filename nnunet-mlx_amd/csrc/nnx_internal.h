@@ -149,6 +149,22 @@ void conv3d_x3(const float* x1, int c1, const float* x2, int c2, const void* pac
                hipStream_t st, float4* stats = nullptr, const PendingNorm& n1 = {},
                const PendingNorm& n2 = {}, int arith = kArithSplit3);
 int conv_x3_stats_tiles(const ConvGeom& g, int cout);
+
+// Winograd F(2x2x2, 3x3x3) convolution with split-fp16 products (nnx_wino.hip): stride-1
+// 3x3x3 layers with C_out % 32 == 0 and input channel counts that are multiples of 16.
+// Weights are transformed (U = G w G^T per input/output channel pair), multiplied by
+// `scale` (wino_weight_scale) and split at packing; stats as conv3d_x3 with tiles =
+// conv_wino_stats_tiles (4 x 8 x 8 output boxes).
+bool conv_wino_supported(const ConvGeom& g, int c1, int c2, int cout);
+int conv_wino_stats_tiles(const ConvGeom& g);
+float wino_weight_scale(float max_abs);
+int64_t conv_wino_packed_bytes(int cout, int c1, int c2);
+void conv_wino_pack_weight(const float* d_w, int cout, int c1, int c2, float scale,
+                           void* d_packed, hipStream_t st);
+void conv3d_wino(const float* x1, int c1, const float* x2, int c2, const void* packed,
+                 float scale, const float* bias, float* y, const ConvGeom& g, int cout,
+                 hipStream_t st, float4* stats = nullptr, const PendingNorm& n1 = {},
+                 const PendingNorm& n2 = {});
 // Whether the split kernel handles this kernel size / stride (tap count and halo size).
 bool conv_x3_supported(const int* ksize, const int* stride, int cout);
 // With `stats`: per-block InstanceNorm partials, conv_direct_stats_tiles(size) per item.

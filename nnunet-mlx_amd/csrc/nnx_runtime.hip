@@ -148,6 +148,7 @@ struct ConvNorm {
   bool direct_multi = false;  // 2 input channels: direct with split products if first
   bool first = false;   // reads the network input (kept in exact float32 products)
   bool split = false;   // packed for the split-fp16 kernel
+  bool wino = false;    // packed for the Winograd split-fp16 kernel (within `split`)
   float scale = 1.f;    // power-of-two weight scale of the split packing
   DevBuf packed;
 };
@@ -348,6 +349,17 @@ bool uses_split_kernels(const nnx_model* m) {
   return m->precision == NNX_PRECISION_FP32_SPLIT || m->precision == NNX_PRECISION_BF16;
 }
 
+// The Winograd form serves the fp32-split precision's stride-1 3x3x3 layers it supports;
+// NNX_CONV_ALGO=winograd routes the stride-1 3x3x3 split layers with C_out % 32 == 0 and
+// 16-channel input blocks to the Winograd kernel (read when a model's weights are packed).
+// The direct implicit GEMM stays the default: the Winograd kernel measures level with it
+// (one wave a SIMD holds its 256 accumulator registers, which leaves its loads, transforms
+// and epilogue unhidden).
+bool winograd_enabled() {
+  const char* v = std::getenv("NNX_CONV_ALGO");
+  return v && std::string(v) == "winograd";
+}
+
 void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
   if (c.first && c.direct_multi && m->precision == NNX_PRECISION_FP32_SPLIT) c.direct = true;
   if (c.direct) {
@@ -365,6 +377,16 @@ void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
   // products with a per-tile input scale in the fp32-split precision).
   const int taps = c.k[0] * c.k[1] * c.k[2];
   c.split = uses_split_kernels(m) && !c.first && taps >= 8 && conv_x3_supported(c.k, c.s, c.cout);
+  if (c.split && m->precision == NNX_PRECISION_FP32_SPLIT && winograd_enabled()) {
+    const int probe[3] = {16, 16, 16};
+    c.wino = conv_wino_supported(make_conv_geom(1, probe, c.k, c.s), c.cin1, c.cin2, c.cout);
+  }
+  if (c.wino) {
+    c.scale = wino_weight_scale(m->params[c.pw].max_abs);
+    c.packed.ensure((size_t)conv_wino_packed_bytes(c.cout, c.cin1, c.cin2));
+    conv_wino_pack_weight(pdev(m, c.pw), c.cout, c.cin1, c.cin2, c.scale, c.packed.ptr, st);
+    return;
+  }
   if (c.split) {
     c.scale = split_weight_scale(m->params[c.pw].max_abs);
     c.packed.ensure((size_t)conv_x3_packed_bytes(c.cout, c.k, c.cin1, c.cin2));
@@ -486,14 +508,18 @@ struct Runner {
     // Implicit GEMM: the epilogue writes per-tile statistics, so the norm never re-reads the
     // tensor for them.
     const ConvGeom g = make_conv_geom(n, in.d, c.k, c.s);
-    const int tiles = c.split ? conv_x3_stats_tiles(g, c.cout)
-                              : conv_stats_tiles(g, c.cout, c.cin1, c.cin2);
+    const int tiles = c.wino    ? conv_wino_stats_tiles(g)
+                      : c.split ? conv_x3_stats_tiles(g, c.cout)
+                                : conv_stats_tiles(g, c.cout, c.cin1, c.cin2);
     if (plan->planning) {
       plan->stats = std::max(plan->stats, (size_t)n * tiles * c.cout * sizeof(float4));
       return result;
     }
     float4* stats = plan->ws->stats.as<float4>();
-    if (c.split)
+    if (c.wino)
+      conv3d_wino(x1.data, c.cin1, x2.data, c.cin2, c.packed.ptr, c.scale, pdev(m, c.pb), out, g,
+                  c.cout, st, stats, x1.norm, x2.norm);
+    else if (c.split)
       conv3d_x3(x1.data, c.cin1, x2.data, c.cin2, c.packed.ptr, c.scale, pdev(m, c.pb), out, g,
                 c.cout, st, stats, x1.norm, x2.norm, split_arith(m));
     else
@@ -1095,6 +1121,34 @@ int nnx_conv3d_split(const float* d_x1, int c1, const float* d_x2, int c2, const
     require(cout >= 1, "convolution needs at least one output channel");
     const ConvGeom g = make_conv_geom(batch, in_size, ksize, stride);
     conv3d_x3(d_x1, c1, d_x2, c2, d_packed, scale, d_bias, d_y, g, cout, as_stream(stream));
+  });
+}
+
+float nnx_winograd_weight_scale(float max_abs) {
+  if (!std::isfinite(max_abs) || max_abs < 0.f) return 0.f;
+  return wino_weight_scale(max_abs);
+}
+
+size_t nnx_conv3d_winograd_packed_bytes(int cout, int c1, int c2) {
+  if (cout < 1 || c1 < 1 || c2 < 0) return 0;
+  return (size_t)conv_wino_packed_bytes(cout, c1, c2);
+}
+
+int nnx_conv3d_winograd_pack_weight(const float* d_weight, int cout, int c1, int c2, float scale,
+                                    void* d_packed, void* stream) {
+  return guarded([&] {
+    conv_wino_pack_weight(d_weight, cout, c1, c2, scale, d_packed, as_stream(stream));
+  });
+}
+
+int nnx_conv3d_winograd(const float* d_x1, int c1, const float* d_x2, int c2, const void* d_packed,
+                        float scale, const float* d_bias, float* d_y, int batch,
+                        const int* in_size, int cout, void* stream) {
+  return guarded([&] {
+    require(in_size != nullptr, "null argument");
+    const int k3[3] = {3, 3, 3}, s1[3] = {1, 1, 1};
+    const ConvGeom g = make_conv_geom(batch, in_size, k3, s1);
+    conv3d_wino(d_x1, c1, d_x2, c2, d_packed, scale, d_bias, d_y, g, cout, as_stream(stream));
   });
 }
 

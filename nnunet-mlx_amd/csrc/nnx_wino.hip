@@ -1,0 +1,621 @@
+// Winograd F(2x2x2, 3x3x3) convolution for the stride-1, padding-1 3x3x3 layers, with
+// split-fp16 products (hi*hi + hi*lo + lo*hi, float32 accumulation) on
+// v_mfma_f32_32x32x16_f16.
+//
+// A 2x2x2 output tile is Y = A^T [ U (.) V ] A along each axis, with V = B^T d B the
+// transform of the tile's 4x4x4 input patch and U = G w G^T the transform of the 3x3x3
+// filter (F(2,3): B^T = [1 0 -1 0; 0 1 1 0; 0 -1 1 0; 0 1 0 -1], G = [1 0 0; .5 .5 .5;
+// .5 -.5 .5; 0 0 1], A^T = [1 1 1 0; 0 1 -1 -1]).  Summed over input channels, each of the
+// 64 transform positions xi = (xz, xy, xx) is an independent GEMM M[xi] = V[xi] U[xi]
+// (tiles x C_in times C_in x C_out): 64 products per 8 outputs instead of 216, so the
+// three split products cost fewer MFMA operations than one product of the direct
+// convolution.  The transforms are exact additions/subtractions of float32 values (and
+// the 1/2 of G, exact), so the arithmetic stays float32-class; U is formed in float64 and
+// rounded once, V in float32, each then split into fp16 halves.
+//
+// Workgroup: 4 waves, an output box of 4 x 8 x 8 voxels (2 x 4 x 4 tiles, the 32 MFMA rows)
+// of one batch item, and 32 output channels (the 32 MFMA columns).  Wave w owns the 16
+// transform positions xz = w, xy = 0..3, xx = 0..3: its accumulators are 16 blocks of
+// 32 x 32 floats (256 registers a lane, one wave a SIMD).  Per chunk of 16 input channels:
+//   1. the raw 6 x 10 x 10 input halo was fetched by global_load_lds_dwordx4 into one of two
+//      LDS buffers (issued during the previous chunk's products);
+//   2. 400 threads apply the pending InstanceNorm (+ LeakyReLU) of the input to in-volume
+//      voxels and write the z-transform (4 xz x 2 tile rows of z) as 8 padded planes, laid
+//      out so that the 32 tiles of a half-wave read 32 different 16-byte bank groups;
+//   3. each wave reads the four z-transformed rows of its tile patch once, forms V for its
+//      positions (y- then x-transform), splits it into fp16 halves in registers and issues
+//      three MFMAs per position against the packed U of this chunk, read from L2 eight
+//      positions ahead; the next chunk's halo DMA is issued right after this chunk's LDS
+//      reads, and the first half's products cover its latency.
+// Epilogue: each wave applies the x- and y-output transforms to its accumulators, the four
+// partials are combined through LDS (z-output transform), scaled back, + bias, written to
+// an LDS tile for the InstanceNorm partials of the box and stored as 16-byte channel runs.
+#include <cmath>
+#include <cstdlib>
+#include <string>
+#include <type_traits>
+
+#include "nnx_internal.h"
+
+namespace nnx {
+namespace {
+
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f16v __attribute__((ext_vector_type(16)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+
+constexpr int kWThreads = 256;                    // 4 waves
+constexpr int kWChunk = 16;                       // input channels per chunk (one MFMA K)
+constexpr int kHaloVox = 6 * 10 * 10;             // input halo of a 4 x 8 x 8 output box
+constexpr int kRawLines = kHaloVox * 4;           // 16-byte lines (4 channels each)
+constexpr int kRawRounds = (kRawLines + kWThreads - 1) / kWThreads;
+constexpr int kRawSlots = kRawRounds * kWThreads;  // 16-byte slots per raw buffer
+constexpr int kZRow = 41;                          // slots per z-plane row: 10 voxels x 4 + 1
+constexpr int kZPlane = 411;                       // slots per plane: 10 rows + 1 slot
+constexpr int kZSlots = 8 * kZPlane;
+constexpr int kLdsSlots = 2 * kRawSlots + kZSlots;
+constexpr int kPartSlots = 4 * 32 * 32;            // epilogue: 4 waves x 32 tiles x 32 columns
+constexpr int kTileStride = 36;                    // floats per voxel row of the output tile
+static_assert(kPartSlots <= kLdsSlots, "epilogue partials must fit the main-loop LDS");
+static_assert(256 * kTileStride / 4 + kWThreads / 4 <= kLdsSlots, "output tile fits");
+
+struct WinoArgs {
+  const float* x0;
+  const float* x1;
+  int c0, c1, chunks0, chunks;
+  const uint4* u;  // packed transformed weights
+  const float* bias;
+  float* y;
+  int D, H, W;
+  int cout, ntn;
+  int nbz, nby, nbx;
+  int nwg;
+  float out_scale;
+  float4* stats;
+  const float4* nrm0;
+  const float4* nrm1;
+  int act0, act1;
+  float slope;
+};
+
+// 16 zero bytes: halo lines outside the volume are fetched from here.
+__device__ __align__(16) float g_wino_zero[4];
+
+__device__ __forceinline__ f16v mfma32(h8 a, h8 b, f16v c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// hi = fp16(v) (nearest even), lo = fp16(v - hi).  v - hi is exact in float32, so the
+// single rounding of v_fma_mix{lo,hi}_f16 (fma(-hi, 1, v) formed exactly, rounded once to
+// fp16) gives the same lo as converting hi back, subtracting and converting: one
+// instruction per element instead of three.
+__device__ __forceinline__ void split8(const float (&v)[8], h8& hi, h8& lo) {
+#pragma unroll
+  for (int q = 0; q < 8; q += 2) {
+    const h2 h = __builtin_convertvector((f2{v[q], v[q + 1]}), h2);
+    h2 l;
+    asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(l) : "v"(h), "v"(v[q]));
+    asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+        : "+v"(l) : "v"(h), "v"(v[q + 1]));
+    hi[q] = h[0];
+    hi[q + 1] = h[1];
+    lo[q] = l[0];
+    lo[q + 1] = l[1];
+  }
+}
+
+// The InstanceNorm apply pass's operations: r = fma(x - mean, scale, beta), then
+// max(s * r, r) with s = the LeakyReLU slope under the activation and s = 1 (the identity,
+// exactly) without it.
+__device__ __forceinline__ f4 wino_norm(f4 v, const float4 (&p)[4], float s) {
+  f4 r;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float t = fmaf(v[q] - p[q].x, p[q].y, p[q].z);
+    r[q] = fmaxf(s * t, t);
+  }
+  return r;
+}
+
+__global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
+  extern __shared__ __align__(16) f4 lds[];
+  f4* const zp = lds + 2 * kRawSlots;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int logical = xcd_remap(blockIdx.x, a.nwg);
+  const int nt = logical % a.ntn;
+  int box = logical / a.ntn;
+  const int bxi = box % a.nbx;
+  box /= a.nbx;
+  const int byi = box % a.nby;
+  box /= a.nby;
+  const int bzi = box % a.nbz;
+  const int b = box / a.nbz;
+  const int oz0 = bzi * 4, oy0 = byi * 8, ox0 = bxi * 8;
+  const int iz0 = oz0 - 1, iy0 = oy0 - 1, ix0 = ox0 - 1;
+  const int64_t bvox = (int64_t)b * a.D * a.H * a.W;
+
+  // ---- raw halo fetch of one chunk into buffer `buf` (LDS slot = line = voxel * 4 + quad);
+  // this thread's lines r * 512 + tid have fixed voxels: their offsets inside the batch
+  // item (-1 outside the volume or past the halo) are computed once
+  const int cq_line = tid & 3;
+  int vofs[kRawRounds];
+#pragma unroll
+  for (int r = 0; r < kRawRounds; ++r) {
+    const int line = r * kWThreads + tid;
+    int o = -1;
+    if (line < kRawLines) {
+      const int v = line >> 2;
+      const int hz = v / 100, rem = v - hz * 100;
+      const int hy = rem / 10, hx = rem - hy * 10;
+      const int z = iz0 + hz, yy = iy0 + hy, xx = ix0 + hx;
+      if ((unsigned)z < (unsigned)a.D && (unsigned)yy < (unsigned)a.H &&
+          (unsigned)xx < (unsigned)a.W)
+        o = (z * a.H + yy) * a.W + xx;
+    }
+    vofs[r] = o;
+  }
+  auto fetch = [&](int chunk, int buf) __attribute__((always_inline)) {
+    const bool first = chunk < a.chunks0;
+    const float* src = first ? a.x0 : a.x1;
+    const int C = first ? a.c0 : a.c1;
+    const float* base = src + bvox * C + (first ? chunk : chunk - a.chunks0) * kWChunk + cq_line * 4;
+    f4* dst = lds + buf * kRawSlots + wave * 64;
+#pragma unroll
+    for (int r = 0; r < kRawRounds; ++r) {
+      // both addresses formed and one selected: no branch around the load, so the
+      // compiler's wait counts stay exact
+      const float* in = base + (int64_t)(vofs[r] < 0 ? 0 : vofs[r]) * C;
+      const float* g = vofs[r] >= 0 ? in : g_wino_zero;
+      __builtin_amdgcn_global_load_lds(
+          g, (__attribute__((address_space(3))) void*)(dst + r * kWThreads), 16, 0, 0);
+    }
+  };
+
+  // ---- pending InstanceNorm parameters of every input channel (both inputs, in chunk
+  // order) for this batch item, kept in LDS after the main buffers
+  f4* const prm = lds + kLdsSlots;
+  for (int c = tid; c < a.c0 + a.c1; c += kWThreads) {
+    const float4* p = c < a.c0 ? a.nrm0 : a.nrm1;
+    const int C = c < a.c0 ? a.c0 : a.c1;
+    const int cc = c < a.c0 ? c : c - a.c0;
+    float4 v = make_float4(0.f, 1.f, 0.f, 0.f);
+    if (p) v = p[(int64_t)b * C + cc];
+    prm[c] = f4{v.x, v.y, v.z, 0.f};
+  }
+
+  // ---- pending norm + z-transform: thread (hy, hx, quad) of the 10 x 10 x 4 columns.  A
+  // halo wholly inside the volume (uniform over the workgroup) needs no padding selects.
+  const bool interior = iz0 >= 0 && iz0 + 6 <= a.D && iy0 >= 0 && iy0 + 10 <= a.H &&
+                        ix0 >= 0 && ix0 + 10 <= a.W;
+  auto transform_column = [&](auto inner, int chunk, int buf, int col) __attribute__((always_inline)) {
+    const int hy = col / 40, rem = col - hy * 40;
+    const int hx = rem >> 2, cq = rem & 3;
+    const bool first = chunk < a.chunks0;
+    const float s = (first ? a.act0 : a.act1) != 0 ? a.slope : 1.f;
+    // parameters of inputs without a pending norm are (0, 1, 0): the identity
+    float4 pm[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const f4 v = prm[chunk * kWChunk + cq * 4 + q];
+      pm[q] = make_float4(v[0], v[1], v[2], 0.f);
+    }
+    const f4* raw = lds + buf * kRawSlots + (hy * 10 + hx) * 4 + cq;
+    f4 d[6];
+#pragma unroll
+    for (int hz = 0; hz < 6; ++hz) d[hz] = raw[hz * 400];
+    if constexpr (decltype(inner)::value) {
+#pragma unroll
+      for (int hz = 0; hz < 6; ++hz) d[hz] = wino_norm(d[hz], pm, s);
+    } else {
+      const bool inyx =
+          (unsigned)(iy0 + hy) < (unsigned)a.H && (unsigned)(ix0 + hx) < (unsigned)a.W;
+#pragma unroll
+      for (int hz = 0; hz < 6; ++hz) {
+        // the padding stays zero; in-volume voxels take the pending norm
+        const f4 t = wino_norm(d[hz], pm, s);
+        const bool inside = inyx && (unsigned)(iz0 + hz) < (unsigned)a.D;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) d[hz][e] = inside ? t[e] : 0.f;
+      }
+    }
+    f4* dst = zp + hy * kZRow + hx * 4 + cq;
+#pragma unroll
+    for (int tz = 0; tz < 2; ++tz) {
+      const f4 d0 = d[2 * tz], d1 = d[2 * tz + 1], d2 = d[2 * tz + 2], d3 = d[2 * tz + 3];
+      dst[(0 * 2 + tz) * kZPlane] = d0 - d2;
+      dst[(1 * 2 + tz) * kZPlane] = d1 + d2;
+      dst[(2 * 2 + tz) * kZPlane] = d2 - d1;
+      dst[(3 * 2 + tz) * kZPlane] = d1 - d3;
+    }
+  };
+  auto transform = [&](int chunk, int buf) __attribute__((always_inline)) {
+    if (interior) {
+      transform_column(std::true_type{}, chunk, buf, tid);
+      if (tid + kWThreads < 400) transform_column(std::true_type{}, chunk, buf, tid + kWThreads);
+    } else {
+      transform_column(std::false_type{}, chunk, buf, tid);
+      if (tid + kWThreads < 400) transform_column(std::false_type{}, chunk, buf, tid + kWThreads);
+    }
+  };
+
+  // ---- this lane's tile, channel half and transform positions
+  const int xz = wave;
+  const int t = lane & 31, tzl = t >> 4, tyl = (t >> 2) & 3, txl = t & 3, g8 = lane >> 5;
+  const f4* zb = zp + (xz * 2 + tzl) * kZPlane + (2 * tyl) * kZRow + (2 * txl) * 4 + 2 * g8;
+
+  // packed U: [nt][chunk][xi = (xz * 4 + xy) * 4 + xx][hi | lo][64 lanes] x 16 bytes; step
+  // s = xy * 4 + xx of a chunk uses position xi = xz * 16 + s
+  const uint4* ub = a.u + ((int64_t)nt * a.chunks * 64 + xz * 16) * 128 + lane;
+  auto uaddr = [&](int chunk, int step) { return ub + ((int64_t)chunk * 64 + step) * 128; };
+
+  f16v acc[4][4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int x = 0; x < 4; ++x)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[j][x][r] = 0.f;
+
+  constexpr int kRing = 8;  // B operands of eight steps in flight
+  uint4 uh[kRing], ul[kRing];
+  fetch(0, 0);
+#pragma unroll
+  for (int s = 0; s < kRing; ++s) {
+    const uint4* p = uaddr(0, s);
+    uh[s] = p[0];
+    ul[s] = p[64];
+  }
+
+  // the three products of step s (position xy = s / 4, xx = s % 4) for two steps at a
+  // time, then the refill of their ring slots eight steps ahead
+  auto products = [&](int s0, const float (&q)[4][8], int chunk) __attribute__((always_inline)) {
+    h8 ah[2], al[2];
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int xx = (s0 + k) & 3;
+      float v[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if (xx == 0) v[e] = q[0][e] - q[2][e];
+        else if (xx == 1) v[e] = q[1][e] + q[2][e];
+        else if (xx == 2) v[e] = q[2][e] - q[1][e];
+        else v[e] = q[1][e] - q[3][e];
+      }
+      split8(v, ah[k], al[k]);
+    }
+    const int xy = s0 >> 2, x0 = s0 & 3;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      acc[xy][x0 + k] = mfma32(ah[k], *reinterpret_cast<const h8*>(&uh[(s0 + k) % kRing]),
+                               acc[xy][x0 + k]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      acc[xy][x0 + k] = mfma32(ah[k], *reinterpret_cast<const h8*>(&ul[(s0 + k) % kRing]),
+                               acc[xy][x0 + k]);
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const int s = s0 + k, slot = s % kRing;
+      acc[xy][x0 + k] = mfma32(al[k], *reinterpret_cast<const h8*>(&uh[slot]), acc[xy][x0 + k]);
+      // unconditional (past the last chunk the last chunk's words are read again)
+      const int ns = s + kRing;
+      int nchunk = ns < 16 ? chunk : chunk + 1;
+      nchunk = nchunk < a.chunks ? nchunk : a.chunks - 1;
+      const uint4* p = uaddr(nchunk, ns & 15);
+      uh[slot] = p[0];
+      ul[slot] = p[64];
+    }
+  };
+
+  for (int chunk = 0; chunk < a.chunks; ++chunk) {
+    const int buf = chunk & 1;
+    __builtin_amdgcn_s_waitcnt(0);  // this thread's halo lines and B operands have landed
+    __syncthreads();                 // every thread's; the z-planes are free
+    transform(chunk, buf);
+    __syncthreads();                 // z-planes written; the raw buffer `buf` is free
+    // the four z-transformed rows of the tile patch, y-transformed: Q[xy][column][channel]
+    float q[4][4][8];
+    {
+      f4 rows[4][4][2];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+          const f4* p = zb + r * kZRow + c * 4;
+          rows[r][c][0] = p[0];
+          rows[r][c][1] = p[1];
+        }
+#pragma unroll
+      for (int c = 0; c < 4; ++c)
+#pragma unroll
+        for (int h = 0; h < 2; ++h)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float r0 = rows[0][c][h][e], r1 = rows[1][c][h][e];
+            const float r2 = rows[2][c][h][e], r3 = rows[3][c][h][e];
+            q[0][c][4 * h + e] = r0 - r2;
+            q[1][c][4 * h + e] = r1 + r2;
+            q[2][c][4 * h + e] = r2 - r1;
+            q[3][c][4 * h + e] = r1 - r3;
+          }
+    }
+    // the next chunk's halo, after this chunk's last LDS read; vector-memory loads
+    // complete in order, so the second-half operands requested below land after it: the
+    // first half's products cover its latency
+    if (chunk + 1 < a.chunks) fetch(chunk + 1, buf ^ 1);
+#pragma unroll
+    for (int s0 = 0; s0 < 16; s0 += 2) products(s0, q[s0 >> 2], chunk);
+  }
+
+  // ---- epilogue
+  // x- and y-output transforms of this wave's 16 positions: per accumulator element, the
+  // (oy, ox) outputs of its tile row for this xz
+  __syncthreads();  // every wave is past its last z-plane read
+  f4* part = lds;   // [wave][tile][column] x (oy0ox0, oy0ox1, oy1ox0, oy1ox1)
+  const int col = lane & 31;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float xo[4][2];  // [xy][ox]
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const float m0 = acc[j][0][r], m1 = acc[j][1][r], m2 = acc[j][2][r], m3 = acc[j][3][r];
+      xo[j][0] = (m0 + m1) + m2;
+      xo[j][1] = (m1 - m2) - m3;
+    }
+    const f4 pv = {(xo[0][0] + xo[1][0]) + xo[2][0], (xo[0][1] + xo[1][1]) + xo[2][1],
+                   (xo[1][0] - xo[2][0]) - xo[3][0], (xo[1][1] - xo[2][1]) - xo[3][1]};
+    const int tile = 8 * (r >> 2) + 4 * g8 + (r & 3);
+    part[(wave * 32 + tile) * 32 + col] = pv;
+  }
+  __syncthreads();
+  // z-output transform over the four partials: oz0 = P0 + P1 + P2, oz1 = P1 - P2 - P3; then
+  // the weight scale and the bias
+  constexpr int kPairs = 32 * 32 / kWThreads;
+  f4 yo[kPairs][2];  // [pair][oz]
+  const float bias_c = a.bias ? a.bias[nt * 32 + (tid & 31)] : 0.f;
+#pragma unroll
+  for (int k = 0; k < kPairs; ++k) {
+    const int idx = tid + k * kWThreads;
+    const int tile = idx >> 5, c = idx & 31;
+    f4 pz[4];
+#pragma unroll
+    for (int z = 0; z < 4; ++z) pz[z] = part[(z * 32 + tile) * 32 + c];
+    const f4 y0 = (pz[0] + pz[1]) + pz[2];
+    const f4 y1 = (pz[1] - pz[2]) - pz[3];
+    yo[k][0] = y0 * a.out_scale;
+    yo[k][1] = y1 * a.out_scale;
+    if (a.bias) {
+      yo[k][0] = yo[k][0] + bias_c;
+      yo[k][1] = yo[k][1] + bias_c;
+    }
+  }
+  __syncthreads();
+  float* otile = reinterpret_cast<float*>(lds);  // [box voxel (z, y, x)][column], stride 36
+#pragma unroll
+  for (int k = 0; k < kPairs; ++k) {
+    const int idx = tid + k * kWThreads;
+    const int tile = idx >> 5, c = idx & 31;
+    const int tz = tile >> 4, ty = (tile >> 2) & 3, tx = tile & 3;
+#pragma unroll
+    for (int oz = 0; oz < 2; ++oz)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int oy = e >> 1, ox = e & 1;
+        const int v = ((2 * tz + oz) * 8 + 2 * ty + oy) * 8 + 2 * tx + ox;
+        otile[v * kTileStride + c] = yo[k][oz][e];
+      }
+  }
+  __syncthreads();
+  // a box wholly inside the volume (uniform over the workgroup) skips the voxel checks
+  const bool full = oz0 + 4 <= a.D && oy0 + 8 <= a.H && ox0 + 8 <= a.W;
+  auto valid = [&](int v) {
+    return oz0 + (v >> 6) < a.D && oy0 + ((v >> 3) & 7) < a.H && ox0 + (v & 7) < a.W;
+  };
+  // InstanceNorm partials of the box per column: mean over the valid voxels, then the
+  // centred sum of squares (thread = column c, part p of 8)
+  auto box_stats = [&](auto all) __attribute__((always_inline)) {
+    constexpr bool kAll = decltype(all)::value;
+    constexpr int kParts = kWThreads / 32;
+    float* red = otile + 256 * kTileStride;  // kWThreads floats
+    const int c = tid & 31, pidx = tid >> 5;
+    const int nz = min(4, a.D - oz0), ny = min(8, a.H - oy0), nx = min(8, a.W - ox0);
+    const float cnt = (float)(nz * ny * nx);
+    float s = 0.f;
+#pragma unroll 8
+    for (int v = pidx; v < 256; v += kParts)
+      if (kAll || valid(v)) s += otile[v * kTileStride + c];
+    red[tid] = s;
+    __syncthreads();
+    float mean = 0.f;
+#pragma unroll
+    for (int k = 0; k < kParts; ++k) mean += red[k * 32 + c];
+    mean = mean / cnt;
+    __syncthreads();
+    float m2 = 0.f;
+#pragma unroll 8
+    for (int v = pidx; v < 256; v += kParts)
+      if (kAll || valid(v)) {
+        const float d = otile[v * kTileStride + c] - mean;
+        m2 = fmaf(d, d, m2);
+      }
+    red[tid] = m2;
+    __syncthreads();
+    if (pidx == 0) {
+      float tot = 0.f;
+#pragma unroll
+      for (int k = 0; k < kParts; ++k) tot += red[k * 32 + c];
+      const int tiles = a.nbz * a.nby * a.nbx;
+      const int tile_s = (bzi * a.nby + byi) * a.nbx + bxi;
+      a.stats[((int64_t)b * tiles + tile_s) * a.cout + nt * 32 + c] = make_float4(mean, tot, cnt, 0.f);
+    }
+  };
+  if (a.stats) {
+    if (full)
+      box_stats(std::true_type{});
+    else
+      box_stats(std::false_type{});
+  }
+  // stores: 256 voxels x 8 runs of 4 channels
+#pragma unroll
+  for (int k = 0; k < 256 * 8 / kWThreads; ++k) {
+    const int idx = tid + k * kWThreads;
+    const int v = idx >> 3, qd = idx & 7;
+    if (full || valid(v)) {
+      const int z = oz0 + (v >> 6), yy = oy0 + ((v >> 3) & 7), xx = ox0 + (v & 7);
+      const float* src = otile + v * kTileStride + 4 * qd;
+      *reinterpret_cast<f4*>(a.y + (bvox + ((int64_t)z * a.H + yy) * a.W + xx) * a.cout +
+                             nt * 32 + 4 * qd) = f4{src[0], src[1], src[2], src[3]};
+    }
+  }
+}
+
+// U[cout][cin][xi] = sum_{a,b,e} G[xz][a] G[xy][b] G[xx][e] w[cout][a][b][e][cin] in float64,
+// times `scale`, rounded to float32, split into fp16 halves.  Word layout:
+// packed[(((nt * chunks + chunk) * 64 + xi) * 2 + part) * 64 + lane], lane = column
+// (cout = nt * 32 + lane % 32) and k slot (cin = chunk channel 8 * (lane / 32) + q).
+__global__ void pack_wino_weight_kernel(const float* __restrict__ w, uint4* __restrict__ out,
+                                        int cout, int c1, int c2, int chunks0, int chunks,
+                                        int ntn, float scale) {
+  const double G[4][3] = {{1.0, 0.0, 0.0}, {0.5, 0.5, 0.5}, {0.5, -0.5, 0.5}, {0.0, 0.0, 1.0}};
+  const int cin_total = c1 + c2;
+  const int64_t total = (int64_t)ntn * chunks * 64 * 64;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int lane = (int)(i & 63);
+    int64_t rest = i >> 6;
+    const int xi = (int)(rest % 64);
+    rest /= 64;
+    const int chunk = (int)(rest % chunks);
+    const int nt = (int)(rest / chunks);
+    const int xz = xi >> 4, xy = (xi >> 2) & 3, xx = xi & 3;
+    const int n = nt * 32 + (lane & 31);
+    h8 hv, lv;
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int k = 8 * (lane >> 5) + q;
+      int wc = -1;
+      if (chunk < chunks0) {
+        const int cc = chunk * kWChunk + k;
+        if (cc < c1) wc = cc;
+      } else {
+        const int cc = (chunk - chunks0) * kWChunk + k;
+        if (cc < c2) wc = c1 + cc;
+      }
+      float v = 0.f;
+      if (n < cout && wc >= 0) {
+        double u = 0.0;
+        for (int az = 0; az < 3; ++az)
+          for (int ay = 0; ay < 3; ++ay)
+            for (int ax = 0; ax < 3; ++ax) {
+              const double gw = G[xz][az] * G[xy][ay] * G[xx][ax];
+              if (gw != 0.0)
+                u += gw * (double)w[(((int64_t)n * 3 + az) * 3 + ay) * 3 * cin_total +
+                                    (int64_t)ax * cin_total + wc];
+            }
+        v = (float)(u * (double)scale);
+      }
+      const _Float16 h = (_Float16)v;
+      hv[q] = h;
+      lv[q] = (_Float16)(v - (float)h);
+    }
+    const int64_t word = ((((int64_t)nt * chunks + chunk) * 64 + xi) * 2) * 64 + lane;
+    out[word] = *reinterpret_cast<const uint4*>(&hv);
+    out[word + 64] = *reinterpret_cast<const uint4*>(&lv);
+  }
+}
+
+}  // namespace
+
+bool conv_wino_supported(const ConvGeom& g, int c1, int c2, int cout) {
+  for (int i = 0; i < 3; ++i)
+    if (g.k[i] != 3 || g.s[i] != 1) return false;
+  return cout % 32 == 0 && c1 % kWChunk == 0 && c2 % kWChunk == 0 && c1 > 0;
+}
+
+int conv_wino_stats_tiles(const ConvGeom& g) {
+  return (int)(ceil_div(g.out[0], 4) * ceil_div(g.out[1], 8) * ceil_div(g.out[2], 8));
+}
+
+float wino_weight_scale(float max_abs) {
+  // |U| <= (1.5)^3 max |w|: the scale keeps every split high half below 2^15
+  return split_weight_scale(3.375f * max_abs);
+}
+
+int64_t conv_wino_packed_bytes(int cout, int c1, int c2) {
+  const int64_t chunks = ceil_div(c1, kWChunk) + ceil_div(c2, kWChunk);
+  return ceil_div(cout, 32) * chunks * 64 * 2 * 64 * 16;
+}
+
+void conv_wino_pack_weight(const float* d_w, int cout, int c1, int c2, float scale,
+                           void* d_packed, hipStream_t st) {
+  require(d_w && d_packed, "Winograd packing pointers must not be null");
+  require(cout >= 1 && c1 >= 1 && c2 >= 0, "invalid Winograd convolution channel counts");
+  require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+  const int chunks0 = (int)ceil_div(c1, kWChunk);
+  const int chunks = chunks0 + (int)ceil_div(c2, kWChunk);
+  const int ntn = (int)ceil_div(cout, 32);
+  const int64_t total = (int64_t)ntn * chunks * 64 * 64;
+  const int blocks = (int)std::min<int64_t>(ceil_div(total, 256), 65536);
+  hipLaunchKernelGGL(pack_wino_weight_kernel, dim3(blocks), dim3(256), 0, st, d_w,
+                     reinterpret_cast<uint4*>(d_packed), cout, c1, c2, chunks0, chunks, ntn,
+                     scale);
+  launch_check("conv3d_winograd_pack_weight");
+}
+
+void conv3d_wino(const float* x1, int c1, const float* x2, int c2, const void* packed,
+                 float scale, const float* bias, float* y, const ConvGeom& g, int cout,
+                 hipStream_t st, float4* stats, const PendingNorm& n1, const PendingNorm& n2) {
+  require(x1 && y && packed, "convolution pointers must not be null");
+  require(c2 == 0 || x2, "invalid convolution inputs");
+  require(conv_wino_supported(g, c1, c2, cout),
+          "the Winograd convolution takes stride-1 3x3x3 layers with C_out % 32 == 0 and input "
+          "channel counts that are multiples of 16");
+  require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
+  require(!(n1.params && n2.params) || n1.slope == n2.slope,
+          "pending normalisations of one convolution must share the LeakyReLU slope");
+  require(reinterpret_cast<uintptr_t>(y) % 16 == 0 && reinterpret_cast<uintptr_t>(x1) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(x2) % 16 == 0,
+          "Winograd convolution tensors must be 16-byte aligned");
+  WinoArgs a{};
+  a.x0 = x1;
+  a.x1 = x2;
+  a.c0 = c1;
+  a.c1 = c2;
+  a.chunks0 = c1 / kWChunk;
+  a.chunks = a.chunks0 + c2 / kWChunk;
+  a.u = reinterpret_cast<const uint4*>(packed);
+  a.bias = bias;
+  a.y = y;
+  a.D = g.in[0];
+  a.H = g.in[1];
+  a.W = g.in[2];
+  a.cout = cout;
+  a.ntn = cout / 32;
+  a.nbz = (int)ceil_div(g.out[0], 4);
+  a.nby = (int)ceil_div(g.out[1], 8);
+  a.nbx = (int)ceil_div(g.out[2], 8);
+  const int64_t nwg = (int64_t)g.batch * a.nbz * a.nby * a.nbx * a.ntn;
+  require(nwg < (1LL << 31), "convolution grid too large");
+  a.nwg = (int)nwg;
+  a.out_scale = 1.0f / scale;
+  a.stats = stats;
+  a.nrm0 = n1.params;
+  a.nrm1 = n2.params;
+  a.act0 = n1.act ? 1 : 0;
+  a.act1 = n2.act ? 1 : 0;
+  a.slope = n1.params ? n1.slope : n2.slope;
+  const double out_vox = (double)g.batch * g.out[0] * g.out[1] * g.out[2];
+  const double flops = 2.0 * (c1 + c2) * cout * 27.0 * out_vox;
+  const double bytes = 4.0 * ((double)g.batch * g.in[0] * g.in[1] * g.in[2] * (c1 + c2) +
+                              out_vox * cout);
+  ProfScope prof("conv3d_wino", flops, bytes, st);
+  const size_t lds_bytes = ((size_t)kLdsSlots + c1 + c2) * 16;
+  require(lds_bytes <= 160 * 1024, "too many input channels for the Winograd convolution");
+  hipLaunchKernelGGL(wino_x3_kernel, dim3(a.nwg), dim3(kWThreads), lds_bytes, st, a);
+  launch_check("conv3d_winograd");
+}
+
+}  // namespace nnx

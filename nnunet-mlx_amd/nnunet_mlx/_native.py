@@ -151,6 +151,17 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p,
          ctypes.c_int, c_int_p, ctypes.c_int, c_int_p, c_int_p, c_void_p],
     ),
+    "nnx_winograd_weight_scale": (ctypes.c_float, [ctypes.c_float]),
+    "nnx_conv3d_winograd_packed_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int, ctypes.c_int]),
+    "nnx_conv3d_winograd_pack_weight": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_float, c_void_p, c_void_p],
+    ),
+    "nnx_conv3d_winograd": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, c_void_p, ctypes.c_int, c_void_p, ctypes.c_float, c_void_p, c_void_p,
+         ctypes.c_int, c_int_p, ctypes.c_int, c_void_p],
+    ),
     "nnx_conv3d_direct_small_cin": (
         ctypes.c_int, [c_void_p, c_void_p, c_void_p, c_void_p, ctypes.c_int, c_int_p, ctypes.c_int, c_void_p]
     ),

@@ -124,6 +124,77 @@ def test_conv3d_split_matches_float64(lib, case):
     assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
 
 
+WINOGRAD_CASES = [
+    # batch, in_size, c1, c2, cout
+    (2, (16, 16, 16), 32, 0, 32),
+    (1, (17, 9, 20), 32, 0, 32),     # ragged: partial 4 x 8 x 8 boxes on every axis
+    (2, (16, 16, 16), 32, 32, 32),   # concat-free decoder input
+    (1, (12, 12, 12), 64, 0, 64),
+    (2, (8, 8, 8), 128, 0, 128),
+    (1, (24, 24, 32), 64, 0, 128),
+    (1, (4, 4, 4), 320, 320, 320),
+    (1, (5, 7, 6), 16, 16, 32),      # smaller than one box
+    (3, (9, 13, 11), 48, 16, 96),
+]
+
+
+@pytest.mark.parametrize("case", WINOGRAD_CASES, ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}")
+def test_conv3d_winograd_matches_float64(lib, case):
+    """Winograd F(2x2x2, 3x3x3) with split-fp16 products holds the float32 bar of the
+    direct kernels against float64 (activations up to ~30, weights spanning three decades)."""
+    batch, size, c1, c2, cout = case
+    print(f"winograd conv case {case}", flush=True)
+    rng = np.random.default_rng((hash(case) + 11) % 2**32)
+    x1 = (rng.standard_normal((batch, *size, c1)) * rng.uniform(0.5, 8.0)).astype(np.float32)
+    x2 = rng.standard_normal((batch, *size, c2)).astype(np.float32) if c2 else None
+    w = (rng.standard_normal((cout, 3, 3, 3, c1 + c2)) / np.sqrt((c1 + c2) * 27)).astype(np.float32)
+    w.reshape(-1)[:: 7] *= 1e-3
+    bias = rng.standard_normal(cout).astype(np.float32)
+    scale = lib.nnx_winograd_weight_scale(float(np.abs(w).max()))
+    assert scale > 0 and np.log2(scale) == int(np.log2(scale))
+    packed = torch.empty(lib.nnx_conv3d_winograd_packed_bytes(cout, c1, c2), dtype=torch.uint8,
+                         device="cuda")
+    dw = dev(w)
+    _native.check(lib.nnx_conv3d_winograd_pack_weight(dw.data_ptr(), cout, c1, c2, scale,
+                                                      packed.data_ptr(), stream()))
+    dx1, db = dev(x1), dev(bias)
+    dx2 = dev(x2) if c2 else None
+    y = torch.full((batch, *size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    _native.check(lib.nnx_conv3d_winograd(
+        dx1.data_ptr(), c1, dx2.data_ptr() if c2 else None, c2, packed.data_ptr(), scale,
+        db.data_ptr(), y.data_ptr(), batch, _native.ints(size), cout, stream()))
+    got = host(y)
+    full = np.concatenate([x1, x2], axis=-1) if c2 else x1
+    ref = _conv_ref64(full, w, (1, 1, 1)) + bias.astype(np.float64)
+    msg = report("winograd conv", got, ref)
+    print(msg, flush=True)
+    assert np.isfinite(got).all(), msg
+    assert rel_l2(got, ref) <= 1e-5, msg
+    assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
+
+
+def test_conv3d_winograd_rejects_unsupported_layers(lib):
+    """Channel counts off the 16 / 32 grid, a second input off the grid and a bad weight
+    scale are refused before any launch, with valid buffers so that the layer check (not a
+    null pointer) is what refuses; the output keeps its contents."""
+    x = torch.zeros((1, 8, 8, 8, 64), dtype=torch.float32, device="cuda")
+    packed = torch.zeros(lib.nnx_conv3d_winograd_packed_bytes(64, 64, 64), dtype=torch.uint8,
+                         device="cuda")
+    y = torch.full((1, 8, 8, 8, 64), 7.0, dtype=torch.float32, device="cuda")
+    size = _native.ints((8, 8, 8))
+    for c1, c2, cout, scale, needle in [(12, 0, 32, 1.0, "multiples of 16"),
+                                        (32, 0, 24, 1.0, "multiples of 16"),
+                                        (32, 8, 32, 1.0, "multiples of 16"),
+                                        (32, 0, 32, 0.0, "scale")]:
+        rc = lib.nnx_conv3d_winograd(x.data_ptr(), c1, x.data_ptr() if c2 else None, c2,
+                                     packed.data_ptr(), scale, None, y.data_ptr(), 1, size, cout,
+                                     stream())
+        assert rc == _native.NNX_ERR_INVALID, (c1, c2, cout)
+        assert needle in _native.last_error(), _native.last_error()
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
+
+
 @pytest.mark.parametrize("size,cout", [((16, 16, 16), 32), ((5, 7, 9), 8)])
 def test_direct_single_channel_conv(lib, size, cout):
     print(f"direct conv {size} {cout}", flush=True)

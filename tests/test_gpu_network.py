@@ -104,6 +104,35 @@ def test_forward_matches_oracle(device, name):
         net.close()
 
 
+@pytest.mark.parametrize("name", ["liver-32", "brats-4ch", "autopet-aniso", "tiny-residual"])
+def test_winograd_route_matches_oracle(device, monkeypatch, name):
+    """NNX_CONV_ALGO=winograd (read when the weights are packed) sends the stride-1 3x3x3
+    split layers with 16-channel input blocks and C_out % 32 == 0 to the Winograd kernel;
+    the network then holds the same float32 bar.  The kernel profile shows the route was
+    taken (tiny-residual has no eligible layer: every layer stays direct)."""
+    from nnunet_mlx import _native
+
+    spec, patch, batch, affine = CASES[name]
+    weights = random_weights(spec, seed=3, random_affine=affine)
+    x = np.random.default_rng(5).standard_normal((batch, *patch, spec.input_channels)).astype(np.float32)
+    residual = isinstance(spec, ResidualEncoderUNetSpec)
+    ref = OracleNetwork(spec, weights, residual=residual)(x)
+    monkeypatch.setenv("NNX_CONV_ALGO", "winograd")
+    print(f"winograd network case {name} patch={patch} batch={batch}", flush=True)
+    net = build_network(spec, precision="fp32-split")
+    net.load_weights(weights)
+    with _native.KernelProfile() as prof:
+        got = net(torch.from_numpy(x).to(device)).cpu().numpy()
+    net.close()
+    wino = prof.classes.get("conv3d_wino", {}).get("launches", 0)
+    assert (wino == 0) == (name == "tiny-residual"), prof.classes.keys()
+    msg = report(f"{name} winograd", got, ref)
+    print(msg, f"winograd launches {wino}", flush=True)
+    assert np.isfinite(got).all(), msg
+    assert np.abs(got - ref).max() <= 1e-3, msg
+    assert rel_l2(got, ref) <= 1e-5, msg
+
+
 def test_forward_rejects_bad_input(device):
     from nnunet_mlx.errors import ContractError
 
