@@ -203,6 +203,8 @@ def kernel_class_of(short: str) -> str | None:
     split-fp16 kernels igemm_x3s_kernel / igemm_x3_kernel -> conv3d_x3s_* / conv3d_x3_*)."""
     import re
 
+    if short.startswith("wino_x3_kernel"):
+        return "conv3d_wino"
     m = re.match(r"igemm(_x3s|_x3)?_kernel<(\d+), (\d+), (\d+), (\d+)([^>]*)>", short)
     if not m:
         return None
@@ -672,6 +674,11 @@ def main() -> int:
                 # issued fp16 MFMA work: 3 products per term, 4-tap groups (27 -> 28 taps)
                 entry["frac_fp16_mfma_issued"] = round(
                     entry["tflops"] * SPLIT_PRODUCTS * 28 / 27 / PEAK_FP16_MFMA_TFLOPS, 4)
+            elif name == "conv3d_wino":
+                # issued fp16 MFMA work: 3 products per term, 64 transform positions per 8
+                # outputs in place of 8 x 27 taps
+                entry["frac_fp16_mfma_issued"] = round(
+                    entry["tflops"] * SPLIT_PRODUCTS * 64 / 216 / PEAK_FP16_MFMA_TFLOPS, 4)
             else:
                 entry["frac_fp32_mfma"] = round(entry["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4)
         elif c["bytes"]:
@@ -684,11 +691,12 @@ def main() -> int:
         achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
         # the split kernel runs on fp16 MFMA: its algorithmic (float32-product) rate is
         # priced against the dense fp16 peak, the issued rate is reported beside it
-        peak = PEAK_FP16_MFMA_TFLOPS if dominant.startswith("conv3d_x3") else PEAK_FP32_MFMA_TFLOPS
+        fp16 = dominant.startswith(("conv3d_x3", "conv3d_wino"))
+        peak = PEAK_FP16_MFMA_TFLOPS if fp16 else PEAK_FP32_MFMA_TFLOPS
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 2),
                     "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
                     "traffic": measured_traffic(dominant)}
-        if dominant.startswith("conv3d_x3"):
+        if fp16:
             roofline["issued_frac"] = kernels[dominant].get(
                 "frac_bf16_mfma_issued", kernels[dominant].get("frac_fp16_mfma_issued"))
     else:
@@ -696,7 +704,7 @@ def main() -> int:
         roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
                     "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
                     "traffic": None}
-    conv = [c for n, c in classes.items() if n.startswith(("conv3d_igemm", "conv3d_x3"))]
+    conv = [c for n, c in classes.items() if n.startswith(("conv3d_igemm", "conv3d_x3", "conv3d_wino"))]
     conv_flops = sum(c["flops"] for c in conv)
     conv_ms = sum(c["ms"] for c in conv)
     # 3x3x3 convolution rate against the float32-class MFMA peak of the arithmetic used

@@ -350,14 +350,13 @@ bool uses_split_kernels(const nnx_model* m) {
 }
 
 // The Winograd form serves the fp32-split precision's stride-1 3x3x3 layers it supports;
-// NNX_CONV_ALGO=winograd routes the stride-1 3x3x3 split layers with C_out % 32 == 0 and
-// 16-channel input blocks to the Winograd kernel (read when a model's weights are packed).
-// The direct implicit GEMM stays the default: the Winograd kernel measures level with it
-// (one wave a SIMD holds its 256 accumulator registers, which leaves its loads, transforms
-// and epilogue unhidden).
+// The stride-1 3x3x3 split layers with C_out % 32 == 0 and 16-channel input blocks run on
+// the Winograd kernel (fewer fp16 MFMA products per output, so less energy per output under
+// the chip's power cap); NNX_CONV_ALGO=direct keeps every layer on the direct implicit GEMM
+// (read when a model's weights are packed, for comparisons).
 bool winograd_enabled() {
   const char* v = std::getenv("NNX_CONV_ALGO");
-  return v && std::string(v) == "winograd";
+  return !(v && std::string(v) == "direct");
 }
 
 void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {

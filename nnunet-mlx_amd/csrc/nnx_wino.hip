@@ -13,21 +13,22 @@
 // the 1/2 of G, exact), so the arithmetic stays float32-class; U is formed in float64 and
 // rounded once, V in float32, each then split into fp16 halves.
 //
-// Workgroup: 4 waves, an output box of 4 x 8 x 8 voxels (2 x 4 x 4 tiles, the 32 MFMA rows)
-// of one batch item, and 32 output channels (the 32 MFMA columns).  Wave w owns the 16
-// transform positions xz = w, xy = 0..3, xx = 0..3: its accumulators are 16 blocks of
-// 32 x 32 floats (256 registers a lane, one wave a SIMD).  Per chunk of 16 input channels:
+// Workgroup: 8 waves (two a SIMD), an output box of 4 x 8 x 8 voxels (2 x 4 x 4 tiles, the 32
+// MFMA rows) of one batch item, and 32 output channels (the 32 MFMA columns).  Wave
+// w = 2 xz + p owns the 8 transform positions (xz, xy = 2p or 2p + 1, xx = 0..3): its
+// accumulators are 8 blocks of 32 x 32 floats (128 registers a lane), which leaves room for
+// a second wave on the SIMD to issue while one waits.  Per chunk of 16 input channels:
 //   1. the raw 6 x 10 x 10 input halo was fetched by global_load_lds_dwordx4 into one of two
-//      LDS buffers (issued during the previous chunk's products);
+//      LDS buffers during the previous chunk;
 //   2. 400 threads apply the pending InstanceNorm (+ LeakyReLU) of the input to in-volume
 //      voxels and write the z-transform (4 xz x 2 tile rows of z) as 8 padded planes, laid
-//      out so that the 32 tiles of a half-wave read 32 different 16-byte bank groups;
-//   3. each wave reads the four z-transformed rows of its tile patch once, forms V for its
-//      positions (y- then x-transform), splits it into fp16 halves in registers and issues
-//      three MFMAs per position against the packed U of this chunk, read from L2 eight
-//      positions ahead; the next chunk's halo DMA is issued right after this chunk's LDS
-//      reads, and the first half's products cover its latency.
-// Epilogue: each wave applies the x- and y-output transforms to its accumulators, the four
+//      out so that the 32 tiles of a half-wave read 32 different 16-byte bank groups; then
+//      the next chunk's halo DMA is issued;
+//   3. per y-row of its positions, each wave reads two z-transformed rows of its tile patch,
+//      forms V (y- then x-transform), splits it into fp16 halves in registers and issues
+//      three MFMAs per position against the packed U of this chunk, read from L2 four
+//      positions ahead.
+// Epilogue: each wave applies the x- and y-output transforms to its accumulators, the eight
 // partials are combined through LDS (z-output transform), scaled back, + bias, written to
 // an LDS tile for the InstanceNorm partials of the box and stored as 16-byte channel runs.
 #include <cmath>
@@ -46,7 +47,9 @@ typedef float f16v __attribute__((ext_vector_type(16)));
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
-constexpr int kWThreads = 256;                    // 4 waves
+constexpr int kWThreads = 512;                    // 8 waves, two a SIMD
+constexpr int kSteps = 8;                         // transform positions (steps) per wave
+constexpr int kRing = 4;                          // B operands of four steps in flight
 constexpr int kWChunk = 16;                       // input channels per chunk (one MFMA K)
 constexpr int kHaloVox = 6 * 10 * 10;             // input halo of a 4 x 8 x 8 output box
 constexpr int kRawLines = kHaloVox * 4;           // 16-byte lines (4 channels each)
@@ -55,11 +58,12 @@ constexpr int kRawSlots = kRawRounds * kWThreads;  // 16-byte slots per raw buff
 constexpr int kZRow = 41;                          // slots per z-plane row: 10 voxels x 4 + 1
 constexpr int kZPlane = 411;                       // slots per plane: 10 rows + 1 slot
 constexpr int kZSlots = 8 * kZPlane;
-constexpr int kLdsSlots = 2 * kRawSlots + kZSlots;
-constexpr int kPartSlots = 4 * 32 * 32;            // epilogue: 4 waves x 32 tiles x 32 columns
+constexpr int kMaxChannels = 1024;                 // c1 + c2 (pending-norm parameters in LDS)
 constexpr int kTileStride = 36;                    // floats per voxel row of the output tile
-static_assert(kPartSlots <= kLdsSlots, "epilogue partials must fit the main-loop LDS");
-static_assert(256 * kTileStride / 4 + kWThreads / 4 <= kLdsSlots, "output tile fits");
+// epilogue: 8 waves x 32 tiles x 32 columns of partials over the raw and z arrays, then the
+// output tile + reduction in the raw array
+static_assert(8 * 32 * 32 <= 2 * kRawSlots + kZSlots, "epilogue partials fit the main LDS");
+static_assert(256 * kTileStride / 4 + kWThreads / 4 <= 2 * kRawSlots, "output tile fits");
 
 struct WinoArgs {
   const float* x0;
@@ -106,6 +110,29 @@ __device__ __forceinline__ void split8(const float (&v)[8], h8& hi, h8& lo) {
   }
 }
 
+// Two z-plane rows of a tile patch (4 columns x 2 channel halves each, 16 B per read) at LDS
+// byte offsets a and b, with the wait for them.  Written as one asm block so that the
+// compiler's wait-count pass does not see LDS reads here: it would otherwise order them
+// behind the halo DMA issued just before into another buffer (it cannot tell the two apart)
+// and wait for that DMA first.
+__device__ __forceinline__ void zrow_pair(unsigned a, unsigned b, f4 (&va)[8], f4 (&vb)[8]) {
+  asm volatile(
+      "ds_read_b128 %0, %16\n\tds_read_b128 %1, %16 offset:16\n\t"
+      "ds_read_b128 %2, %16 offset:64\n\tds_read_b128 %3, %16 offset:80\n\t"
+      "ds_read_b128 %4, %16 offset:128\n\tds_read_b128 %5, %16 offset:144\n\t"
+      "ds_read_b128 %6, %16 offset:192\n\tds_read_b128 %7, %16 offset:208\n\t"
+      "ds_read_b128 %8, %17\n\tds_read_b128 %9, %17 offset:16\n\t"
+      "ds_read_b128 %10, %17 offset:64\n\tds_read_b128 %11, %17 offset:80\n\t"
+      "ds_read_b128 %12, %17 offset:128\n\tds_read_b128 %13, %17 offset:144\n\t"
+      "ds_read_b128 %14, %17 offset:192\n\tds_read_b128 %15, %17 offset:208\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(va[0]), "=&v"(va[1]), "=&v"(va[2]), "=&v"(va[3]), "=&v"(va[4]), "=&v"(va[5]),
+        "=&v"(va[6]), "=&v"(va[7]), "=&v"(vb[0]), "=&v"(vb[1]), "=&v"(vb[2]), "=&v"(vb[3]),
+        "=&v"(vb[4]), "=&v"(vb[5]), "=&v"(vb[6]), "=&v"(vb[7])
+      : "v"(a), "v"(b)
+      : "memory");
+}
+
 // The InstanceNorm apply pass's operations: r = fma(x - mean, scale, beta), then
 // max(s * r, r) with s = the LeakyReLU slope under the activation and s = 1 (the identity,
 // exactly) without it.
@@ -120,8 +147,11 @@ __device__ __forceinline__ f4 wino_norm(f4 v, const float4 (&p)[4], float s) {
 }
 
 __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
-  extern __shared__ __align__(16) f4 lds[];
-  f4* const zp = lds + 2 * kRawSlots;
+  // three LDS objects: the compiler then knows that the halo DMA into s_raw does not write
+  // what the later reads of s_prm read
+  __shared__ __align__(16) f4 s_raw[2 * kRawSlots];  // two raw halo buffers
+  __shared__ __align__(16) f4 s_z[kZSlots];          // z-transformed planes
+  __shared__ __align__(16) f4 s_prm[kMaxChannels];   // pending-norm parameters
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -139,7 +169,7 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
   const int64_t bvox = (int64_t)b * a.D * a.H * a.W;
 
   // ---- raw halo fetch of one chunk into buffer `buf` (LDS slot = line = voxel * 4 + quad);
-  // this thread's lines r * 512 + tid have fixed voxels: their offsets inside the batch
+  // this thread's lines r * kWThreads + tid have fixed voxels: their offsets inside the batch
   // item (-1 outside the volume or past the halo) are computed once
   const int cq_line = tid & 3;
   int vofs[kRawRounds];
@@ -158,33 +188,34 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
     }
     vofs[r] = o;
   }
-  auto fetch = [&](int chunk, int buf) __attribute__((always_inline)) {
+  // past the last chunk (live = false) every line reads the zero line: the DMA is issued
+  // unconditionally, so no branch joins paths with different counts of loads in flight
+  auto fetch = [&](int chunk, int buf, bool live) __attribute__((always_inline)) {
     const bool first = chunk < a.chunks0;
     const float* src = first ? a.x0 : a.x1;
     const int C = first ? a.c0 : a.c1;
     const float* base = src + bvox * C + (first ? chunk : chunk - a.chunks0) * kWChunk + cq_line * 4;
-    f4* dst = lds + buf * kRawSlots + wave * 64;
+    f4* dst = s_raw + buf * kRawSlots + wave * 64;
 #pragma unroll
     for (int r = 0; r < kRawRounds; ++r) {
       // both addresses formed and one selected: no branch around the load, so the
       // compiler's wait counts stay exact
       const float* in = base + (int64_t)(vofs[r] < 0 ? 0 : vofs[r]) * C;
-      const float* g = vofs[r] >= 0 ? in : g_wino_zero;
+      const float* g = live && vofs[r] >= 0 ? in : g_wino_zero;
       __builtin_amdgcn_global_load_lds(
           g, (__attribute__((address_space(3))) void*)(dst + r * kWThreads), 16, 0, 0);
     }
   };
 
   // ---- pending InstanceNorm parameters of every input channel (both inputs, in chunk
-  // order) for this batch item, kept in LDS after the main buffers
-  f4* const prm = lds + kLdsSlots;
+  // order) for this batch item
   for (int c = tid; c < a.c0 + a.c1; c += kWThreads) {
-    const float4* p = c < a.c0 ? a.nrm0 : a.nrm1;
+    const float4* pp = c < a.c0 ? a.nrm0 : a.nrm1;
     const int C = c < a.c0 ? a.c0 : a.c1;
     const int cc = c < a.c0 ? c : c - a.c0;
     float4 v = make_float4(0.f, 1.f, 0.f, 0.f);
-    if (p) v = p[(int64_t)b * C + cc];
-    prm[c] = f4{v.x, v.y, v.z, 0.f};
+    if (pp) v = pp[(int64_t)b * C + cc];
+    s_prm[c] = f4{v.x, v.y, v.z, 0.f};
   }
 
   // ---- pending norm + z-transform: thread (hy, hx, quad) of the 10 x 10 x 4 columns.  A
@@ -200,10 +231,10 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
     float4 pm[4];
 #pragma unroll
     for (int q = 0; q < 4; ++q) {
-      const f4 v = prm[chunk * kWChunk + cq * 4 + q];
+      const f4 v = s_prm[chunk * kWChunk + cq * 4 + q];
       pm[q] = make_float4(v[0], v[1], v[2], 0.f);
     }
-    const f4* raw = lds + buf * kRawSlots + (hy * 10 + hx) * 4 + cq;
+    const f4* raw = s_raw + buf * kRawSlots + (hy * 10 + hx) * 4 + cq;
     f4 d[6];
 #pragma unroll
     for (int hz = 0; hz < 6; ++hz) d[hz] = raw[hz * 400];
@@ -222,7 +253,7 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
         for (int e = 0; e < 4; ++e) d[hz][e] = inside ? t[e] : 0.f;
       }
     }
-    f4* dst = zp + hy * kZRow + hx * 4 + cq;
+    f4* dst = s_z + hy * kZRow + hx * 4 + cq;
 #pragma unroll
     for (int tz = 0; tz < 2; ++tz) {
       const f4 d0 = d[2 * tz], d1 = d[2 * tz + 1], d2 = d[2 * tz + 2], d3 = d[2 * tz + 3];
@@ -233,45 +264,47 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
     }
   };
   auto transform = [&](int chunk, int buf) __attribute__((always_inline)) {
-    if (interior) {
-      transform_column(std::true_type{}, chunk, buf, tid);
-      if (tid + kWThreads < 400) transform_column(std::true_type{}, chunk, buf, tid + kWThreads);
-    } else {
-      transform_column(std::false_type{}, chunk, buf, tid);
-      if (tid + kWThreads < 400) transform_column(std::false_type{}, chunk, buf, tid + kWThreads);
+    if (tid < 400) {
+      if (interior)
+        transform_column(std::true_type{}, chunk, buf, tid);
+      else
+        transform_column(std::false_type{}, chunk, buf, tid);
     }
   };
 
-  // ---- this lane's tile, channel half and transform positions
-  const int xz = wave;
+  // ---- this lane's tile, channel half and transform positions: wave = (xz, half p), the
+  // half owning xy = 2p and 2p + 1
+  const int xz = wave >> 1, p = wave & 1;
   const int t = lane & 31, tzl = t >> 4, tyl = (t >> 2) & 3, txl = t & 3, g8 = lane >> 5;
-  const f4* zb = zp + (xz * 2 + tzl) * kZPlane + (2 * tyl) * kZRow + (2 * txl) * 4 + 2 * g8;
+  // LDS byte offset of this lane's first z-row read (tile patch corner, channel half g8)
+  const unsigned zb_lds = (unsigned)(uintptr_t)(
+      (__attribute__((address_space(3))) f4*)s_z + ((xz * 2 + tzl) * kZPlane + (2 * tyl) * kZRow +
+                                                    (2 * txl) * 4 + 2 * g8));
 
   // packed U: [nt][chunk][xi = (xz * 4 + xy) * 4 + xx][hi | lo][64 lanes] x 16 bytes; step
-  // s = xy * 4 + xx of a chunk uses position xi = xz * 16 + s
-  const uint4* ub = a.u + ((int64_t)nt * a.chunks * 64 + xz * 16) * 128 + lane;
+  // s (local xy = s / 4, xx = s % 4) of a chunk uses position xi = xz * 16 + p * 8 + s
+  const uint4* ub = a.u + ((int64_t)nt * a.chunks * 64 + xz * 16 + p * kSteps) * 128 + lane;
   auto uaddr = [&](int chunk, int step) { return ub + ((int64_t)chunk * 64 + step) * 128; };
 
-  f16v acc[4][4];
+  f16v acc[2][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int x = 0; x < 4; ++x)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[j][x][r] = 0.f;
 
-  constexpr int kRing = 8;  // B operands of eight steps in flight
   uint4 uh[kRing], ul[kRing];
-  fetch(0, 0);
+  fetch(0, 0, true);
 #pragma unroll
   for (int s = 0; s < kRing; ++s) {
-    const uint4* p = uaddr(0, s);
-    uh[s] = p[0];
-    ul[s] = p[64];
+    const uint4* up = uaddr(0, s);
+    uh[s] = up[0];
+    ul[s] = up[64];
   }
 
-  // the three products of step s (position xy = s / 4, xx = s % 4) for two steps at a
-  // time, then the refill of their ring slots eight steps ahead
+  // the three products of step s (local xy = s / 4, xx = s % 4) for two steps at a time,
+  // then the refill of their ring slots kRing steps ahead
   auto products = [&](int s0, const float (&q)[4][8], int chunk) __attribute__((always_inline)) {
     h8 ah[2], al[2];
 #pragma unroll
@@ -302,77 +335,80 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
       acc[xy][x0 + k] = mfma32(al[k], *reinterpret_cast<const h8*>(&uh[slot]), acc[xy][x0 + k]);
       // unconditional (past the last chunk the last chunk's words are read again)
       const int ns = s + kRing;
-      int nchunk = ns < 16 ? chunk : chunk + 1;
+      int nchunk = ns < kSteps ? chunk : chunk + 1;
       nchunk = nchunk < a.chunks ? nchunk : a.chunks - 1;
-      const uint4* p = uaddr(nchunk, ns & 15);
-      uh[slot] = p[0];
-      ul[slot] = p[64];
+      const uint4* up = uaddr(nchunk, ns & (kSteps - 1));
+      uh[slot] = up[0];
+      ul[slot] = up[64];
     }
   };
 
+  // one y-row of Q at a time: half 0 forms xy 0, 1 (r0 - r2, r1 + r2), half 1 xy 2, 3
+  // (r2 - r1, r1 - r3), i.e. Q0 = R[2p] - R[2 - p] and Q1 = R[1] + sg R[2 + p] with sg = +-1
+  // (fma: one rounding, as the add or subtract)
+  const float sg = p ? -1.f : 1.f;
   for (int chunk = 0; chunk < a.chunks; ++chunk) {
     const int buf = chunk & 1;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's halo lines and B operands have landed
     __syncthreads();                 // every thread's; the z-planes are free
     transform(chunk, buf);
-    __syncthreads();                 // z-planes written; the raw buffer `buf` is free
-    // the four z-transformed rows of the tile patch, y-transformed: Q[xy][column][channel]
-    float q[4][4][8];
-    {
-      f4 rows[4][4][2];
+    // the next chunk's halo into the other buffer (free since this chunk began), after this
+    // thread's reads of `buf`: a whole chunk of products covers its latency
+    const bool more = chunk + 1 < a.chunks;
+    fetch(more ? chunk + 1 : chunk, buf ^ 1, more);
+    // z-planes written: this thread's LDS writes complete, then the barrier.  Not
+    // __syncthreads(), whose release fence would also wait for the DMA just issued (nothing
+    // reads that buffer before the next chunk's full wait and barrier).
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-          const f4* p = zb + r * kZRow + c * 4;
-          rows[r][c][0] = p[0];
-          rows[r][c][1] = p[1];
-        }
+    for (int j = 0; j < 2; ++j) {
+      f4 va[8], vb[8];  // [column * 2 + half]
+      zrow_pair(zb_lds + (j == 0 ? 2 * p : 1) * kZRow * 16,
+                zb_lds + (j == 0 ? 2 - p : 2 + p) * kZRow * 16, va, vb);
+      float q[4][8];
 #pragma unroll
       for (int c = 0; c < 4; ++c)
 #pragma unroll
         for (int h = 0; h < 2; ++h)
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float r0 = rows[0][c][h][e], r1 = rows[1][c][h][e];
-            const float r2 = rows[2][c][h][e], r3 = rows[3][c][h][e];
-            q[0][c][4 * h + e] = r0 - r2;
-            q[1][c][4 * h + e] = r1 + r2;
-            q[2][c][4 * h + e] = r2 - r1;
-            q[3][c][4 * h + e] = r1 - r3;
-          }
+          for (int e = 0; e < 4; ++e)
+            q[c][4 * h + e] = j == 0 ? va[2 * c + h][e] - vb[2 * c + h][e]
+                                     : fmaf(sg, vb[2 * c + h][e], va[2 * c + h][e]);
+      products(4 * j, q, chunk);
+      products(4 * j + 2, q, chunk);
     }
-    // the next chunk's halo, after this chunk's last LDS read; vector-memory loads
-    // complete in order, so the second-half operands requested below land after it: the
-    // first half's products cover its latency
-    if (chunk + 1 < a.chunks) fetch(chunk + 1, buf ^ 1);
-#pragma unroll
-    for (int s0 = 0; s0 < 16; s0 += 2) products(s0, q[s0 >> 2], chunk);
   }
 
   // ---- epilogue
-  // x- and y-output transforms of this wave's 16 positions: per accumulator element, the
-  // (oy, ox) outputs of its tile row for this xz
-  __syncthreads();  // every wave is past its last z-plane read
-  f4* part = lds;   // [wave][tile][column] x (oy0ox0, oy0ox1, oy1ox0, oy1ox1)
+  // x- and y-output transforms of this wave's positions: per accumulator element, this
+  // half's share of the (oy, ox) outputs of its tile row for this xz (oy0 = xy0 + xy1 +
+  // xy2, oy1 = xy1 - xy2 - xy3)
+  __builtin_amdgcn_s_waitcnt(0);  // the last (zero-line) DMA has landed in s_raw
+  __syncthreads();                 // every wave is past its last z-plane read and DMA
+  // partials [wave][tile][column] x (oy0ox0, oy0ox1, oy1ox0, oy1ox1): waves 0-4 in s_raw,
+  // waves 5-7 in s_z
+  auto part = [&](int w, int tile, int c) -> f4& {
+    const int i = (w * 32 + tile) * 32 + c;
+    return i < 2 * kRawSlots ? s_raw[i] : s_z[i - 2 * kRawSlots];
+  };
   const int col = lane & 31;
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    float xo[4][2];  // [xy][ox]
+    float xo[2][2];  // [local xy][ox]
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
+    for (int j = 0; j < 2; ++j) {
       const float m0 = acc[j][0][r], m1 = acc[j][1][r], m2 = acc[j][2][r], m3 = acc[j][3][r];
       xo[j][0] = (m0 + m1) + m2;
       xo[j][1] = (m1 - m2) - m3;
     }
-    const f4 pv = {(xo[0][0] + xo[1][0]) + xo[2][0], (xo[0][1] + xo[1][1]) + xo[2][1],
-                   (xo[1][0] - xo[2][0]) - xo[3][0], (xo[1][1] - xo[2][1]) - xo[3][1]};
+    const f4 pv = p == 0 ? f4{xo[0][0] + xo[1][0], xo[0][1] + xo[1][1], xo[1][0], xo[1][1]}
+                         : f4{xo[0][0], xo[0][1], -(xo[0][0] + xo[1][0]), -(xo[0][1] + xo[1][1])};
     const int tile = 8 * (r >> 2) + 4 * g8 + (r & 3);
-    part[(wave * 32 + tile) * 32 + col] = pv;
+    part(wave, tile, col) = pv;
   }
   __syncthreads();
-  // z-output transform over the four partials: oz0 = P0 + P1 + P2, oz1 = P1 - P2 - P3; then
-  // the weight scale and the bias
+  // z-output transform over the four xz partials: oz0 = P0 + P1 + P2, oz1 = P1 - P2 - P3;
+  // then the weight scale and the bias
   constexpr int kPairs = 32 * 32 / kWThreads;
   f4 yo[kPairs][2];  // [pair][oz]
   const float bias_c = a.bias ? a.bias[nt * 32 + (tid & 31)] : 0.f;
@@ -382,7 +418,7 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
     const int tile = idx >> 5, c = idx & 31;
     f4 pz[4];
 #pragma unroll
-    for (int z = 0; z < 4; ++z) pz[z] = part[(z * 32 + tile) * 32 + c];
+    for (int z = 0; z < 4; ++z) pz[z] = part(2 * z, tile, c) + part(2 * z + 1, tile, c);
     const f4 y0 = (pz[0] + pz[1]) + pz[2];
     const f4 y1 = (pz[1] - pz[2]) - pz[3];
     yo[k][0] = y0 * a.out_scale;
@@ -393,7 +429,7 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
     }
   }
   __syncthreads();
-  float* otile = reinterpret_cast<float*>(lds);  // [box voxel (z, y, x)][column], stride 36
+  float* otile = reinterpret_cast<float*>(s_raw);  // [box voxel (z, y, x)][column], stride 36
 #pragma unroll
   for (int k = 0; k < kPairs; ++k) {
     const int idx = tid + k * kWThreads;
@@ -612,9 +648,8 @@ void conv3d_wino(const float* x1, int c1, const float* x2, int c2, const void* p
   const double bytes = 4.0 * ((double)g.batch * g.in[0] * g.in[1] * g.in[2] * (c1 + c2) +
                               out_vox * cout);
   ProfScope prof("conv3d_wino", flops, bytes, st);
-  const size_t lds_bytes = ((size_t)kLdsSlots + c1 + c2) * 16;
-  require(lds_bytes <= 160 * 1024, "too many input channels for the Winograd convolution");
-  hipLaunchKernelGGL(wino_x3_kernel, dim3(a.nwg), dim3(kWThreads), lds_bytes, st, a);
+  require(c1 + c2 <= kMaxChannels, "too many input channels for the Winograd convolution");
+  hipLaunchKernelGGL(wino_x3_kernel, dim3(a.nwg), dim3(kWThreads), 0, st, a);
   launch_check("conv3d_winograd");
 }
 

@@ -104,12 +104,13 @@ def test_forward_matches_oracle(device, name):
         net.close()
 
 
+@pytest.mark.parametrize("algo", ["winograd", "direct"])
 @pytest.mark.parametrize("name", ["liver-32", "brats-4ch", "autopet-aniso", "tiny-residual"])
-def test_winograd_route_matches_oracle(device, monkeypatch, name):
-    """NNX_CONV_ALGO=winograd (read when the weights are packed) sends the stride-1 3x3x3
-    split layers with 16-channel input blocks and C_out % 32 == 0 to the Winograd kernel;
-    the network then holds the same float32 bar.  The kernel profile shows the route was
-    taken (tiny-residual has no eligible layer: every layer stays direct)."""
+def test_conv_route_matches_oracle(device, monkeypatch, name, algo):
+    """The stride-1 3x3x3 split layers with 16-channel input blocks and C_out % 32 == 0 run
+    on the Winograd kernel by default; NNX_CONV_ALGO=direct (read when the weights are
+    packed) keeps them on the direct implicit GEMM.  Either route holds the float32 bar, and
+    the kernel profile shows which one ran (tiny-residual has no eligible layer)."""
     from nnunet_mlx import _native
 
     spec, patch, batch, affine = CASES[name]
@@ -117,16 +118,22 @@ def test_winograd_route_matches_oracle(device, monkeypatch, name):
     x = np.random.default_rng(5).standard_normal((batch, *patch, spec.input_channels)).astype(np.float32)
     residual = isinstance(spec, ResidualEncoderUNetSpec)
     ref = OracleNetwork(spec, weights, residual=residual)(x)
-    monkeypatch.setenv("NNX_CONV_ALGO", "winograd")
-    print(f"winograd network case {name} patch={patch} batch={batch}", flush=True)
+    monkeypatch.setenv("NNX_CONV_ALGO", algo)
+    print(f"{algo} network case {name} patch={patch} batch={batch}", flush=True)
     net = build_network(spec, precision="fp32-split")
     net.load_weights(weights)
     with _native.KernelProfile() as prof:
         got = net(torch.from_numpy(x).to(device)).cpu().numpy()
     net.close()
     wino = prof.classes.get("conv3d_wino", {}).get("launches", 0)
-    assert (wino == 0) == (name == "tiny-residual"), prof.classes.keys()
-    msg = report(f"{name} winograd", got, ref)
+    direct = sum(c["launches"] for n, c in prof.classes.items() if n.startswith("conv3d_x3s"))
+    if algo == "direct" or name == "tiny-residual":
+        assert wino == 0, prof.classes.keys()
+    else:
+        assert wino > 0, prof.classes.keys()
+    if algo == "direct" and name != "tiny-residual":
+        assert direct > 0, prof.classes.keys()
+    msg = report(f"{name} {algo}", got, ref)
     print(msg, f"winograd launches {wino}", flush=True)
     assert np.isfinite(got).all(), msg
     assert np.abs(got - ref).max() <= 1e-3, msg
