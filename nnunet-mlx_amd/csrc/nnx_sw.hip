@@ -20,76 +20,98 @@ struct Flips {
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
-__global__ __launch_bounds__(256) void gather_flip_kernel(
+// A workgroup per patch row (y, z) = (blockIdx.x, blockIdx.y), its threads along x: every
+// view's flipped source row is uniform over the workgroup, only x flips per lane.  Reads
+// the source voxel of each channel (zero outside the volume) and writes the channels-last
+// row of every view.
+__global__ __launch_bounds__(512) void gather_flip_kernel(
     const float* __restrict__ vol, int C, int64_t Z, int64_t Y, int64_t X, int pz, int py, int px,
     int oz, int oy, int ox, int PZ, int PY, int PX, Flips flips, int nviews,
     float* __restrict__ out) {
+  const int y = blockIdx.x, z = blockIdx.y;
   const int64_t pvox = (int64_t)PZ * PY * PX;
   const int64_t zyx = Z * Y * X;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < pvox * nviews;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int v = (int)(i / pvox);
-    const int64_t p = i - (int64_t)v * pvox;
-    const int x = (int)(p % PX);
-    const int y = (int)((p / PX) % PY);
-    const int z = (int)(p / ((int64_t)PX * PY));
-    const int f = flips.f[v];
-    const int sz = (f & 1) ? PZ - 1 - z : z;
-    const int sy = (f & 2) ? PY - 1 - y : y;
-    const int sx = (f & 4) ? PX - 1 - x : x;
-    const int64_t gz = (int64_t)oz + sz - pz, gy = (int64_t)oy + sy - py, gx = (int64_t)ox + sx - px;
-    const bool inside = gz >= 0 && gz < Z && gy >= 0 && gy < Y && gx >= 0 && gx < X;
-    const int64_t src = (gz * Y + gy) * X + gx;
-    float* dst = out + i * C;
-    for (int c = 0; c < C; ++c) dst[c] = inside ? vol[(int64_t)c * zyx + src] : 0.f;
+  const int64_t prow = ((int64_t)z * PY + y) * PX;
+  for (int x = threadIdx.x; x < PX; x += blockDim.x) {
+    for (int c = 0; c < C; ++c) {
+      // every view's value first (loads in flight together), then the stores
+      float val[8];
+#pragma unroll
+      for (int v = 0; v < 8; ++v) {
+        val[v] = 0.f;
+        if (v < nviews) {
+          const int f = flips.f[v];
+          const int64_t gz = (int64_t)oz + ((f & 1) ? PZ - 1 - z : z) - pz;
+          const int64_t gy = (int64_t)oy + ((f & 2) ? PY - 1 - y : y) - py;
+          const int64_t gx = (int64_t)ox + ((f & 4) ? PX - 1 - x : x) - px;
+          if (gz >= 0 && gz < Z && gy >= 0 && gy < Y && gx >= 0 && gx < X)
+            val[v] = vol[(int64_t)c * zyx + (gz * Y + gy) * X + gx];
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < 8; ++v)
+        if (v < nviews) out[((int64_t)v * pvox + prow + x) * C + c] = val[v];
+    }
   }
 }
 
+// A workgroup per patch row (y, z), its threads along the row's (x, class) pairs: each
+// view's flipped source row is uniform over the workgroup, consecutive lanes read
+// consecutive floats of the prediction rows and update consecutive accumulator elements
+// (whole cache lines); the class-0 lane of a voxel updates its normaliser.
 template <bool kHalf>
-__global__ __launch_bounds__(256) void accumulate_kernel(
+__global__ __launch_bounds__(512) void accumulate_kernel(
     const float* __restrict__ pred, int nviews, Flips flips, int K, int PZ, int PY, int PX,
     const void* __restrict__ gaussian, int oz, int oy, int ox, int64_t QY, int64_t QX,
     void* __restrict__ acc, void* __restrict__ norm) {
+  const int y = blockIdx.x, z = blockIdx.y;
   const int64_t pvox = (int64_t)PZ * PY * PX;
+  const int64_t prow = ((int64_t)z * PY + y) * PX;
+  const int64_t qrow = (((int64_t)oz + z) * QY + (oy + y)) * QX + ox;
   const float count = (float)nviews;
-  for (int64_t p = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; p < pvox;
-       p += (int64_t)gridDim.x * blockDim.x) {
-    const int x = (int)(p % PX);
-    const int y = (int)((p / PX) % PY);
-    const int z = (int)(p / ((int64_t)PX * PY));
-    int64_t src[8];
-    for (int v = 0; v < nviews; ++v) {
-      const int f = flips.f[v];
-      const int sz = (f & 1) ? PZ - 1 - z : z;
-      const int sy = (f & 2) ? PY - 1 - y : y;
-      const int sx = (f & 4) ? PX - 1 - x : x;
-      src[v] = (int64_t)v * pvox + ((int64_t)sz * PY + sy) * PX + sx;
-    }
-    const int64_t dst = (((int64_t)oz + z) * QY + (oy + y)) * QX + (ox + x);
-    float g;
-    if constexpr (kHalf)
-      g = __half2float(reinterpret_cast<const __half*>(gaussian)[p]);
-    else
-      g = reinterpret_cast<const float*>(gaussian)[p];
-    for (int k = 0; k < K; ++k) {
-      float s = pred[src[0] * K + k];
-      for (int v = 1; v < nviews; ++v) s = add_rn(s, pred[src[v] * K + k]);
-      if (nviews > 1) s = __fdiv_rn(s, count);
-      const float w = mul_rn(s, g);
-      if constexpr (kHalf) {
-        __half* a = reinterpret_cast<__half*>(acc) + dst * K + k;
-        *a = __float2half_rn(add_rn(__half2float(*a), w));
-      } else {
-        float* a = reinterpret_cast<float*>(acc) + dst * K + k;
-        *a = add_rn(*a, w);
+  const int n = PX * K;
+  for (int e = threadIdx.x; e < n; e += blockDim.x) {
+    const int x = e / K;
+    const int k = e - x * K;
+    // every view's value first (loads in flight together), then the sum in view order
+    float t[8];
+#pragma unroll
+    for (int v = 0; v < 8; ++v) {
+      t[v] = 0.f;
+      if (v < nviews) {
+        const int f = flips.f[v];
+        const int64_t srow =
+            ((int64_t)((f & 1) ? PZ - 1 - z : z) * PY + ((f & 2) ? PY - 1 - y : y)) * PX;
+        const int sx = (f & 4) ? PX - 1 - x : x;
+        t[v] = pred[((int64_t)v * pvox + srow + sx) * K + k];
       }
     }
+    float s = t[0];
+#pragma unroll
+    for (int v = 1; v < 8; ++v)
+      if (v < nviews) s = add_rn(s, t[v]);
+    if (nviews > 1) s = __fdiv_rn(s, count);
+    float g;
+    if constexpr (kHalf)
+      g = __half2float(reinterpret_cast<const __half*>(gaussian)[prow + x]);
+    else
+      g = reinterpret_cast<const float*>(gaussian)[prow + x];
+    const float w = mul_rn(s, g);
+    const int64_t dst = qrow + x;
     if constexpr (kHalf) {
-      __half* nrm = reinterpret_cast<__half*>(norm) + dst;
-      *nrm = __float2half_rn(add_rn(__half2float(*nrm), g));
+      __half* a = reinterpret_cast<__half*>(acc) + dst * K + k;
+      *a = __float2half_rn(add_rn(__half2float(*a), w));
+      if (k == 0) {
+        __half* nrm = reinterpret_cast<__half*>(norm) + dst;
+        *nrm = __float2half_rn(add_rn(__half2float(*nrm), g));
+      }
     } else {
-      float* nrm = reinterpret_cast<float*>(norm) + dst;
-      *nrm = add_rn(*nrm, g);
+      float* a = reinterpret_cast<float*>(acc) + dst * K + k;
+      *a = add_rn(*a, w);
+      if (k == 0) {
+        float* nrm = reinterpret_cast<float*>(norm) + dst;
+        *nrm = add_rn(*nrm, g);
+      }
     }
   }
 }
@@ -174,6 +196,9 @@ __global__ __launch_bounds__(256) void fold_finalize_kernel(const void* __restri
   if (threadIdx.x == 0 && block_invalid && invalid_count) atomicAdd(invalid_count, block_invalid);
 }
 
+// Threads of a one-row workgroup: the row's elements rounded up to whole waves, at most 512.
+unsigned row_threads(int64_t n) { return (unsigned)std::min<int64_t>(512, std::max<int64_t>(64, ceil_div(n, 64) * 64)); }
+
 unsigned grid_for(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 65536)); }
 
 Flips make_flips(const int* flips, int nviews) {
@@ -195,8 +220,10 @@ void sw_gather_flip(const float* vol, int channels, const int64_t* size, const i
   require(channels >= 1, "gather needs at least one channel");
   const Flips f = make_flips(flips, nviews);
   const int64_t n = (int64_t)patch[0] * patch[1] * patch[2] * nviews;
+  require(patch[1] <= 65535 && patch[0] <= 65535, "patch rows exceed the launch grid");
   ProfScope prof("sw_gather_flip", 0.0, 4.0 * (double)n / nviews * channels * (1 + nviews), st);
-  hipLaunchKernelGGL(gather_flip_kernel, dim3(grid_for(n)), dim3(256), 0, st, vol, channels,
+  hipLaunchKernelGGL(gather_flip_kernel, dim3(patch[1], patch[0]), dim3(row_threads(patch[2])), 0,
+                     st, vol, channels,
                      size[0], size[1], size[2], pad_before[0], pad_before[1], pad_before[2],
                      offset[0], offset[1], offset[2], patch[0], patch[1], patch[2], f, nviews, out);
   launch_check("sw_gather_flip");
@@ -211,15 +238,18 @@ void sw_accumulate(const float* pred, int nviews, const int* flips, int k, const
     require(offset[i] >= 0 && offset[i] + patch[i] <= padded[i], "tile outside the padded volume");
   const Flips f = make_flips(flips, nviews);
   const int64_t n = (int64_t)patch[0] * patch[1] * patch[2];
+  require(patch[1] <= 65535 && patch[0] <= 65535, "patch rows exceed the launch grid");
   const double esz = accum == NNX_ACCUM_NNUNET_F16 ? 2.0 : 4.0;
   ProfScope prof("sw_accumulate", 0.0,
                  (double)n * (nviews * k * 4.0 + 2.0 * k * esz + 2.0 * esz + esz), st);
   if (accum == NNX_ACCUM_NNUNET_F16)
-    hipLaunchKernelGGL(accumulate_kernel<true>, dim3(grid_for(n)), dim3(256), 0, st, pred, nviews,
+    hipLaunchKernelGGL(accumulate_kernel<true>, dim3(patch[1], patch[0]),
+                       dim3(row_threads((int64_t)patch[2] * k)), 0, st, pred, nviews,
                        f, k, patch[0], patch[1], patch[2], gaussian, offset[0], offset[1],
                        offset[2], padded[1], padded[2], acc, norm);
   else
-    hipLaunchKernelGGL(accumulate_kernel<false>, dim3(grid_for(n)), dim3(256), 0, st, pred, nviews,
+    hipLaunchKernelGGL(accumulate_kernel<false>, dim3(patch[1], patch[0]),
+                       dim3(row_threads((int64_t)patch[2] * k)), 0, st, pred, nviews,
                        f, k, patch[0], patch[1], patch[2], gaussian, offset[0], offset[1],
                        offset[2], padded[1], padded[2], acc, norm);
   launch_check("sw_accumulate");
