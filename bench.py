@@ -325,11 +325,65 @@ def measured_traffic(kernel_class: str) -> float | None:
     return None
 
 
-def cpu_baseline(spec, weights) -> dict:
-    """The CPU oracle on a bounded sample of the liver case: one 128^3 forward (median of 3
-    after one warm-up) and one tile's mirrored average + Gaussian accumulation with the
-    oracle's own flips (8 views: flip, forward output, flip back, sum, divide, accumulate;
-    median of 3), extrapolated to the case's 968 forwards and 121 tiles."""
+def kernel_table(classes: dict, steps: int, traffic: bool = True) -> tuple[dict, dict]:
+    """Per-kernel-class rates of a KernelProfile (launches and ms per step) and the roofline
+    object of the dominant class (largest share of the timed region): algorithmic FLOPs or
+    bytes over its launch time, against the published peak of the unit that bounds it.
+    `traffic`: take the HBM bytes per launch from the liver-case counter summary (only the
+    liver workload's launches are the ones it measured)."""
+    kernels = {}
+    for name, c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
+        entry = {"launches": c["launches"] // steps, "ms": round(c["ms"] / steps, 3)}
+        if c["flops"]:
+            entry["tflops"] = round(c["flops"] / (c["ms"] * 1e-3) / 1e12, 2)
+            if name.startswith("conv3d_x3") and "_bf16" in name:
+                # issued bf16 MFMA work: 1 product per term, 4-tap groups (27 -> 28 taps)
+                entry["frac_bf16_mfma_issued"] = round(
+                    entry["tflops"] * 28 / 27 / PEAK_FP16_MFMA_TFLOPS, 4)
+            elif name.startswith("conv3d_x3"):
+                # issued fp16 MFMA work: 3 products per term, 4-tap groups (27 -> 28 taps)
+                entry["frac_fp16_mfma_issued"] = round(
+                    entry["tflops"] * SPLIT_PRODUCTS * 28 / 27 / PEAK_FP16_MFMA_TFLOPS, 4)
+            elif name == "conv3d_wino":
+                # issued fp16 MFMA work: 3 products per term, 64 transform positions per 8
+                # outputs in place of 8 x 27 taps
+                entry["frac_fp16_mfma_issued"] = round(
+                    entry["tflops"] * SPLIT_PRODUCTS * 64 / 216 / PEAK_FP16_MFMA_TFLOPS, 4)
+            else:
+                entry["frac_fp32_mfma"] = round(entry["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4)
+        elif c["bytes"]:
+            entry["gbs"] = round(c["bytes"] / (c["ms"] * 1e-3) / 1e9, 1)
+            entry["frac_hbm"] = round(entry["gbs"] / PEAK_HBM_GBS, 4)
+        kernels[name] = entry
+    dominant = max(classes, key=lambda n: classes[n]["ms"])
+    d = classes[dominant]
+    if d["flops"]:
+        achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
+        # the split kernels run on fp16 MFMA: their algorithmic (float32-product) rate is
+        # priced against the dense fp16 peak, the issued rate is reported beside it
+        fp16 = dominant.startswith(("conv3d_x3", "conv3d_wino"))
+        peak = PEAK_FP16_MFMA_TFLOPS if fp16 else PEAK_FP32_MFMA_TFLOPS
+        roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 2),
+                    "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
+                    "traffic": measured_traffic(dominant) if traffic else None}
+        if fp16:
+            roofline["issued_frac"] = kernels[dominant].get(
+                "frac_bf16_mfma_issued", kernels[dominant].get("frac_fp16_mfma_issued"))
+    else:
+        achieved = d["bytes"] / (d["ms"] * 1e-3) / 1e9
+        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
+                    "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                    "traffic": None}
+    return kernels, roofline
+
+
+def cpu_baseline(spec, weights, *, patch=None, forwards=968, accumulations=121,
+                 axes=(0, 1, 2), voxels=None, residual=False, case="case") -> dict:
+    """The CPU oracle on a bounded sample of a case: one patch forward (median of 3 after one
+    warm-up) and one tile's mirrored average + Gaussian accumulation with the oracle's own
+    flips (flip, forward output, flip back, sum, divide, accumulate; median of 3),
+    extrapolated to the case's forwards (tiles x folds x views) and accumulations (tiles x
+    folds).  Defaults: the liver case (968 forwards, 121 tiles)."""
     import statistics
 
     import numpy as np
@@ -338,10 +392,11 @@ def cpu_baseline(spec, weights) -> dict:
     from oracle import sliding_window as osw
     from oracle.network import OracleNetwork
 
+    patch = tuple(patch or PATCH)
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    net = OracleNetwork(spec, weights)
-    x = synthetic_ct((1, *PATCH), seed=3)[0][None, ..., None]
+    net = OracleNetwork(spec, weights, residual=residual)
+    x = np.random.default_rng(3).standard_normal((1, *patch, spec.input_channels)).astype(np.float32)
     pred = net(x)                                          # warm-up
     forward_times = []
     for _ in range(3):
@@ -349,20 +404,20 @@ def cpu_baseline(spec, weights) -> dict:
         pred = net(x)
         forward_times.append(time.perf_counter() - t0)
     forward_s = statistics.median(forward_times)
-    g = osw.gaussian_importance(PATCH)[..., None]
-    acc = np.zeros((*PATCH, 3), dtype=np.float32)
-    norm = np.zeros((*PATCH, 1), dtype=np.float32)
+    g = osw.gaussian_importance(patch)[..., None]
+    acc = np.zeros((*patch, spec.num_classes), dtype=np.float32)
+    norm = np.zeros((*patch, 1), dtype=np.float32)
     cached = pred  # the network's output stands in for each view's forward
     accumulate_times = []
     for _ in range(3):
         t0 = time.perf_counter()
-        p = osw.mirrored_prediction(lambda tile: cached, x, (0, 1, 2))[0]
+        p = osw.mirrored_prediction(lambda tile: cached, x, tuple(axes))[0]
         acc += p * g
         norm += g
         accumulate_times.append(time.perf_counter() - t0)
     accumulate_s = statistics.median(accumulate_times)
-    case_s = 968 * forward_s + 121 * accumulate_s
-    voxels = int(np.prod(VOLUME_SHAPE[1:]))
+    case_s = forwards * forward_s + accumulations * accumulate_s
+    voxels = voxels or int(np.prod(VOLUME_SHAPE[1:]))
     cpu_model = ""
     try:
         for line in open("/proc/cpuinfo"):
@@ -377,10 +432,11 @@ def cpu_baseline(spec, weights) -> dict:
         "cores": cores,
         "kind": "port",
         "sample": (f"CPU oracle (torch-CPU fp32 network, numpy sliding window) on {cores} "
-                   f"threads of {cpu_model or 'the host CPU'}: one 128^3 forward "
-                   f"{forward_s:.2f} s (median of 3 after a warm-up) and one tile's 8-view "
-                   f"mirrored average + Gaussian accumulation {accumulate_s:.3f} s (median of "
-                   f"3), extrapolated to 968 forwards + 121 tiles = {case_s:.0f} s per case"),
+                   f"threads of {cpu_model or 'the host CPU'}: one {'x'.join(map(str, patch))} "
+                   f"forward {forward_s:.2f} s (median of 3 after a warm-up) and one tile's "
+                   f"{2 ** len(axes)}-view mirrored average + Gaussian accumulation "
+                   f"{accumulate_s:.3f} s (median of 3), extrapolated to {forwards} forwards + "
+                   f"{accumulations} tile accumulations = {case_s:.0f} s per {case}"),
     }
 
 
@@ -469,18 +525,19 @@ def ensemble_workload(args) -> int:
             labels = sw.average_fold_labels(nets, d_volume, return_device=True, **kwargs)
         torch.cuda.synchronize()
         step_s = (time.perf_counter() - t0) / args.steps
-    kernels = {}
-    for name, c in sorted(prof.classes.items(), key=lambda kv: -kv[1]["ms"]):
-        entry = {"launches": c["launches"] // args.steps, "ms": round(c["ms"] / args.steps, 3)}
-        if c["flops"]:
-            entry["tflops"] = round(c["flops"] / (c["ms"] * 1e-3) / 1e12, 2)
-        elif c["bytes"]:
-            entry["gbs"] = round(c["bytes"] / (c["ms"] * 1e-3) / 1e9, 1)
-        kernels[name] = entry
+    kernels, roofline = kernel_table(prof.classes, steps=args.steps, traffic=False)
     steps = [len(s) for s in sw.compute_steps([max(a, b) for a, b in zip(volume.shape[1:], patch)],
                                               patch, step_fraction=0.5)]
     tiles = int(np.prod(steps))
     voxels = int(np.prod(volume.shape[1:]))
+    baseline = None
+    if not args.no_cpu_baseline:
+        print(f"[bench] {args.workload} CPU baseline sample", file=sys.stderr, flush=True)
+        baseline = cpu_baseline(spec, random_weights(spec, seed=seeds[0]), patch=patch,
+                                forwards=tiles * len(nets) * 2 ** len(axes),
+                                accumulations=tiles * len(nets), axes=axes, voxels=voxels,
+                                residual=isinstance(spec, ResidualEncoderUNetSpec),
+                                case=f"{args.workload} case")
     line = {
         "metric": f"sliding-window voxels/s, {args.workload} configuration",
         "value": round(voxels / step_s, 1), "unit": "voxels/s", "n_gpus": 1, "steps": args.steps,
@@ -495,7 +552,7 @@ def ensemble_workload(args) -> int:
                                f"{tiles * len(nets) * 2 ** len(axes)} forwards",
                    "label_counts": torch.bincount(labels.reshape(-1).to(torch.int64),
                                                   minlength=spec.num_classes).tolist()},
-        "kernels": kernels, "roofline": None, "cpu_baseline": None,
+        "kernels": kernels, "roofline": roofline, "cpu_baseline": baseline,
     }
     for net in nets:
         net.close()
@@ -661,49 +718,7 @@ def main() -> int:
     print(f"[bench] {step_s:.3f} s per case; label counts {counts.tolist()}", file=sys.stderr, flush=True)
 
     classes = prof.classes
-    kernels = {}
-    for name, c in sorted(classes.items(), key=lambda kv: -kv[1]["ms"]):
-        entry = {"launches": c["launches"], "ms": round(c["ms"], 3)}
-        if c["flops"]:
-            entry["tflops"] = round(c["flops"] / (c["ms"] * 1e-3) / 1e12, 2)
-            if name.startswith("conv3d_x3") and "_bf16" in name:
-                # issued bf16 MFMA work: 1 product per term, 4-tap groups (27 -> 28 taps)
-                entry["frac_bf16_mfma_issued"] = round(
-                    entry["tflops"] * 28 / 27 / PEAK_FP16_MFMA_TFLOPS, 4)
-            elif name.startswith("conv3d_x3"):
-                # issued fp16 MFMA work: 3 products per term, 4-tap groups (27 -> 28 taps)
-                entry["frac_fp16_mfma_issued"] = round(
-                    entry["tflops"] * SPLIT_PRODUCTS * 28 / 27 / PEAK_FP16_MFMA_TFLOPS, 4)
-            elif name == "conv3d_wino":
-                # issued fp16 MFMA work: 3 products per term, 64 transform positions per 8
-                # outputs in place of 8 x 27 taps
-                entry["frac_fp16_mfma_issued"] = round(
-                    entry["tflops"] * SPLIT_PRODUCTS * 64 / 216 / PEAK_FP16_MFMA_TFLOPS, 4)
-            else:
-                entry["frac_fp32_mfma"] = round(entry["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4)
-        elif c["bytes"]:
-            entry["gbs"] = round(c["bytes"] / (c["ms"] * 1e-3) / 1e9, 1)
-            entry["frac_hbm"] = round(entry["gbs"] / PEAK_HBM_GBS, 4)
-        kernels[name] = entry
-    dominant = max(classes, key=lambda n: classes[n]["ms"])
-    d = classes[dominant]
-    if d["flops"]:
-        achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
-        # the split kernel runs on fp16 MFMA: its algorithmic (float32-product) rate is
-        # priced against the dense fp16 peak, the issued rate is reported beside it
-        fp16 = dominant.startswith(("conv3d_x3", "conv3d_wino"))
-        peak = PEAK_FP16_MFMA_TFLOPS if fp16 else PEAK_FP32_MFMA_TFLOPS
-        roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 2),
-                    "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
-                    "traffic": measured_traffic(dominant)}
-        if fp16:
-            roofline["issued_frac"] = kernels[dominant].get(
-                "frac_bf16_mfma_issued", kernels[dominant].get("frac_fp16_mfma_issued"))
-    else:
-        achieved = d["bytes"] / (d["ms"] * 1e-3) / 1e9
-        roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
-                    "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
-                    "traffic": None}
+    kernels, roofline = kernel_table(classes, steps=args.steps)
     conv = [c for n, c in classes.items() if n.startswith(("conv3d_igemm", "conv3d_x3", "conv3d_wino"))]
     conv_flops = sum(c["flops"] for c in conv)
     conv_ms = sum(c["ms"] for c in conv)
