@@ -29,6 +29,13 @@ for _p in (str(ROOT / "nnunet-mlx_amd"), str(ROOT)):
 METRIC = "sliding-window voxels/s, liver 768²×101 8×TTA; conv3d MFMA % of peak"
 PEAK_FP32_MFMA_TFLOPS = 157.3
 PEAK_FP16_MFMA_TFLOPS = 2500.0   # dense
+# arithmetic the path computes in, per network precision
+DTYPES = {
+    "fp32": "f32",
+    "fp32-split": "f32 (fp16-split products, f32 accumulate)",
+    "bf16": "bf16 products, f32 accumulate",
+    "bf16-mixed": "bf16 products below full resolution, fp16-split at full resolution, f32 accumulate",
+}
 SPLIT_PRODUCTS = 3               # hi*hi + hi*lo + lo*hi per float32 product
 PEAK_HBM_GBS = 8000.0
 VOLUME_SHAPE = (1, 101, 768, 768)
@@ -502,7 +509,7 @@ def ensemble_workload(args) -> int:
         spec = ResidualEncoderUNetSpec(1, 3, (32, 64, 128, 256, 320, 320, 320), k3 * 7,
                                        ((1, 1, 1),) + ((2, 2, 2),) * 5 + ((2, 1, 1),),
                                        (1, 3, 4, 6, 6, 6, 6), (1,) * 6)
-        patch, seeds, axes, precision = (128, 160, 160), (4,), (), "bf16"
+        patch, seeds, axes, precision = (128, 160, 160), (4,), (), "bf16-mixed"
         volume = synthetic_ct()
     nets = []
     for seed in seeds:
@@ -543,8 +550,7 @@ def ensemble_workload(args) -> int:
         "value": round(voxels / step_s, 1), "unit": "voxels/s", "n_gpus": 1, "steps": args.steps,
         "warmup": max(args.warmup, 1), "ms_per_step": round(step_s * 1e3, 1),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "bf16 products, f32 accumulate" if precision == "bf16" else
-                 "f32 (fp16-split products, f32 accumulate)",
+        "dtype": DTYPES[precision],
         "data": "synthetic",
         "config": {"workload": f"{args.workload}: volume {list(volume.shape)} fp32 resident in HBM, "
                                f"{len(nets)} fold(s), patch {list(patch)}, step 0.5, "
@@ -640,7 +646,7 @@ def main() -> int:
                              "(torch.neg) whose HBM counters calibrate FETCH_SIZE/WRITE_SIZE")
     parser.add_argument("--summarize-profiles", metavar="DIR",
                         help="write the profiles/ summaries from rocprofv3 CSV output in DIR and exit")
-    parser.add_argument("--precision", choices=("fp32", "fp32-split", "bf16"), default="fp32-split",
+    parser.add_argument("--precision", choices=tuple(DTYPES), default="fp32-split",
                         help="convolution arithmetic: fp16-split products (3 per term) on fp16 "
                              "MFMA (default), or float32 products on fp32 MFMA; both float32 I/O "
                              "and accumulation, both within the float32 logits tolerance")
@@ -724,12 +730,12 @@ def main() -> int:
     conv_ms = sum(c["ms"] for c in conv)
     # 3x3x3 convolution rate against the float32-class MFMA peak of the arithmetic used
     conv_peak = {"fp32": PEAK_FP32_MFMA_TFLOPS, "fp32-split": PEAK_FP16_MFMA_TFLOPS / SPLIT_PRODUCTS,
-                 "bf16": PEAK_FP16_MFMA_TFLOPS}[args.precision]
+                 "bf16": PEAK_FP16_MFMA_TFLOPS, "bf16-mixed": PEAK_FP16_MFMA_TFLOPS}[args.precision]
     conv_frac = conv_flops / (conv_ms * 1e-3) / 1e12 / conv_peak if conv_ms else None
 
     alt = None
     if not args.no_alt:
-        other = "fp32" if args.precision in ("fp32-split", "bf16") else "fp32-split"
+        other = "fp32" if args.precision != "fp32" else "fp32-split"
         print(f"[bench] one step with precision {other}", file=sys.stderr, flush=True)
         alt_net = build_network(spec, precision=other)
         alt_net.load_weights(weights)
@@ -772,8 +778,7 @@ def main() -> int:
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": {"fp32": "f32", "fp32-split": "f32 (fp16-split products, f32 accumulate)",
-                  "bf16": "bf16 products, f32 accumulate"}[args.precision],
+        "dtype": DTYPES[args.precision],
         "precision": args.precision,
         "data": "synthetic",
         "config": {

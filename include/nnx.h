@@ -61,6 +61,14 @@ const char* nnx_version(void);
  * relative-L2 1.0e-2 to 2.3e-2 of the float32 logits, the distance the same bf16 rounding
  * reaches when emulated on the CPU; relative-L2 1e-2 is not met in general. */
 #define NNX_PRECISION_BF16 2
+/* bf16 below full resolution: as NNX_PRECISION_BF16 for every layer whose output is below
+ * the network's full resolution (encoder stages >= 1, decoder stages and transposed
+ * convolutions that end below full resolution), NNX_PRECISION_FP32_SPLIT for the
+ * full-resolution encoder stage (the stem included), the last decoder stage and the
+ * transposed convolution into it.  On the pancreas ResEnc-L (128 x 160 x 160) two thirds of
+ * the convolution FLOPs run in bf16 and the logits land at relative-L2 7.6e-3 of the
+ * float32 logits (all-bf16: 1.2e-2). */
+#define NNX_PRECISION_BF16_MIXED 3
 
 typedef struct nnx_spec {
   int arch;              /* NNX_ARCH_PLAIN or NNX_ARCH_RESIDUAL */
@@ -80,7 +88,7 @@ typedef struct nnx_spec {
   int stem_channels; /* residual only; 0 means features[0] */
   const int* bottleneck_channels; /* residual only: n_stages entries for BottleneckD, or NULL
                                      for BasicBlockD */
-  int precision;     /* NNX_PRECISION_FP32, NNX_PRECISION_FP32_SPLIT or NNX_PRECISION_BF16 */
+  int precision;     /* NNX_PRECISION_FP32, _FP32_SPLIT, _BF16 or _BF16_MIXED */
 } nnx_spec;
 
 typedef struct nnx_model nnx_model;

@@ -149,6 +149,8 @@ struct ConvNorm {
   bool first = false;   // reads the network input (kept in exact float32 products)
   bool split = false;   // packed for the split-fp16 kernel
   bool wino = false;    // packed for the Winograd split-fp16 kernel (within `split`)
+  int level = 0;        // resolution level of the output (0 = full resolution)
+  int arith = 0;        // split kernels' operand arithmetic (kArithSplit3 or kArithBf16)
   float scale = 1.f;    // power-of-two weight scale of the split packing
   DevBuf packed;
 };
@@ -157,7 +159,9 @@ struct Upsample {
   int cin = 0, cout = 0;
   int k[3] = {2, 2, 2};
   int pw = -1, pb = -1;
-  bool split = false;  // split-fp16 packing (fp32-split precision)
+  bool split = false;  // split-fp16 (or bf16) packing
+  int level = 0;       // resolution level of the output
+  int arith = 0;       // split kernels' operand arithmetic
   float scale = 1.f;
   DevBuf packed;
 };
@@ -225,8 +229,9 @@ int add_param(nnx_model* m, const std::string& name, std::vector<int64_t> shape)
   return id;
 }
 
-void declare_convnorm(nnx_model* m, ConvNorm& c, const std::string& prefix, int cin1, int cin2,
-                      int cout, const int* k, const int* s, bool act, bool bias) {
+void declare_convnorm(nnx_model* m, ConvNorm& c, const std::string& prefix, int level, int cin1,
+                      int cin2, int cout, const int* k, const int* s, bool act, bool bias) {
+  c.level = level;
   c.cin1 = cin1;
   c.cin2 = cin2;
   c.cout = cout;
@@ -263,6 +268,7 @@ void build_decoder(nnx_model* m) {
     const int below = m->features[src];
     const int skip = m->features[src - 1];
     Upsample& u = m->up[d];
+    u.level = src - 1;
     u.cin = below;
     u.cout = skip;
     for (int i = 0; i < 3; ++i) u.k[i] = m->strides[src * 3 + i];
@@ -271,7 +277,7 @@ void build_decoder(nnx_model* m) {
     m->dec[d].resize(m->dec_count[d]);
     for (int j = 0; j < m->dec_count[d]; ++j) {
       declare_convnorm(m, m->dec[d][j], "dec" + std::to_string(d) + ".block" + std::to_string(j),
-                       j == 0 ? skip : skip, j == 0 ? skip : 0, skip, &m->ksz[(src - 1) * 3],
+                       src - 1, j == 0 ? skip : skip, j == 0 ? skip : 0, skip, &m->ksz[(src - 1) * 3],
                        kUnit, true, m->conv_bias);
     }
     SegHead& sh = m->seg[d];
@@ -291,14 +297,14 @@ void build_graph(nnx_model* m) {
       m->enc[s].resize(m->enc_count[s]);
       for (int j = 0; j < m->enc_count[s]; ++j) {
         declare_convnorm(m, m->enc[s][j], "enc" + std::to_string(s) + ".block" + std::to_string(j),
-                         j == 0 ? cin : m->features[s], 0, m->features[s], &m->ksz[s * 3],
+                         s, j == 0 ? cin : m->features[s], 0, m->features[s], &m->ksz[s * 3],
                          j == 0 ? &m->strides[s * 3] : kUnit, true, m->conv_bias);
       }
       cin = m->features[s];
     }
   } else {
     const int stem_ch = m->stem_channels > 0 ? m->stem_channels : m->features[0];
-    declare_convnorm(m, m->stem, "stem", m->cin, 0, stem_ch, &m->ksz[0], kUnit, true, m->conv_bias);
+    declare_convnorm(m, m->stem, "stem", 0, m->cin, 0, stem_ch, &m->ksz[0], kUnit, true, m->conv_bias);
     m->res.resize(S);
     int cin = stem_ch;
     for (int s = 0; s < S; ++s) {
@@ -311,25 +317,25 @@ void build_graph(nnx_model* m) {
         const std::string pre = "res" + std::to_string(s) + ".block" + std::to_string(b);
         if (m->bottleneck.empty()) {
           rb.convs.resize(2);
-          declare_convnorm(m, rb.convs[0], pre + ".conv1", bin, 0, bout, &m->ksz[s * 3], stride,
+          declare_convnorm(m, rb.convs[0], pre + ".conv1", s, bin, 0, bout, &m->ksz[s * 3], stride,
                            true, m->conv_bias);
-          declare_convnorm(m, rb.convs[1], pre + ".conv2", bout, 0, bout, &m->ksz[s * 3], kUnit,
+          declare_convnorm(m, rb.convs[1], pre + ".conv2", s, bout, 0, bout, &m->ksz[s * 3], kUnit,
                            false, m->conv_bias);
         } else {
           const int bc = m->bottleneck[s];
           rb.convs.resize(3);
-          declare_convnorm(m, rb.convs[0], pre + ".conv1", bin, 0, bc, kUnit, kUnit, true,
+          declare_convnorm(m, rb.convs[0], pre + ".conv1", s, bin, 0, bc, kUnit, kUnit, true,
                            m->conv_bias);
-          declare_convnorm(m, rb.convs[1], pre + ".conv2", bc, 0, bc, &m->ksz[s * 3], stride, true,
+          declare_convnorm(m, rb.convs[1], pre + ".conv2", s, bc, 0, bc, &m->ksz[s * 3], stride, true,
                            m->conv_bias);
-          declare_convnorm(m, rb.convs[2], pre + ".conv3", bc, 0, bout, kUnit, kUnit, false,
+          declare_convnorm(m, rb.convs[2], pre + ".conv3", s, bc, 0, bout, kUnit, kUnit, false,
                            m->conv_bias);
         }
         rb.pool = !(stride[0] == 1 && stride[1] == 1 && stride[2] == 1);
         for (int i = 0; i < 3; ++i) rb.pool_k[i] = stride[i];
         rb.proj = bin != bout;
         if (rb.proj)
-          declare_convnorm(m, rb.projc, pre + ".proj", bin, 0, bout, kUnit, kUnit, false, false);
+          declare_convnorm(m, rb.projc, pre + ".proj", s, bin, 0, bout, kUnit, kUnit, false, false);
       }
       cin = m->features[s];
     }
@@ -341,30 +347,38 @@ const float* pdev(const nnx_model* m, int id) {
   return id < 0 ? nullptr : m->params[id].dev.as<float>();
 }
 
-// The split kernels' operand arithmetic for the model's precision.
-int split_arith(const nnx_model* m) {
-  return m->precision == NNX_PRECISION_BF16 ? kArithBf16 : kArithSplit3;
+// The split kernels' operand arithmetic of a layer at resolution `level`: bf16 in the bf16
+// precision, and in the mixed bf16 precision below full resolution; fp16-split otherwise.
+int layer_arith(const nnx_model* m, int level) {
+  if (m->precision == NNX_PRECISION_BF16) return kArithBf16;
+  if (m->precision == NNX_PRECISION_BF16_MIXED && level > 0) return kArithBf16;
+  return kArithSplit3;
 }
 bool uses_split_kernels(const nnx_model* m) {
-  return m->precision == NNX_PRECISION_FP32_SPLIT || m->precision == NNX_PRECISION_BF16;
+  return m->precision != NNX_PRECISION_FP32;
+}
+// Precisions whose first convolution with 1 or 2 input channels takes split products with a
+// per-tile input scale (the all-bf16 precision keeps float32 products there).
+bool split_first_conv(const nnx_model* m) {
+  return m->precision == NNX_PRECISION_FP32_SPLIT || m->precision == NNX_PRECISION_BF16_MIXED;
 }
 
-// The Winograd form serves the fp32-split precision's stride-1 3x3x3 layers it supports;
-// The stride-1 3x3x3 split layers with C_out % 32 == 0 and 16-channel input blocks run on
-// the Winograd kernel (fewer fp16 MFMA products per output, so less energy per output under
-// the chip's power cap); NNX_CONV_ALGO=direct keeps every layer on the direct implicit GEMM
-// (read when a model's weights are packed, for comparisons).
+// The stride-1 3x3x3 fp16-split layers with C_out % 32 == 0 and 16-channel input blocks run
+// on the Winograd kernel (fewer fp16 MFMA products per output, so less energy per output
+// under the chip's power cap); NNX_CONV_ALGO=direct keeps every layer on the direct implicit
+// GEMM (read when a model's weights are packed, for comparisons).
 bool winograd_enabled() {
   const char* v = std::getenv("NNX_CONV_ALGO");
   return !(v && std::string(v) == "direct");
 }
 
 void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
-  if (c.first && c.direct_multi && m->precision == NNX_PRECISION_FP32_SPLIT) c.direct = true;
+  if (c.first && c.direct_multi && split_first_conv(m)) c.direct = true;
   if (c.direct) {
-    // the direct kernel reads the reference layout; split products in the fp32-split
-    // precision (the bf16 precision keeps float32 products for the first convolution)
-    c.split = m->precision == NNX_PRECISION_FP32_SPLIT;
+    // the direct kernel reads the reference layout; split products in the fp32-split and
+    // mixed bf16 precisions (the bf16 precision keeps float32 products for the first
+    // convolution)
+    c.split = split_first_conv(m);
     c.scale = c.split ? split_weight_scale(m->params[c.pw].max_abs) : 0.f;
     return;
   }
@@ -376,7 +390,8 @@ void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
   // products with a per-tile input scale in the fp32-split precision).
   const int taps = c.k[0] * c.k[1] * c.k[2];
   c.split = uses_split_kernels(m) && !c.first && taps >= 8 && conv_x3_supported(c.k, c.s, c.cout);
-  if (c.split && m->precision == NNX_PRECISION_FP32_SPLIT && winograd_enabled()) {
+  c.arith = layer_arith(m, c.level);
+  if (c.split && c.arith == kArithSplit3 && winograd_enabled()) {
     const int probe[3] = {16, 16, 16};
     c.wino = conv_wino_supported(make_conv_geom(1, probe, c.k, c.s), c.cin1, c.cin2, c.cout);
   }
@@ -390,7 +405,7 @@ void pack_convnorm(nnx_model* m, ConvNorm& c, hipStream_t st) {
     c.scale = split_weight_scale(m->params[c.pw].max_abs);
     c.packed.ensure((size_t)conv_x3_packed_bytes(c.cout, c.k, c.cin1, c.cin2));
     conv_x3_pack_weight(pdev(m, c.pw), c.cout, c.k, c.cin1, c.cin2, c.scale, c.packed.ptr, st,
-                        split_arith(m));
+                        c.arith);
     return;
   }
   const int64_t n = conv_packed_floats(c.cout, c.k, c.cin1, c.cin2);
@@ -520,7 +535,7 @@ struct Runner {
                   c.cout, st, stats, x1.norm, x2.norm);
     else if (c.split)
       conv3d_x3(x1.data, c.cin1, x2.data, c.cin2, c.packed.ptr, c.scale, pdev(m, c.pb), out, g,
-                c.cout, st, stats, x1.norm, x2.norm, split_arith(m));
+                c.cout, st, stats, x1.norm, x2.norm, c.arith);
     else
       conv3d_igemm(x1.data, c.cin1, x2.data, c.cin2, c.packed.as<float>(), pdev(m, c.pb), out, g,
                    c.cout, st, stats, x1.norm, x2.norm);
@@ -559,7 +574,7 @@ struct Runner {
       if (!plan->planning) {
         if (u.split)
           tconv3d_x3(hidden.data, u.cin, u.packed.ptr, u.scale, pdev(m, u.pb), upbuf, n, hs.d,
-                     u.cout, u.k, st, split_arith(m));
+                     u.cout, u.k, st, u.arith);
         else
           tconv3d_gemm(hidden.data, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d,
                        u.cout, u.k, st);
@@ -842,7 +857,8 @@ int nnx_model_create(const nnx_spec* spec, nnx_model** out) {
     require(spec->arch == NNX_ARCH_PLAIN || spec->arch == NNX_ARCH_RESIDUAL,
             "unsupported network architecture");
     require(spec->precision == NNX_PRECISION_FP32 || spec->precision == NNX_PRECISION_FP32_SPLIT ||
-                spec->precision == NNX_PRECISION_BF16,
+                spec->precision == NNX_PRECISION_BF16 ||
+                spec->precision == NNX_PRECISION_BF16_MIXED,
             "unsupported precision");
     require(spec->input_channels >= 1 && spec->num_classes >= 1,
             "network needs input channels and at least one output");
@@ -962,11 +978,12 @@ int nnx_model_finalize(nnx_model* model) {
       for (auto& c : stage) pack_convnorm(model, c, st);
     for (auto& u : model->up) {
       u.split = uses_split_kernels(model);
+      u.arith = layer_arith(model, u.level);
       if (u.split) {
         u.scale = split_weight_scale(model->params[u.pw].max_abs);
         u.packed.ensure((size_t)tconv_x3_packed_bytes(u.cout, u.k, u.cin));
         tconv_x3_pack_weight(pdev(model, u.pw), u.cout, u.k, u.cin, u.scale, u.packed.ptr, st,
-                             split_arith(model));
+                             u.arith);
         continue;
       }
       const int64_t n = tconv_packed_floats(u.cout, u.k, u.cin);

@@ -33,6 +33,7 @@ NNX_ARCH_RESIDUAL = 1
 NNX_PRECISION_FP32 = 0
 NNX_PRECISION_FP32_SPLIT = 1
 NNX_PRECISION_BF16 = 2
+NNX_PRECISION_BF16_MIXED = 3
 NNX_NORM_NONE = 0
 NNX_NORM_CT = 1
 NNX_NORM_ZSCORE = 2

@@ -146,6 +146,23 @@ def test_pancreas_bf16_forward(device, fixtures):
         assert agree >= 0.98
 
 
+def test_pancreas_bf16_mixed_forward(device, fixtures):
+    """The pancreas ResEnc-L in "bf16-mixed" (bf16 below full resolution, fp16-split at full
+    resolution: two thirds of the convolution FLOPs in bf16) meets the north star's bf16 bar,
+    relative L2 <= 1e-2 of the float32 logits, on both probed items."""
+    got = _forward("pancreas", "bf16-mixed", device)
+    for item, logits in zip(cc.ITEMS, got):
+        mine = cc.probe(logits)["strided"]
+        ref = fixtures[f"pancreas__{item}__fp32__strided"]
+        dist = rel_l2(mine, ref)
+        agree = (mine.argmax(-1) == ref.argmax(-1)).mean()
+        print(f"pancreas bf16-mixed item {item}: vs float32 {dist:.3e}, argmax agreement "
+              f"{agree:.5f}", flush=True)
+        assert np.isfinite(mine).all()
+        assert dist <= 1e-2
+        assert agree >= 0.99
+
+
 def test_liver_item_matches_live_oracle(device):
     """One 128^3 liver item against the oracle run here (no fixture in between)."""
     from oracle.network import OracleNetwork

@@ -104,6 +104,29 @@ def test_forward_matches_oracle(device, name):
         net.close()
 
 
+@pytest.mark.parametrize("name", ["liver-32", "brats-4ch", "autopet-aniso", "resenc-L", "liver-128"])
+def test_bf16_mixed_is_closer_than_bf16(device, name):
+    """"bf16-mixed" keeps the full-resolution layers in fp16-split: its logits lie closer to
+    the float32 oracle than the all-bf16 network's (both distances printed)."""
+    spec, patch, batch, affine = CASES[name]
+    weights = random_weights(spec, seed=1, random_affine=affine)
+    x = np.random.default_rng(0).standard_normal((batch, *patch, spec.input_channels)).astype(np.float32)
+    residual = isinstance(spec, ResidualEncoderUNetSpec)
+    ref = OracleNetwork(spec, weights, residual=residual)(x)
+    dist = {}
+    for precision in ("bf16", "bf16-mixed"):
+        print(f"network case {name} precision={precision}", flush=True)
+        net = build_network(spec, precision=precision)
+        net.load_weights(weights)
+        got = net(torch.from_numpy(x).to(device)).cpu().numpy()
+        net.close()
+        assert np.isfinite(got).all()
+        dist[precision] = rel_l2(got, ref)
+    print(f"{name}: relative L2 to float32, bf16 {dist['bf16']:.3e}, bf16-mixed "
+          f"{dist['bf16-mixed']:.3e}", flush=True)
+    assert dist["bf16-mixed"] < dist["bf16"]
+
+
 @pytest.mark.parametrize("algo", ["winograd", "direct"])
 @pytest.mark.parametrize("name", ["liver-32", "brats-4ch", "autopet-aniso", "tiny-residual"])
 def test_conv_route_matches_oracle(device, monkeypatch, name, algo):

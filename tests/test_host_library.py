@@ -21,6 +21,19 @@ def test_header_declarations_match_binding_table():
     assert _declared_symbols() == set(_native.EXPORTED_SYMBOLS)
 
 
+def test_header_constants_match_the_binding():
+    """Every NNX_* integer constant include/nnx.h defines has the same value in _native."""
+    import re
+
+    from nnunet_mlx import _native
+
+    header = (Path(__file__).resolve().parents[1] / "include" / "nnx.h").read_text()
+    defines = dict(re.findall(r"^#define (NNX_\w+) (-?\d+)\s*$", header, re.M))
+    assert "NNX_PRECISION_BF16_MIXED" in defines
+    for name, value in defines.items():
+        assert getattr(_native, name) == int(value), name
+
+
 def test_library_loads_and_exports_every_symbol():
     from nnunet_mlx import _native
 
