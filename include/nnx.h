@@ -318,6 +318,35 @@ int nnx_tconv3d_bf16(const float* d_x, int cin, const void* d_packed, float scal
 int nnx_restore_labels(const void* d_logits, int half, int classes, const int* src_shape,
                        const int* dst_shape, uint16_t* d_labels, void* stream);
 
+/* Torch-grid resampling (the plans' resample_torch_fornnunet): one pass from in_size to
+ * out_size over three spatial axes, mode 0 linear (align_corners=False half-pixel grid,
+ * edge-clamped; the eight corner terms ((v * w0) * w1) * w2 summed in float64 in corner
+ * order and rounded once to float32), 1 nearest (floor(i * S / T)) or 2 nearest-exact
+ * (floor((i + 0.5) * S / T)), with float32 coordinates (scale = S / T in float32).
+ * Input float32, or float16 when `half` (widened exactly); output float32.  Strides
+ * (elements) are given for the channel and the three axes of input and output, so
+ * channels-first images and channels-last logits are read and written in place.  A
+ * separate-axis resampling is two calls: the planes across the axis with the plans' mode
+ * (that axis kept at its size), then the whole volume with aniso_axis_mode.  At most 2^31
+ * output elements.
+ * Replaces torch_resize / resample_torch (src/nnunet_mlx/kernels/metal_torch_resample.py:
+ * 136-215) for images and probabilities (is_seg false), as resample_probabilities_or_data
+ * calls it (src/nnunet_mlx/data/resampling.py:127-145). */
+int nnx_torch_resize(const void* d_in, int half, int channels, const int* in_size,
+                     const int64_t* in_strides, float* d_out, const int* out_size,
+                     const int64_t* out_strides, int mode, void* stream);
+
+/* One Torch-grid pass of every class of (strided) logits followed by the first-maximum
+ * argmax per output voxel, without a float intermediate: d_labels receives
+ * out_size[0] x out_size[1] x out_size[2] contiguous uint16 labels (1..65536 classes,
+ * at most 2^31 voxels).  The last pass of a Torch-plan class restoration.
+ * Replaces resample_probabilities_or_data (Torch resampler) followed by the argmax of
+ * the class-model export (src/nnunet_mlx/data/resampling.py:127-145,
+ * src/nnunet_mlx/prediction/export.py:137-202). */
+int nnx_torch_resize_argmax(const void* d_logits, int half, int classes, const int* in_size,
+                            const int64_t* in_strides, const int* out_size, int mode,
+                            uint16_t* d_labels, void* stream);
+
 /* Restoration along the plans' spline resampler, for the cases the trilinear entry does not
  * take (separate-axis resampling with order_z 0, or order 3): each class of the
  * channels-last logits (src_shape, classes) is resampled to dst_shape as

@@ -221,6 +221,15 @@ void resample_spline(const float* x, int channels, const int64_t* size, const in
 // Class-logit restoration along a spline plan: each class of channels-last logits
 // (src, classes) resampled like resample_spline (rounded to float16 when `half`), then the
 // first-maximum argmax into uint16 labels (dst); one class at a time through `work`.
+// Torch-grid resampling (nnx_torchgrid.hip): one pass, strided (channel, axis 0, 1, 2),
+// float32 or float16 (`half`) input, float32 output; torch_resize_argmax resamples every
+// class of a voxel and writes the first-maximum label (contiguous uint16 labels).
+void torch_resize(const void* in, bool half, int channels, const int* in_size,
+                  const int64_t* in_strides, float* out, const int* out_size,
+                  const int64_t* out_strides, int mode, hipStream_t st);
+void torch_resize_argmax(const void* in, bool half, int classes, const int* in_size,
+                         const int64_t* in_strides, const int* out_size, int mode,
+                         uint16_t* labels, hipStream_t st);
 size_t restore_labels_spline_workspace(const int* src, const int* dst, int separate_axis);
 void restore_labels_spline(const void* logits, bool half, int classes, const int* src,
                            const int* dst, int order, int separate_axis, void* work,

@@ -1303,6 +1303,24 @@ int nnx_restore_labels_spline(const void* d_logits, int half, int classes, const
   });
 }
 
+int nnx_torch_resize(const void* d_in, int half, int channels, const int* in_size,
+                     const int64_t* in_strides, float* d_out, const int* out_size,
+                     const int64_t* out_strides, int mode, void* stream) {
+  return guarded([&] {
+    torch_resize(d_in, half != 0, channels, in_size, in_strides, d_out, out_size, out_strides,
+                 mode, as_stream(stream));
+  });
+}
+
+int nnx_torch_resize_argmax(const void* d_logits, int half, int classes, const int* in_size,
+                            const int64_t* in_strides, const int* out_size, int mode,
+                            uint16_t* d_labels, void* stream) {
+  return guarded([&] {
+    torch_resize_argmax(d_logits, half != 0, classes, in_size, in_strides, out_size, mode,
+                        d_labels, as_stream(stream));
+  });
+}
+
 int nnx_nonzero_bbox(const float* d_data, int channels, const int64_t* size, int* d_bbox,
                      void* stream) {
   return guarded([&] { nonzero_bbox(d_data, channels, size, d_bbox, as_stream(stream)); });

@@ -210,6 +210,16 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
         [c_void_p, ctypes.c_int, ctypes.c_int, c_int_p, c_int_p, ctypes.c_int, ctypes.c_int,
          c_void_p, ctypes.c_size_t, c_void_p, c_void_p],
     ),
+    "nnx_torch_resize": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, ctypes.c_int, c_int_p, c_i64_p, c_void_p, c_int_p, c_i64_p,
+         ctypes.c_int, c_void_p],
+    ),
+    "nnx_torch_resize_argmax": (
+        ctypes.c_int,
+        [c_void_p, ctypes.c_int, ctypes.c_int, c_int_p, c_i64_p, c_int_p, ctypes.c_int, c_void_p,
+         c_void_p],
+    ),
     "nnx_nonzero_bbox": (ctypes.c_int, [c_void_p, ctypes.c_int, c_i64_p, c_void_p, c_void_p]),
     "nnx_nonzero_mask_filled": (
         ctypes.c_int, [c_void_p, ctypes.c_int, c_i64_p, c_i64_p, c_i64_p, c_void_p, c_void_p, c_void_p]

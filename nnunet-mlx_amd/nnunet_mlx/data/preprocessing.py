@@ -17,7 +17,9 @@ filled nonzero mask; mean and std accumulated in float64 and rounded to float32,
 few float32 steps of numpy's float32 statistics) and spline plans
 (``resample_data_or_seg_to_shape``; orders 1 and 3, order_z 0); RescaleTo01 and RGBTo01 run
 as the z-score form with host-computed (min, max - min) and (0, 255) after a device min/max
-(``nnx_channel_minmax``).  The Torch-grid resampler and cascade inputs raise
+(``nnx_channel_minmax``).  Torch-grid plans (``resample_torch_fornnunet``) resample with
+``nnx_torch_resize`` (one pass, or the planes and then the separate axis;
+src/nnunet_mlx/kernels/metal_torch_resample.py:195-215).  Cascade inputs raise
 ``ContractError`` rather than run elsewhere.
 """
 
@@ -30,7 +32,7 @@ from dataclasses import dataclass
 import numpy as np
 
 from nnunet_mlx import _native
-from nnunet_mlx.data.resampling import separate_z_axis, validate_spacing
+from nnunet_mlx.data.resampling import resample_torch_device, separate_z_axis, validate_spacing
 from nnunet_mlx.errors import ContractError
 from nnunet_mlx.plans import ResamplingContract, resolve_configuration
 
@@ -274,6 +276,15 @@ def preprocess_raw_case(data, properties: Mapping[str, object], plan: Preprocess
     if tuple(new_shape) == cropped_shape:
         return PreprocessedRawCase(cropped, None, result)
     contract = plan.data_resampling
+    if contract.function_name == "resample_torch_fornnunet":
+        _, axis = separate_z_axis(validate_spacing(original_spacing, name="current spacing"),
+                                  validate_spacing(target_spacing, name="new spacing"),
+                                  force=contract.force_separate_z,
+                                  threshold=contract.separate_z_anisotropy_threshold)
+        out = resample_torch_device(cropped, new_shape, axis=axis, mode=contract.mode,
+                                    aniso_axis_mode=contract.aniso_axis_mode)
+        _check_finite(lib, out, "resampling produced non-finite values")
+        return PreprocessedRawCase(out, None, result)
     if contract.function_name != "resample_data_or_seg_to_shape":
         raise ContractError(f"data resampling {contract.function_name!r} is not supported on the device path")
     separate, axis = separate_z_axis(validate_spacing(original_spacing, name="current spacing"),

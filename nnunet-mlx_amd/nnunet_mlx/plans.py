@@ -70,10 +70,19 @@ def patch_size(plans: Mapping[str, object], configuration: str) -> tuple[int, ..
 # restoration policy reads; the parser accepts the two upstream resampling functions and
 # keeps nnU-Net 2.8.1's defaults for omitted spline options (order 3, order_z 0,
 # force_separate_z False, anisotropy threshold 3; the Torch resampler: order 1, order_z 0,
-# force_separate_z None).
+# force_separate_z None, mode "linear", aniso_axis_mode "nearest-exact", seg_tiebreak
+# "nearest").
 
 
 RESAMPLING_FUNCTIONS = ("resample_data_or_seg_to_shape", "resample_torch_fornnunet")
+INTERPOLATION_MODES = ("linear", "nearest", "nearest-exact")
+SEG_TIEBREAKS = ("nearest", "lowest", "highest")
+TORCH_RESAMPLING_KWARGS = frozenset({
+    "is_seg", "force_separate_z", "seg_tiebreak", "mode", "aniso_axis_mode",
+    "separate_z_anisotropy_threshold", "num_threads", "device", "memefficient_seg_resampling"})
+SPLINE_RESAMPLING_KWARGS = frozenset({
+    "is_seg", "order", "order_z", "force_separate_z", "seg_tiebreak",
+    "separate_z_anisotropy_threshold"})
 
 
 @dataclass(frozen=True)
@@ -85,6 +94,9 @@ class ResamplingContract:
     order_z: int
     force_separate_z: bool | None
     separate_z_anisotropy_threshold: float = 3.0
+    mode: str = "linear"                    # Torch resampler: in-plane (or only) pass
+    aniso_axis_mode: str = "nearest-exact"  # Torch resampler: the separate axis's pass
+    seg_tiebreak: str | None = None
 
     @classmethod
     def from_configuration(cls, configuration: Mapping[str, object], *, field: str,
@@ -107,10 +119,33 @@ class ResamplingContract:
         threshold = kwargs.get("separate_z_anisotropy_threshold", 3.0)
         if isinstance(threshold, bool) or not isinstance(threshold, (int, float)) or threshold <= 0:
             raise ContractError(f"{field}.separate_z_anisotropy_threshold must be positive")
+        tiebreak = kwargs.get("seg_tiebreak")
+        if "seg_tiebreak" in kwargs and tiebreak not in SEG_TIEBREAKS:
+            raise ContractError(f"{field}.seg_tiebreak must be 'nearest', 'lowest', or 'highest'")
+        unknown = set(kwargs) - (TORCH_RESAMPLING_KWARGS if torch_resampling
+                                 else SPLINE_RESAMPLING_KWARGS)
+        if unknown:
+            kind = "resample_torch_fornnunet" if torch_resampling else "spline"
+            raise ContractError(f"{field}: unsupported {kind} kwargs: {', '.join(sorted(unknown))}")
         if torch_resampling:
-            return cls(name, 1, 0, force, float(threshold))
+            threads = kwargs.get("num_threads", 4)
+            if isinstance(threads, bool) or not isinstance(threads, int) or threads <= 0:
+                raise ContractError(f"{field}.num_threads must be a positive integer")
+            if not isinstance(kwargs.get("memefficient_seg_resampling", True), bool):
+                raise ContractError(f"{field}.memefficient_seg_resampling must be boolean")
+            if kwargs.get("device", "cpu") != "cpu":
+                raise ContractError(f"{field}.device supports only 'cpu' host resampling")
+            modes = {}
+            for key, default in (("mode", "linear"), ("aniso_axis_mode", "nearest-exact")):
+                modes[key] = kwargs.get(key, default)
+                if modes[key] not in INTERPOLATION_MODES:
+                    raise ContractError(
+                        f"{field}.{key} must be 'linear', 'nearest', or 'nearest-exact'")
+            return cls(name, 1, 0, force, float(threshold), mode=modes["mode"],
+                       aniso_axis_mode=modes["aniso_axis_mode"],
+                       seg_tiebreak=tiebreak or "nearest")
         order, order_z = kwargs.get("order", 3), kwargs.get("order_z", 0)
         for label, value in (("order", order), ("order_z", order_z)):
             if isinstance(value, bool) or not isinstance(value, int) or not 0 <= value <= 5:
                 raise ContractError(f"{field}.{label} must be an integer in [0, 5]")
-        return cls(name, order, order_z, force, float(threshold))
+        return cls(name, order, order_z, force, float(threshold), seg_tiebreak=tiebreak)

@@ -17,7 +17,10 @@ the interpolation, as the reference's host path stores them.
 restoration (src/nnunet_mlx/prediction/restore.py:28-158): spline plans with separate-axis
 resampling (``order_z`` 0) or ``order`` 3 run ``nnx_restore_labels_spline`` — each class
 resampled as ``resample_probabilities_or_data`` does (float64, clipped, one rounding to
-the logits' precision) and folded into the first-maximum argmax on the device.
+the logits' precision) and folded into the first-maximum argmax on the device; Torch-grid
+plans (``resample_torch_fornnunet``) run ``nnx_torch_resize`` for the in-plane pass of a
+separate-axis plan and ``nnx_torch_resize_argmax`` for the last pass and the argmax
+(float32 values, as the reference's Torch resampler returns them for float16 logits too).
 """
 
 from __future__ import annotations
@@ -28,7 +31,8 @@ import numpy as np
 import torch
 
 from nnunet_mlx import _native
-from nnunet_mlx.data.resampling import separate_z_axis, validate_spacing
+from nnunet_mlx.data.resampling import (resample_torch_argmax_device, separate_z_axis,
+                                        validate_spacing)
 from nnunet_mlx.errors import ContractError
 from nnunet_mlx.plans import ResamplingContract
 
@@ -181,9 +185,10 @@ def resample_class_logits_argmax_spline_device(logits: torch.Tensor, new_shape: 
 def restore_class_labels_device(logits: torch.Tensor, new_shape: Sequence[int],
                                 current_spacing: Sequence[float], new_spacing: Sequence[float],
                                 contract: ResamplingContract) -> torch.Tensor | None:
-    """Device uint16 labels on the target grid for every spline plan: the trilinear entry
-    where the reference's fused path applies, the spline entry for separate-axis or
-    order-3 plans (the reference's host restoration); ``None`` for other plans."""
+    """Device uint16 labels on the target grid: the trilinear entry where the reference's
+    fused path applies, the spline entry for separate-axis or order-3 spline plans, the
+    Torch-grid entries for Torch plans (the reference's host restoration); ``None`` for
+    spline plans with ``order_z`` above 0 or orders other than 1 and 3."""
     if logits.ndim != 4 or logits.dtype not in (torch.float32, torch.float16):
         raise ContractError("restoration requires float32 or float16 (D,H,W,C) logits")
     labels = resample_device_logits_argmax(logits, new_shape, current_spacing, new_spacing,
@@ -192,6 +197,17 @@ def restore_class_labels_device(logits: torch.Tensor, new_shape: Sequence[int],
         return labels
     classes = int(logits.shape[-1])
     source = tuple(int(v) for v in logits.shape[:3])
+    if contract.function_name == "resample_torch_fornnunet":
+        target = _target_shape(new_shape)
+        _validate_index_range((classes, *source), target)
+        _, axis = separate_z_axis(
+            validate_spacing(current_spacing, name="current spacing"),
+            validate_spacing(new_spacing, name="new spacing"),
+            force=contract.force_separate_z,
+            threshold=contract.separate_z_anisotropy_threshold,
+        )
+        return resample_torch_argmax_device(logits, target, axis=axis, mode=contract.mode,
+                                            aniso_axis_mode=contract.aniso_axis_mode)
     if not device_spline_restore_supported(source, new_shape, contract, classes=classes):
         return None
     separate, axis = separate_z_axis(

@@ -205,9 +205,9 @@ def test_preprocess_rejects_unsupported():
                            (False,), plan.intensity_properties, plan.data_resampling)
     with pytest.raises(ContractError):
         preprocess_raw_case(np.ones((1, 4, 4, 4), dtype=np.float32), {"spacing": [1, 1, 1]}, zplan)
-    tplan = ct_plan((2.0, 2.0, 2.0), resampling="resample_torch_fornnunet")
-    with pytest.raises(ContractError):
-        preprocess_raw_case(np.ones((1, 8, 8, 8), dtype=np.float32), {"spacing": [1, 1, 1]}, tplan)
+    with pytest.raises(ContractError):   # cascade inputs stay off the device path
+        preprocess_raw_case(np.ones((1, 8, 8, 8), dtype=np.float32), {"spacing": [1, 1, 1]}, plan,
+                            segmentation_previous_stage=np.zeros((1, 8, 8, 8), dtype=np.int16))
 
 
 def hollow_volume(rng, shape):

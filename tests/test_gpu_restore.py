@@ -122,8 +122,10 @@ def test_spline_restore_labels_match_oracle(device, source, target, classes, ord
 
 def test_restore_class_labels_device_policy(device):
     """Separate-axis plans restore on the device through the spline entry; the trilinear
-    entry keeps the cases the reference's fused path takes; other plans return None."""
+    entry keeps the cases the reference's fused path takes; Torch plans run the Torch-grid
+    entries; spline plans with order_z above 0 return None."""
     from nnunet_mlx.prediction.restore import restore_class_labels_device
+    from oracle import torch_resample as otr
     from oracle.restore import restore_labels_spline
 
     rng = np.random.default_rng(11)
@@ -137,8 +139,10 @@ def test_restore_class_labels_device_policy(device):
     got = restore_class_labels_device(dev, (12, 20, 20), (1.0, 1.0, 1.0), (0.8, 0.8, 0.8), spline)
     np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16), restore_labels(logits, (12, 20, 20)))
     torch_plan = ResamplingContract("resample_torch_fornnunet", 1, 0, None)
-    assert restore_class_labels_device(dev, (12, 20, 20), (1.0, 1.0, 1.0), (0.8, 0.8, 0.8),
-                                       torch_plan) is None
+    got = restore_class_labels_device(dev, (12, 20, 20), (1.0, 1.0, 1.0), (0.8, 0.8, 0.8),
+                                      torch_plan)
+    want = otr.resample(np.moveaxis(logits, -1, 0), (12, 20, 20), axis=None).argmax(axis=0)
+    np.testing.assert_array_equal(got.cpu().numpy().view(np.uint16), want)
     order_z1 = ResamplingContract("resample_data_or_seg_to_shape", 1, 1, None)
     assert restore_class_labels_device(dev, (25, 20, 20), (2.5, 0.8, 0.8), (1.0, 0.64, 0.64),
                                        order_z1) is None

@@ -39,9 +39,30 @@ def test_resampling_contract_parsing():
     torch_fn = ResamplingContract.from_configuration(
         {"f": "resample_torch_fornnunet", "f_kwargs": {}}, field="f", expected_is_seg=False)
     assert (torch_fn.order, torch_fn.force_separate_z) == (1, None)
+    assert (torch_fn.mode, torch_fn.aniso_axis_mode, torch_fn.seg_tiebreak) == (
+        "linear", "nearest-exact", "nearest")
+    upstream = ResamplingContract.from_configuration(
+        {"f": "resample_torch_fornnunet",
+         "f_kwargs": {"is_seg": False, "force_separate_z": None, "memefficient_seg_resampling": True,
+                      "seg_tiebreak": "lowest", "mode": "nearest", "aniso_axis_mode": "linear",
+                      "num_threads": 8, "device": "cpu", "separate_z_anisotropy_threshold": 2}},
+        field="f", expected_is_seg=False)
+    assert (upstream.mode, upstream.aniso_axis_mode, upstream.seg_tiebreak,
+            upstream.separate_z_anisotropy_threshold) == ("nearest", "linear", "lowest", 2.0)
+    spline_tie = ResamplingContract.from_configuration(
+        {"f": "resample_data_or_seg_to_shape", "f_kwargs": {"seg_tiebreak": "highest"}},
+        field="f", expected_is_seg=False)
+    assert spline_tie.seg_tiebreak == "highest"
+    torch_kwargs = lambda **kw: {"f": "resample_torch_fornnunet", "f_kwargs": kw}  # noqa: E731
     for bad in ({"f": "other", "f_kwargs": {}},
                 {"f": "resample_data_or_seg_to_shape", "f_kwargs": {"is_seg": True}},
-                {"f": "resample_data_or_seg_to_shape", "f_kwargs": {"order": 7}}):
+                {"f": "resample_data_or_seg_to_shape", "f_kwargs": {"order": 7}},
+                {"f": "resample_data_or_seg_to_shape", "f_kwargs": {"mode": "linear"}},
+                {"f": "resample_data_or_seg_to_shape", "f_kwargs": {"seg_tiebreak": "first"}},
+                torch_kwargs(order=1), torch_kwargs(mode="cubic"),
+                torch_kwargs(aniso_axis_mode="area"), torch_kwargs(num_threads=0),
+                torch_kwargs(num_threads=True), torch_kwargs(device="cuda"),
+                torch_kwargs(memefficient_seg_resampling=1), torch_kwargs(seg_tiebreak=None)):
         with pytest.raises(ContractError):
             ResamplingContract.from_configuration(bad, field="f", expected_is_seg=False)
 
