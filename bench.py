@@ -98,6 +98,20 @@ PREP_PLANS = {
 }
 
 
+# the same plan with upstream's Torch-grid resampler (resample_torch_fornnunet: linear in
+# plane, nearest-exact along the separate axis)
+TORCH_RESAMPLING = {"resampling_fn_data": "resample_torch_fornnunet",
+                    "resampling_fn_data_kwargs": {"is_seg": False, "force_separate_z": None,
+                                                  "memefficient_seg_resampling": False}}
+
+
+def prep_plans(resampler: str) -> dict:
+    plans = json.loads(json.dumps(PREP_PLANS))
+    if resampler == "torch":
+        plans["configurations"]["3d_fullres"].update(TORCH_RESAMPLING)
+    return plans
+
+
 def synthetic_raw_ct(shape=PREP_RAW_SHAPE, seed: int = 5):
     """int16 CT: air (-1000 HU) outside an elliptic body section, N(40, 60) HU inside."""
     import numpy as np
@@ -123,7 +137,8 @@ def preprocess_workload(args) -> int:
 
     torch.cuda.set_device(0)
     raw = synthetic_raw_ct()
-    plan = PreprocessPlan.from_plans(PREP_PLANS, "3d_fullres")
+    torch_grid = args.resampler == "torch"
+    plan = PreprocessPlan.from_plans(prep_plans(args.resampler), "3d_fullres")
     props = {"spacing": list(PREP_SPACING)}
     d_raw = torch.from_numpy(raw).cuda()
     for _ in range(max(args.warmup, 1)):
@@ -169,30 +184,135 @@ def preprocess_workload(args) -> int:
         base_s = time.perf_counter() - t0
         sample = 12
         new_shape = tuple(int(s) for s in out.data.shape[1:])
+        sample_shape = (round(new_shape[0] * sample / crop.shape[1]), *new_shape[1:])
         t0 = time.perf_counter()
-        op.resample_data(norm[:, :sample], (round(new_shape[0] * sample / crop.shape[1]),
-                                            *new_shape[1:]), separate_axis=0)
+        if torch_grid:
+            from oracle import torch_resample as otr
+
+            otr.resample(norm[:, :sample], sample_shape, axis=0)
+        else:
+            op.resample_data(norm[:, :sample], sample_shape, separate_axis=0)
         sample_s = time.perf_counter() - t0
         case_s = base_s + sample_s * crop.shape[1] / sample
+        kind = "Torch-grid (linear, nearest-exact axis)" if torch_grid else "cubic"
         cpu = {"value": round(out_vox / case_s, 1), "unit": "voxels/s", "cores": 1, "kind": "port",
                "sample": f"oracle (numpy) crop + CT normalisation of the whole case ({base_s:.2f} s) "
-                         f"and its separate-axis cubic resampling of {sample} of "
+                         f"and its separate-axis {kind} resampling of {sample} of "
                          f"{crop.shape[1]} slices ({sample_s:.2f} s), scaled to the case: "
                          f"{case_s:.1f} s per case"}
+    resampling = ("Torch-grid resampler, linear in plane, nearest-exact separate axis"
+                  if torch_grid else "cubic spline, separate axis")
     line = {
         "metric": "raw-case preprocessing output voxels/s, liver CT 512x512x120 int16 -> "
-                  "300x534x534 (CT normalisation, cubic spline, separate axis)",
+                  f"300x534x534 (CT normalisation, {resampling})",
         "value": round(out_vox / step_s, 1), "unit": "voxels/s", "n_gpus": 1, "steps": args.steps,
         "warmup": max(args.warmup, 1), "ms_per_step": round(step_s * 1e3, 3),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
-        "dtype": "f32 data, f64 spline arithmetic", "data": "synthetic",
+        "dtype": "f32 data, f64 " + ("corner sums" if torch_grid else "spline arithmetic"),
+        "data": "synthetic",
         "config": {"workload": "raw CT (1, 120, 512, 512) int16 resident in HBM at spacing "
                                "(2.5, 0.8, 0.8) mm -> plans spacing (1.0, 0.7676, 0.7676) mm",
-                   "output_shape": list(out.data.shape)},
+                   "resampler": args.resampler, "output_shape": list(out.data.shape)},
         "pcie_inclusive_voxels_per_s": round(out_vox / pcie_s, 1),
         "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
     }
     del host_out
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def restore_workload(args) -> int:
+    """Class-logit restoration of the liver raw case on the GPU: float16 channels-last
+    logits of the preprocessed grid (300 x 534 x 534 x 3, what the sliding window leaves on
+    the device) back to the cropped original grid (120 x 512 x 512) at spacing
+    (1.0, 0.7676, 0.7676) -> (2.5, 0.8, 0.8) mm (separate axis 0), with the first-maximum
+    argmax; the plans' probability resampler is the order-1 spline or the Torch-grid
+    resampler (``--resampler``).  value = output voxels per second."""
+    import numpy as np
+    import torch
+
+    from nnunet_mlx import _native
+    from nnunet_mlx.plans import ResamplingContract
+    from nnunet_mlx.prediction.restore import restore_class_labels_device
+
+    torch.cuda.set_device(0)
+    torch_grid = args.resampler == "torch"
+    name = "resample_torch_fornnunet" if torch_grid else "resample_data_or_seg_to_shape"
+    kwargs = {"is_seg": False, "force_separate_z": None}
+    if not torch_grid:
+        kwargs.update(order=1, order_z=0)
+    contract = ResamplingContract.from_configuration(
+        {"f": name, "f_kwargs": kwargs}, field="f", expected_is_seg=False)
+    source, target = (300, 534, 534), (120, 512, 512)
+    current, original = (1.0, 0.7676, 0.7676), PREP_SPACING
+    rng = np.random.default_rng(3)
+    # smooth-ish logits: three classes whose maxima form regions, as a network leaves them
+    coarse = torch.from_numpy(rng.standard_normal((3, 38, 67, 67)).astype(np.float32))
+    logits = torch.nn.functional.interpolate(coarse[None].cuda(), size=source, mode="trilinear",
+                                             align_corners=False)[0]
+    logits = (logits * 4).permute(1, 2, 3, 0).contiguous().half()
+    del coarse
+    for _ in range(max(args.warmup, 1)):
+        labels = restore_class_labels_device(logits, target, current, original, contract)
+    torch.cuda.synchronize()
+    with _native.KernelProfile() as prof:
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            labels = restore_class_labels_device(logits, target, current, original, contract)
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / args.steps
+    out_vox = int(np.prod(target))
+    kernels = {}
+    for kname, c in sorted(prof.classes.items(), key=lambda kv: -kv[1]["ms"]):
+        entry = {"launches": c["launches"], "ms": round(c["ms"] / args.steps, 4)}
+        if c["bytes"]:
+            entry["gbs"] = round(c["bytes"] / (c["ms"] * 1e-3) / 1e9, 1)
+            entry["frac_hbm"] = round(entry["gbs"] / PEAK_HBM_GBS, 4)
+        kernels[kname] = entry
+    dominant = max(prof.classes, key=lambda n: prof.classes[n]["ms"])
+    d = prof.classes[dominant]
+    achieved = d["bytes"] / (d["ms"] * 1e-3) / 1e9
+    roofline = {"kernel": dominant, "bound": "hbm", "achieved": round(achieved, 1),
+                "peak": PEAK_HBM_GBS, "unit": "GB/s", "frac": round(achieved / PEAK_HBM_GBS, 4),
+                "traffic": None}
+    cpu = None
+    if not args.no_cpu_baseline:
+        # bounded sample: the oracle's restoration of the first 30 of 300 source slices
+        # (-> 12 target slices; the separate-axis pass is nearest along axis 0, so slabs
+        # are independent), scaled to the case
+        host = logits[:30].float().cpu().numpy()
+        t0 = time.perf_counter()
+        if torch_grid:
+            from oracle import torch_resample as otr
+
+            otr.resample(np.moveaxis(host, -1, 0), (12, *target[1:]), axis=0).argmax(axis=0)
+        else:
+            from oracle.restore import restore_labels_spline
+
+            restore_labels_spline(host.astype(np.float16), (12, *target[1:]), order=1,
+                                  separate_axis=0)
+        sample_s = time.perf_counter() - t0
+        case_s = sample_s * target[0] / 12
+        cpu = {"value": round(out_vox / case_s, 1), "unit": "voxels/s", "cores": 1, "kind": "port",
+               "sample": f"oracle (numpy) restoration of 30 of 300 source slices -> 12 of 120 "
+                         f"target slices ({sample_s:.2f} s), scaled to the case: "
+                         f"{case_s:.1f} s per case"}
+    resampling = ("Torch-grid resampler, linear in plane, nearest-exact separate axis"
+                  if torch_grid else "order-1 spline, separate axis")
+    line = {
+        "metric": "class-logit restoration output voxels/s, liver case 300x534x534x3 float16 "
+                  f"logits -> 120x512x512 labels ({resampling}, first-maximum argmax)",
+        "value": round(out_vox / step_s, 1), "unit": "voxels/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": max(args.warmup, 1), "ms_per_step": round(step_s * 1e3, 3),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "f16 logits, f64 interpolation", "data": "synthetic",
+        "config": {"workload": "float16 logits (300, 534, 534, 3) resident in HBM, spacing "
+                               "(1.0, 0.7676, 0.7676) -> (2.5, 0.8, 0.8) mm",
+                   "resampler": args.resampler,
+                   "label_counts": torch.bincount(labels.view(torch.int16).long().flatten(),
+                                                  minlength=3).tolist()},
+        "roofline": roofline, "cpu_baseline": cpu, "kernels": kernels,
+    }
     print(json.dumps(line), flush=True)
     return 0
 
@@ -654,12 +774,17 @@ def main() -> int:
                         help="skip the one-step measurement of the other precision")
     parser.add_argument("--shape", type=int, nargs=3, default=VOLUME_SHAPE[1:],
                         help="volume size (Z Y X); the default is the liver case")
+    parser.add_argument("--resampler", choices=("spline", "torch"), default="spline",
+                        help="preprocess-ct / restore-ct: the plans' resampler (order-3 / "
+                             "order-1 spline, or upstream's Torch-grid resampler)")
     parser.add_argument("--workload", choices=("liver-sw", "preprocess-ct", "liver-raw-case",
-                                               "brats-sw", "autopet-sw", "pancreas-sw"),
+                                               "restore-ct", "brats-sw", "autopet-sw",
+                                               "pancreas-sw"),
                         default="liver-sw",
                         help="liver-sw: the sliding-window case (default); preprocess-ct: raw "
                              "CT preprocessing on the GPU; liver-raw-case: raw CT to labels on "
                              "the raw grid (preprocessing, sliding window, restoration); "
+                             "restore-ct: class-logit restoration of the liver case; "
                              "brats-sw / autopet-sw / pancreas-sw: the multi-fold and bf16 "
                              "configurations")
     args = parser.parse_args()
@@ -675,6 +800,8 @@ def main() -> int:
         return preprocess_workload(args)
     if args.workload == "liver-raw-case":
         return raw_case_workload(args)
+    if args.workload == "restore-ct":
+        return restore_workload(args)
     if args.workload in ("brats-sw", "autopet-sw", "pancreas-sw"):
         return ensemble_workload(args)
 

@@ -347,6 +347,9 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
   // (r2 - r1, r1 - r3), i.e. Q0 = R[2p] - R[2 - p] and Q1 = R[1] + sg R[2 + p] with sg = +-1
   // (fma: one rounding, as the add or subtract)
   const float sg = p ? -1.f : 1.f;
+  // the host launches only layers with input channels (chunks >= 1): without this the
+  // compiler keeps a zeroed copy of the accumulators for the loop-skipping path as well
+  __builtin_assume(a.chunks > 0);
   for (int chunk = 0; chunk < a.chunks; ++chunk) {
     const int buf = chunk & 1;
     __builtin_amdgcn_s_waitcnt(0);  // this thread's halo lines and B operands have landed
