@@ -707,9 +707,14 @@ def raw_case_workload(args) -> int:
                                            seeds=(1,), labels=("liver", "tumor"))
         plans = json.loads((folder / "plans.json").read_text())
         cfg = plans["configurations"]["3d_fullres"]
-        cfg.update(PREP_PLANS["configurations"]["3d_fullres"])
+        prep = prep_plans(args.resampler)
+        cfg.update(prep["configurations"]["3d_fullres"])
+        if args.resampler == "torch":
+            cfg["resampling_fn_probabilities"] = "resample_torch_fornnunet"
+            cfg["resampling_fn_probabilities_kwargs"] = dict(
+                TORCH_RESAMPLING["resampling_fn_data_kwargs"])
         plans["foreground_intensity_properties_per_channel"] = \
-            PREP_PLANS["foreground_intensity_properties_per_channel"]
+            prep["foreground_intensity_properties_per_channel"]
         (folder / "plans.json").write_text(json.dumps(plans))
         bundle = load_model_bundle(folder, configuration="3d_fullres")
     predictor = ModelFolderPredictor(bundle, accumulation="nnunet-fp16", step_fraction=0.5,
@@ -733,7 +738,8 @@ def raw_case_workload(args) -> int:
     line = {
         "metric": "raw-case voxels/s, liver CT 512x512x120 int16 -> labels on the raw grid "
                   "(GPU preprocessing, 8x TTA sliding window, fp16 accumulation, "
-                  "separate-axis restoration)",
+                  "separate-axis restoration"
+                  + (", Torch-grid resampler)" if args.resampler == "torch" else ")"),
         "value": round(voxels / step_s, 1), "unit": "voxels/s", "n_gpus": 1,
         "steps": args.steps, "warmup": max(args.warmup, 1), "ms_per_step": round(step_s * 1e3, 1),
         "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
@@ -741,6 +747,7 @@ def raw_case_workload(args) -> int:
         "config": {"workload": "raw CT (1, 120, 512, 512) int16 resident in HBM at spacing "
                                "(2.5, 0.8, 0.8) mm, liver 3d_fullres network (random weights), "
                                "patch 128^3, step 0.5, mirror axes (0, 1, 2)",
+                   "resampler": args.resampler,
                    "preprocessed_shape": list(details["preprocessed_shape"]),
                    "label_counts": np.bincount(labels.ravel(), minlength=3).tolist()},
         "stages_s": {k: round(v, 4) for k, v in stages.items()},
@@ -775,8 +782,8 @@ def main() -> int:
     parser.add_argument("--shape", type=int, nargs=3, default=VOLUME_SHAPE[1:],
                         help="volume size (Z Y X); the default is the liver case")
     parser.add_argument("--resampler", choices=("spline", "torch"), default="spline",
-                        help="preprocess-ct / restore-ct: the plans' resampler (order-3 / "
-                             "order-1 spline, or upstream's Torch-grid resampler)")
+                        help="preprocess-ct / restore-ct / liver-raw-case: the plans' resampler "
+                             "(order-3 / order-1 spline, or upstream's Torch-grid resampler)")
     parser.add_argument("--workload", choices=("liver-sw", "preprocess-ct", "liver-raw-case",
                                                "restore-ct", "brats-sw", "autopet-sw",
                                                "pancreas-sw"),

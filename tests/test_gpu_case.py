@@ -1,9 +1,10 @@
 """Raw case -> label image on the GPU against the oracle composition of the same steps.
 
 The oracle chain: nonzero crop, CT normalisation and spline resampling
-(``oracle.preprocess``), the float32 network (``oracle.network``) under the sliding window
-with float16 accumulation (``oracle.sliding_window``), spline restoration with the
-first-maximum argmax (``oracle.restore``), then uncrop.  The device path differs from it
+(``oracle.preprocess``; Torch-grid plans: ``oracle.torch_resample``), the float32 network
+(``oracle.network``) under the sliding window with float16 accumulation
+(``oracle.sliding_window``), spline restoration with the first-maximum argmax
+(``oracle.restore``; Torch-grid plans: the Torch-grid resampler and argmax), then uncrop.  The device path differs from it
 only by float32 summation order inside the network, so labels may differ where two classes
 are within a rounding of each other: the bar is 99.9 % identical voxels, identical outside
 the crop box.
@@ -101,6 +102,57 @@ def test_run_writes_the_oracle_labels(tmp_path):
     assert details["accumulation"] == "nnunet-fp16" and details["folds"] == [0]
     assert details["preprocessed_shape"][1:] == [18, 37, 34]
     assert result["artifacts"]["mask"]["labels"][1]["name"] == "liver"
+
+
+TORCH_KWARGS = {"is_seg": False, "force_separate_z": None, "memefficient_seg_resampling": False}
+
+
+def test_run_with_torch_grid_plans(tmp_path):
+    """Plans with upstream's Torch-grid resampler for the image and the probabilities
+    (linear in plane, nearest-exact along the separate axis): the device case path against
+    the oracle chain with oracle.torch_resample in both places."""
+    import nnunet_mlx
+    from nnunet_mlx.data.resampling import separate_z_axis
+    from oracle import torch_resample as otr
+
+    folder = ct_model_folder(tmp_path / "model")
+    plans = json.loads((folder / "plans.json").read_text())
+    cfg = plans["configurations"]["3d_fullres"]
+    for field in ("resampling_fn_data", "resampling_fn_probabilities"):
+        cfg[field] = "resample_torch_fornnunet"
+        cfg[f"{field}_kwargs"] = dict(TORCH_KWARGS)
+    (folder / "plans.json").write_text(json.dumps(plans))
+    ct = synthetic_ct(tmp_path / "case_0000.nii.gz", seed=5)
+    print("raw case: run() on a 12x40x36 CT, Torch-grid plans", flush=True)
+    result = nnunet_mlx.run(weights_path=folder, image_paths=[tmp_path / "case_0000.nii.gz"],
+                            output_dir=tmp_path / "out")
+    mask = nifti.read_nifti(result["outputs"]["mask"])
+
+    raw = ct.astype(np.float32)[None]
+    bbox = op.nonzero_bbox(raw)
+    crop = raw[(slice(None), *(slice(a, b) for a, b in bbox))]
+    norm = op.ct_normalize(crop[0], CT["mean"], CT["std"], CT["percentile_00_5"],
+                           CT["percentile_99_5"])[None]
+    original = tuple(reversed(IMAGE_SPACING_XYZ))
+    new_shape = tuple(round(o / n * s) for o, n, s in zip(original, TARGET_SPACING, crop.shape[1:]))
+    _, axis = separate_z_axis(original, TARGET_SPACING, force=None)
+    data = otr.resample(norm, new_shape, axis=axis)
+    nets = [OracleNetwork(SPEC, random_weights(SPEC, 0))]
+    logits, _ = osw.predict(nets, data, PATCH, num_classes=3, axes=(0, 1, 2),
+                            step_fraction=0.5, accumulation="nnunet-fp16")
+    _, back_axis = separate_z_axis(TARGET_SPACING, original, force=None)
+    values = otr.resample(np.moveaxis(np.asarray(logits, dtype=np.float32), -1, 0),
+                          crop.shape[1:], axis=back_axis)
+    want = np.zeros(ct.shape, dtype=np.uint16)
+    want[tuple(slice(a, b) for a, b in bbox)] = values.argmax(axis=0)
+    assert result["details"]["preprocessed_shape"][1:] == list(new_shape)
+    agree = (mask.array == want).mean()
+    print(f"label agreement {agree:.6f}, classes {np.bincount(want.ravel(), minlength=3)}, "
+          f"axes {axis}/{back_axis}", flush=True)
+    assert agree >= 0.999
+    outside = np.ones(ct.shape, dtype=bool)
+    outside[tuple(slice(a, b) for a, b in bbox)] = False
+    assert (mask.array[outside] == 0).all()
 
 
 def test_loaded_model_and_named_model_agree_with_run(tmp_path):
