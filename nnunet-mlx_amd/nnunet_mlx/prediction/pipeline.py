@@ -6,7 +6,7 @@ label restoration of ``restore_device_segmentation`` / ``restore_prediction``
 (src/nnunet_mlx/prediction/export.py:265-373, src/nnunet_mlx/prediction/restore.py:28-158).
 
 One case flows: read the channel images (host) -> ``preprocess_raw_case`` (transpose, crop
-to nonzero, CT normalisation, spline resampling; HIP) -> fold-averaged sliding-window
+to nonzero, normalisation, spline or Torch-grid resampling; HIP) -> fold-averaged sliding-window
 logits (HIP, left on the device) -> class-logit restoration to the cropped original grid
 with the first-maximum argmax (HIP) -> uint16 labels to the host -> uncrop and inverse
 transpose -> label image with the input's geometry.  Only the raw volume goes to the
