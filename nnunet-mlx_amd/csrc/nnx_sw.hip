@@ -20,43 +20,55 @@ struct Flips {
 __device__ __forceinline__ float mul_rn(float a, float b) { return __fmul_rn(a, b); }
 __device__ __forceinline__ float add_rn(float a, float b) { return __fadd_rn(a, b); }
 
-// A workgroup per patch row (y, z) = (blockIdx.x, blockIdx.y), its threads along x: every
-// view's flipped source row is uniform over the workgroup, only x flips per lane.  Reads
-// the source voxel of each channel (zero outside the volume) and writes the channels-last
-// row of every view.
+// Workgroups of one or more patch rows (y along threadIdx.y, z = blockIdx.y), threads along
+// the row: every view's flipped source row is uniform over a row's threads, only x flips per
+// lane.  Reads the source voxel of each channel (zero outside the volume) and writes the
+// channels-last row of every view.  A thread takes a run of V consecutive (x, channel)
+// elements of the row; with V = 4 (row length a multiple of 4 floats and a 16-byte aligned
+// output: checked by the host) each view takes one 16-byte store.
+template <int V>
 __global__ __launch_bounds__(512) void gather_flip_kernel(
     const float* __restrict__ vol, int C, int64_t Z, int64_t Y, int64_t X, int pz, int py, int px,
     int oz, int oy, int ox, int PZ, int PY, int PX, Flips flips, int nviews,
     float* __restrict__ out) {
-  const int y = blockIdx.x, z = blockIdx.y;
+  typedef float run_t __attribute__((ext_vector_type(V)));
+  const int y = blockIdx.x * blockDim.y + threadIdx.y, z = blockIdx.y;
+  if (y >= PY) return;
   const int64_t pvox = (int64_t)PZ * PY * PX;
   const int64_t zyx = Z * Y * X;
   const int64_t prow = ((int64_t)z * PY + y) * PX;
-  for (int x = threadIdx.x; x < PX; x += blockDim.x) {
-    for (int c = 0; c < C; ++c) {
-      // every view's value first (loads in flight together), then the stores
-      float val[8];
+  const int n = PX * C;
+  for (int e0 = V * threadIdx.x; e0 < n; e0 += V * blockDim.x) {
+    // every view's values first (loads in flight together), then the stores
+    run_t val[8];
 #pragma unroll
-      for (int v = 0; v < 8; ++v) {
-        val[v] = 0.f;
-        if (v < nviews) {
-          const int f = flips.f[v];
-          const int64_t gz = (int64_t)oz + ((f & 1) ? PZ - 1 - z : z) - pz;
-          const int64_t gy = (int64_t)oy + ((f & 2) ? PY - 1 - y : y) - py;
-          const int64_t gx = (int64_t)ox + ((f & 4) ? PX - 1 - x : x) - px;
-          if (gz >= 0 && gz < Z && gy >= 0 && gy < Y && gx >= 0 && gx < X)
-            val[v] = vol[(int64_t)c * zyx + (gz * Y + gy) * X + gx];
+    for (int v = 0; v < 8; ++v) {
+#pragma unroll
+      for (int i = 0; i < V; ++i) val[v][i] = 0.f;
+      if (v < nviews) {
+        const int f = flips.f[v];
+        const int64_t gz = (int64_t)oz + ((f & 1) ? PZ - 1 - z : z) - pz;
+        const int64_t gy = (int64_t)oy + ((f & 2) ? PY - 1 - y : y) - py;
+        if (gz >= 0 && gz < Z && gy >= 0 && gy < Y) {
+          const float* src = vol + (gz * Y + gy) * X;
+#pragma unroll
+          for (int i = 0; i < V; ++i) {
+            const int e = e0 + i, x = e / C, c = e - x * C;
+            const int64_t gx = (int64_t)ox + ((f & 4) ? PX - 1 - x : x) - px;
+            if (gx >= 0 && gx < X) val[v][i] = src[(int64_t)c * zyx + gx];
+          }
         }
       }
-#pragma unroll
-      for (int v = 0; v < 8; ++v)
-        if (v < nviews) out[((int64_t)v * pvox + prow + x) * C + c] = val[v];
     }
+#pragma unroll
+    for (int v = 0; v < 8; ++v)
+      if (v < nviews) *reinterpret_cast<run_t*>(out + ((int64_t)v * pvox + prow) * C + e0) = val[v];
   }
 }
 
-// A workgroup per patch row (y, z), its threads along the row's (x, class) pairs: each
-// view's flipped source row is uniform over the workgroup, consecutive lanes read
+// Workgroups of one or more patch rows (y along threadIdx.y, z = blockIdx.y), threads along
+// the row's (x, class) pairs: each view's flipped source row is uniform over a row's
+// threads, consecutive lanes read
 // consecutive floats of the prediction rows and update consecutive accumulator elements
 // (whole cache lines); the class-0 lane of a voxel updates its normaliser.
 template <bool kHalf>
@@ -64,7 +76,8 @@ __global__ __launch_bounds__(512) void accumulate_kernel(
     const float* __restrict__ pred, int nviews, Flips flips, int K, int PZ, int PY, int PX,
     const void* __restrict__ gaussian, int oz, int oy, int ox, int64_t QY, int64_t QX,
     void* __restrict__ acc, void* __restrict__ norm) {
-  const int y = blockIdx.x, z = blockIdx.y;
+  const int y = blockIdx.x * blockDim.y + threadIdx.y, z = blockIdx.y;
+  if (y >= PY) return;
   const int64_t pvox = (int64_t)PZ * PY * PX;
   const int64_t prow = ((int64_t)z * PY + y) * PX;
   const int64_t qrow = (((int64_t)oz + z) * QY + (oy + y)) * QX + ox;
@@ -196,8 +209,14 @@ __global__ __launch_bounds__(256) void fold_finalize_kernel(const void* __restri
   if (threadIdx.x == 0 && block_invalid && invalid_count) atomicAdd(invalid_count, block_invalid);
 }
 
-// Threads of a one-row workgroup: the row's elements rounded up to whole waves, at most 512.
-unsigned row_threads(int64_t n) { return (unsigned)std::min<int64_t>(512, std::max<int64_t>(64, ceil_div(n, 64) * 64)); }
+// Threads along a row: the row's elements rounded up to whole multiples of `unit` (a wave,
+// or half a wave where two short rows share one), at most `cap`; and rows a workgroup
+// (along y): up to 512 threads in all, so that short rows do not make a workgroup per row.
+unsigned row_threads(int64_t n, int64_t cap = 512, int64_t unit = 64) {
+  return (unsigned)std::min<int64_t>(cap, std::max<int64_t>(unit, ceil_div(n, unit) * unit));
+}
+unsigned rows_per_group(unsigned lanes) { return std::max(1u, std::min(16u, 512u / lanes)); }
+constexpr int64_t kAccLanes = 128;  // accumulate: lanes along a row
 
 unsigned grid_for(int64_t n) { return (unsigned)std::max<int64_t>(1, std::min<int64_t>(ceil_div(n, 256), 65536)); }
 
@@ -222,10 +241,20 @@ void sw_gather_flip(const float* vol, int channels, const int64_t* size, const i
   const int64_t n = (int64_t)patch[0] * patch[1] * patch[2] * nviews;
   require(patch[1] <= 65535 && patch[0] <= 65535, "patch rows exceed the launch grid");
   ProfScope prof("sw_gather_flip", 0.0, 4.0 * (double)n / nviews * channels * (1 + nviews), st);
-  hipLaunchKernelGGL(gather_flip_kernel, dim3(patch[1], patch[0]), dim3(row_threads(patch[2])), 0,
-                     st, vol, channels,
-                     size[0], size[1], size[2], pad_before[0], pad_before[1], pad_before[2],
-                     offset[0], offset[1], offset[2], patch[0], patch[1], patch[2], f, nviews, out);
+  // runs of 4 floats where every view's row starts 16-byte aligned, else single floats
+  const int64_t row = (int64_t)patch[2] * channels;
+  const bool vec = row % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
+  const unsigned lanes = row_threads(ceil_div(row, vec ? 4 : 1), 128, 32);
+  const unsigned rows = rows_per_group(lanes);
+  const dim3 grid((unsigned)ceil_div(patch[1], rows), patch[0]), block(lanes, rows);
+  if (vec)
+    hipLaunchKernelGGL(gather_flip_kernel<4>, grid, block, 0, st, vol, channels, size[0], size[1],
+                       size[2], pad_before[0], pad_before[1], pad_before[2], offset[0], offset[1],
+                       offset[2], patch[0], patch[1], patch[2], f, nviews, out);
+  else
+    hipLaunchKernelGGL(gather_flip_kernel<1>, grid, block, 0, st, vol, channels, size[0], size[1],
+                       size[2], pad_before[0], pad_before[1], pad_before[2], offset[0], offset[1],
+                       offset[2], patch[0], patch[1], patch[2], f, nviews, out);
   launch_check("sw_gather_flip");
 }
 
@@ -242,14 +271,15 @@ void sw_accumulate(const float* pred, int nviews, const int* flips, int k, const
   const double esz = accum == NNX_ACCUM_NNUNET_F16 ? 2.0 : 4.0;
   ProfScope prof("sw_accumulate", 0.0,
                  (double)n * (nviews * k * 4.0 + 2.0 * k * esz + 2.0 * esz + esz), st);
+  // at most 128 lanes a row (longer rows loop), several rows a workgroup
+  const unsigned lanes = row_threads((int64_t)patch[2] * k, kAccLanes), rows = rows_per_group(lanes);
+  const dim3 grid((unsigned)ceil_div(patch[1], rows), patch[0]), block(lanes, rows);
   if (accum == NNX_ACCUM_NNUNET_F16)
-    hipLaunchKernelGGL(accumulate_kernel<true>, dim3(patch[1], patch[0]),
-                       dim3(row_threads((int64_t)patch[2] * k)), 0, st, pred, nviews,
+    hipLaunchKernelGGL(accumulate_kernel<true>, grid, block, 0, st, pred, nviews,
                        f, k, patch[0], patch[1], patch[2], gaussian, offset[0], offset[1],
                        offset[2], padded[1], padded[2], acc, norm);
   else
-    hipLaunchKernelGGL(accumulate_kernel<false>, dim3(patch[1], patch[0]),
-                       dim3(row_threads((int64_t)patch[2] * k)), 0, st, pred, nviews,
+    hipLaunchKernelGGL(accumulate_kernel<false>, grid, block, 0, st, pred, nviews,
                        f, k, patch[0], patch[1], patch[2], gaussian, offset[0], offset[1],
                        offset[2], padded[1], padded[2], acc, norm);
   launch_check("sw_accumulate");

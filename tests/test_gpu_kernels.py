@@ -495,20 +495,38 @@ def _unflip(view: np.ndarray, mask: int) -> np.ndarray:
     return np.flip(view, axis=axes) if axes else view
 
 
-def test_gather_flip_exact(lib):
+# (channels, patch, output offset in floats): rows of a multiple of 4 floats into an aligned
+# output take 16-byte runs; odd rows, a misaligned output and rows that do not fill the last
+# workgroup take the single-float path or the row bound
+GATHER_CASES = [
+    (2, (12, 8, 10), 0),
+    (3, (12, 11, 12), 0),
+    (1, (12, 8, 7), 0),
+    (2, (12, 8, 10), 1),
+    (1, (5, 13, 200), 0),
+]
+
+
+@pytest.mark.parametrize("case", GATHER_CASES, ids=str)
+def test_gather_flip_exact(lib, case):
+    channels, patch, shift = case
+    print(f"gather case {case}", flush=True)
     rng = np.random.default_rng(8)
-    vol = rng.standard_normal((2, 9, 11, 13)).astype(np.float32)
+    vol = rng.standard_normal((channels, 9, 11, 13)).astype(np.float32)
     pad = (2, 0, 1)
-    patch = (12, 8, 10)
     offset = (0, 3, 4)
-    padded = np.pad(vol, [(0, 0), (pad[0], 12 - 9 - pad[0]), (0, 0), (pad[2], 1)])
-    out = torch.full((8, *patch, 2), float("nan"), dtype=torch.float32, device="cuda")
+    after = [max(0, o + p - s - b) for o, p, s, b in zip(offset, patch, vol.shape[1:], pad)]
+    padded = np.pad(vol, [(0, 0)] + [(b, a) for b, a in zip(pad, after)])
+    n = 8 * int(np.prod(patch)) * channels
+    buf = torch.full((n + shift,), float("nan"), dtype=torch.float32, device="cuda")
     dvol = dev(vol)
     _native.check(lib.nnx_sw_gather_flip(
-        dvol.data_ptr(), 2, _native.i64s(vol.shape[1:]), _native.ints(pad), _native.ints(offset),
-        _native.ints(patch), _native.ints(FLIPS_3AX), 8, out.data_ptr(), stream()))
-    got = host(out)
-    tile = np.moveaxis(padded[:, offset[0]:offset[0] + 12, offset[1]:offset[1] + 8, offset[2]:offset[2] + 10], 0, -1)
+        dvol.data_ptr(), channels, _native.i64s(vol.shape[1:]), _native.ints(pad),
+        _native.ints(offset), _native.ints(patch), _native.ints(FLIPS_3AX), 8,
+        buf.data_ptr() + 4 * shift, stream()))
+    got = host(buf)[shift:].reshape(8, *patch, channels)
+    sl = tuple(slice(o, o + p) for o, p in zip(offset, patch))
+    tile = np.moveaxis(padded[(slice(None),) + sl], 0, -1)
     for v, mask in enumerate(FLIPS_3AX):
         np.testing.assert_array_equal(got[v], _unflip(tile, mask))
 
