@@ -28,6 +28,12 @@ typedef float f2 __attribute__((ext_vector_type(2)));
 
 constexpr int kChunk = 8;  // input channels per LDS halo chunk / packed weight chunk
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS (and scalar) operations,
+// not for its global loads and stores, which __syncthreads' fence also waits for.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ f4 mfma16x16x4(float a, float b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
@@ -1439,6 +1445,27 @@ __device__ __forceinline__ float split_scale_of(float max_abs) {
   return ldexpf(1.f, 15 - e < 100 ? 15 - e : 100);
 }
 
+// Sum over the 16 lanes of each DPP row (row rotations by 8, 4, 2, 1); every lane of the
+// row receives the sum.
+template <int CTRL>
+__device__ __forceinline__ float dpp_row(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v),
+                                                                CTRL, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float row_sum16(float v) {
+  v += dpp_row<0x128>(v);
+  v += dpp_row<0x124>(v);
+  v += dpp_row<0x122>(v);
+  v += dpp_row<0x121>(v);
+  return v;
+}
+
+// Waves a SIMD the first convolution is built for: 4 (at most 128 registers) where its
+// registers fit without spills (one input channel, at most 32 outputs), else the compiler's
+// choice.
+template <int COUT, int CIN>
+constexpr int kDirX3Waves = (CIN == 1 && COUT <= 32) ? 4 : 1;
+
 // The same convolution with split-fp16 products on MFMA: the weights of 16 output
 // channels form one 16 x 32 A fragment (27 taps zero-padded to 32), the taps of 16 voxels
 // one 32 x 16 B fragment, hi*hi + hi*lo + lo*hi with float32 accumulation.  The raw input
@@ -1448,17 +1475,16 @@ __device__ __forceinline__ float split_scale_of(float max_abs) {
 // = 256 voxels (x fastest); wave w computes voxels 64 w .. 64 w + 63 of the tile:
 // 4 blocks of 16 voxels x ceil(cout / 16) blocks of 16 channels.  A lane's accumulator
 // holds 4 consecutive channels of one voxel, stored as one 16-byte word; the tile's
-// InstanceNorm partials reduce the accumulators across lanes and waves (mean, then the
-// centred M2), so the outputs never pass through LDS.
+// InstanceNorm partials come from the accumulators in one pass (sums of x - s and its square,
+// s a value of the wave's own first voxel, over the lanes of a DPP row; then per wave
+// (count, mean, M2) merged across the 4 waves by Chan's formula), so the outputs never pass
+// through LDS.  The halo is scaled and split once into fp16 hi/lo planes in LDS; barriers
+// wait for LDS only, so output stores and the next tile's halo loads stay in flight.
 template <int COUT, int CIN>
-__global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __restrict__ x,
-                                                             const float* __restrict__ w,
-                                                             float wscale,
-                                                             const float* __restrict__ bias,
-                                                             float* __restrict__ y, int D, int H,
-                                                             int W, int tiles_y, int tiles_x,
-                                                             int ntiles, int tpb,
-                                                             float4* __restrict__ stats) {
+__global__ __launch_bounds__(256, (kDirX3Waves<COUT, CIN>)) void direct_cin1_x3_kernel(
+    const float* __restrict__ x, const float* __restrict__ w, float wscale,
+    const float* __restrict__ bias, float* __restrict__ y, int D, int H, int W, int tiles_y,
+    int tiles_x, int ntiles, int tpb, float4* __restrict__ stats) {
   constexpr int cout = COUT;
   constexpr int NB = (COUT + 15) / 16;
   constexpr int MB = 4;
@@ -1467,9 +1493,10 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
   constexpr int kHalo = (TZ + 2) * HY * HX * CIN;  // voxel-major, CIN channels a voxel
   constexpr int K = 27 * CIN, KS = (K + 31) / 32;    // taps x channels, 32 per MFMA step
   constexpr int kLoads = (kHalo + 255) / 256;
-  __shared__ float halo[kHalo];
-  __shared__ float red[4][NB * 16];
-  __shared__ float wmax[4];
+  // the tile's scaled halo split once into fp16 hi and lo planes
+  __shared__ _Float16 halo_hi[kHalo], halo_lo[kHalo];
+  __shared__ float red[4][NB * 16], red2[4][NB * 16], wcnt[4];
+  __shared__ float wmax[2][4];  // per-wave maxima of |x|, double-buffered over tiles
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int row = lane & 15, slot = lane >> 4;
@@ -1502,7 +1529,8 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
   const float inv_w = 1.f / wscale;
 
   // tiles tpb * blockIdx.x .. of this batch item, one after the other; each tile's halo
-  // is loaded into registers while the previous tile computes
+  // is loaded into registers while the previous tile computes, and its maximum |x| is
+  // reduced per wave at the end of the previous tile
   const int t_begin = blockIdx.x * tpb;
   const int t_end = min(ntiles, t_begin + tpb);
   float hv[kLoads];
@@ -1520,29 +1548,44 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
       hv[j] = inside ? x[(item + ((int64_t)z * H + yy) * W + xx) * CIN + hc] : 0.f;
     }
   };
-  if (t_begin < t_end) load_halo(t_begin);
-  for (int tile = t_begin; tile < t_end; ++tile) {
-    const int txi = tile % tiles_x, tyi = (tile / tiles_x) % tiles_y, tzi = tile / (tiles_x * tiles_y);
-    const int z0 = tzi * TZ, y0 = tyi * TY, x0 = txi * TX;
-    __syncthreads();  // the previous tile's halo, maxima and partials have been read
-    // publish the halo; tile maximum of |x| over it (zeros outside the volume) from the
-    // registers: per thread, per wave, then across the 4 waves
+  // maximum |x| over the registers' halo values (zeros outside the volume): per thread,
+  // then per wave into wmax[buf]
+  auto wave_max = [&](int buf) {
     float mx = 0.f;
 #pragma unroll
     for (int j = 0; j < kLoads; ++j)
-      if (tid + 256 * j < kHalo) {
-        halo[tid + 256 * j] = hv[j];
-        mx = fmaxf(mx, fabsf(hv[j]));
-      }
+      if (tid + 256 * j < kHalo) mx = fmaxf(mx, fabsf(hv[j]));
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) mx = fmaxf(mx, __shfl_xor(mx, o));
-    if (lane == 0) wmax[wave] = mx;
-    if (tile + 1 < t_end) load_halo(tile + 1);
-    __syncthreads();
-    const float xscale = split_scale_of(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    if (lane == 0) wmax[buf][wave] = mx;
+  };
+  if (t_begin < t_end) {
+    load_halo(t_begin);
+    wave_max(0);
+  }
+  for (int tile = t_begin; tile < t_end; ++tile) {
+    const int buf = (tile - t_begin) & 1;
+    const int txi = tile % tiles_x, tyi = (tile / tiles_x) % tiles_y, tzi = tile / (tiles_x * tiles_y);
+    const int z0 = tzi * TZ, y0 = tyi * TY, x0 = txi * TX;
+    // the previous tile's operand reads and partials are done; this tile's maxima are in
+    // wmax[buf]
+    lds_barrier();
+    const float xscale =
+        split_scale_of(fmaxf(fmaxf(wmax[buf][0], wmax[buf][1]), fmaxf(wmax[buf][2], wmax[buf][3])));
     // inverse scales, applied one after the other (exact powers of two; their product
     // alone could leave the float range)
     const float inv_x = 1.f / xscale;
+    // publish the halo times xscale (exact) as fp16 hi and lo planes
+#pragma unroll
+    for (int j = 0; j < kLoads; ++j)
+      if (tid + 256 * j < kHalo) {
+        _Float16 hh, ll;
+        to_operand<kSplit3>(hv[j] * xscale, hh, ll);
+        halo_hi[tid + 256 * j] = hh;
+        halo_lo[tid + 256 * j] = ll;
+      }
+    if (tile + 1 < t_end) load_halo(tile + 1);
+    lds_barrier();
 
     f4 acc[MB][NB];
 #pragma unroll
@@ -1562,11 +1605,8 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
           const int k = st * 32 + slot * 8 + q;
           const int tap = k / CIN, hc = k - tap * CIN;
           const int off = k < K ? ((tap / 9) * HY + (tap / 3) % 3) * HX + tap % 3 : 0;
-          const float hvq = k < K ? halo[(base + off) * CIN + hc] * xscale : 0.f;
-          _Float16 hh, ll;
-          to_operand<kSplit3>(hvq, hh, ll);
-          B[0][q] = hh;
-          B[1][q] = ll;
+          B[0][q] = k < K ? halo_hi[(base + off) * CIN + hc] : (_Float16)0.f;
+          B[1][q] = k < K ? halo_lo[(base + off) * CIN + hc] : (_Float16)0.f;
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
@@ -1587,78 +1627,82 @@ __global__ __launch_bounds__(256) void direct_cin1_x3_kernel(const float* __rest
       valid[mb] = gz < D && gy < H && gx < W;
       vox[mb] = item + ((int64_t)gz * H + gy) * W + gx;
     }
+    // a voxel's channel blocks one after the other, so its row is written by consecutive
+    // stores
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const int n0 = nb * 16 + slot * 4;
+    for (int mb = 0; mb < MB; ++mb) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) {
+      for (int nb = 0; nb < NB; ++nb) {
+        const int n0 = nb * 16 + slot * 4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const float t = (acc[mb][nb][r] * inv_x) * inv_w;
-          acc[mb][nb][r] = has_bias ? t + bn[nb][r] : t;
+          acc[mb][nb][r] = (acc[mb][nb][r] * inv_x) * inv_w + bn[nb][r];
         }
         if (valid[mb] && n0 < cout) *reinterpret_cast<f4*>(y + vox[mb] * cout + n0) = acc[mb][nb];
       }
     }
-    if (!stats) continue;
-    // partials over the tile's voxels: per lane over its 4 row blocks, across the 16 lanes
-    // of its slot, then across the 4 waves
-    const int nz = D - z0 < TZ ? D - z0 : TZ, ny = H - y0 < TY ? H - y0 : TY;
-    const int nx = W - x0 < TX ? W - x0 : TX;
-    const int nv = nz * ny * nx;
-    auto reduce16 = [&](float v) {
+    if (stats) {
+      // partials over the tile's voxels in one pass: per lane, sums of d = x - s and d^2
+      // over its 4 row blocks, with s the value of the wave's first voxel (row 0 of block
+      // 0) in that channel; across the 16 lanes of a slot by row rotations; then per wave
+      // (count, mean, M2), merged across the 4 waves by Chan's formula
+      float cnt = 0.f;
 #pragma unroll
-      for (int o = 8; o >= 1; o >>= 1) v += __shfl_xor(v, o);
-      return v;
-    };
-    float mean[NB][4];
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float t = 0.f;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          if (valid[mb]) t += acc[mb][nb][r];
-        t = reduce16(t);
-        if (row == 0) red[wave][nb * 16 + slot * 4 + r] = t;
-      }
-    __syncthreads();
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int n = nb * 16 + slot * 4 + r;
-        mean[nb][r] = (red[0][n] + red[1][n] + red[2][n] + red[3][n]) / (float)nv;
-      }
-    __syncthreads();
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        float t = 0.f;
-#pragma unroll
-        for (int mb = 0; mb < MB; ++mb)
-          if (valid[mb]) {
-            const float d = acc[mb][nb][r] - mean[nb][r];
-            t = fmaf(d, d, t);
-          }
-        t = reduce16(t);
-        if (row == 0) red[wave][nb * 16 + slot * 4 + r] = t;
-      }
-    __syncthreads();
-    if (wave == 0 && row == 0) {
+      for (int mb = 0; mb < MB; ++mb) cnt += valid[mb] ? 1.f : 0.f;
+      cnt = row_sum16(cnt);
+      const float inv_cnt = cnt > 0.f ? 1.f / cnt : 0.f;
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int n = nb * 16 + slot * 4 + r;
-          if (n < cout)
-            stats[((int64_t)blockIdx.y * ntiles + tile) * cout + n] =
-                make_float4(mean[nb][r], red[0][n] + red[1][n] + red[2][n] + red[3][n],
-                            (float)nv, 0.f);
+          const float shift = __shfl(acc[0][nb][r], lane & 48);
+          float s1 = 0.f, s2 = 0.f;
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb) {
+            const float d = valid[mb] ? acc[mb][nb][r] - shift : 0.f;
+            s1 += d;
+            s2 = fmaf(d, d, s2);
+          }
+          s1 = row_sum16(s1);
+          s2 = row_sum16(s2);
+          if (row == 0) {
+            const int n = nb * 16 + slot * 4 + r;
+            const float m = s1 * inv_cnt;
+            red[wave][n] = shift + m;
+            red2[wave][n] = fmaxf(s2 - s1 * m, 0.f);
+          }
         }
+      if (lane == 0) wcnt[wave] = cnt;
+      lds_barrier();
+      if (wave == 0 && row == 0) {
+        // merge weights of waves 1..3 (the same for every channel)
+        float fw[4], gw[4], na = wcnt[0];
+#pragma unroll
+        for (int q = 1; q < 4; ++q) {
+          const float nq = wcnt[q], nab = na + nq;
+          fw[q] = nq > 0.f ? nq / nab : 0.f;
+          gw[q] = nq > 0.f ? na * nq / nab : 0.f;
+          na = nab;
+        }
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int n = nb * 16 + slot * 4 + r;
+            float mean = red[0][n], m2 = red2[0][n];
+#pragma unroll
+            for (int q = 1; q < 4; ++q) {
+              const float delta = red[q][n] - mean;
+              mean = fmaf(delta, fw[q], mean);
+              m2 += red2[q][n] + delta * delta * gw[q];
+            }
+            if (n < cout)
+              stats[((int64_t)blockIdx.y * ntiles + tile) * cout + n] =
+                  make_float4(mean, m2, na, 0.f);
+          }
+      }
     }
+    if (tile + 1 < t_end) wave_max(buf ^ 1);
   }
 }
 
