@@ -48,7 +48,7 @@ const char* nnx_version(void);
 #define NNX_PRECISION_FP32 0
 /* Float32 semantics (float32 inputs, weights, accumulation and outputs) with the 3-D
  * convolutions computed as three fp16 MFMA products of split operands (x = hi + lo), see
- * nnx_conv3d_split.  A first convolution with 1 or 2 input channels uses split products
+ * nnx_conv3d_split.  A first convolution with 1, 2 or 4 input channels uses split products
  * too, with a per-tile power-of-two scale of the raw input (nnx_conv3d_direct_small_cin_split);
  * other first convolutions keep float32 products.  Meets the float32 logits tolerance;
  * hidden activations must stay below 65504 in magnitude (they are normalised, so they do). */
@@ -254,15 +254,15 @@ int nnx_conv3d_winograd(const float* d_x1, int c1, const float* d_x2, int c2,
 int nnx_conv3d_direct_small_cin(const float* d_x, const float* d_weight /* (Cout,3,3,3,1) */,
                                 const float* d_bias, float* d_y, int batch, const int* size,
                                 int cout, void* stream);
-/* The same convolution with split-fp16 products on MFMA for 1 or 2 input channels (the
+/* The same convolution with split-fp16 products on MFMA for 1, 2 or 4 input channels (the
  * 27 * cin (tap, channel) products of 16 voxels as 16 x 32 fragments, hi*hi + hi*lo +
  * lo*hi, float32 accumulation): weights times `scale` (nnx_split_weight_scale of max |w|),
  * each 4 x 4 x 16 output tile's input (all channels) times one power of two from the tile's
  * own max |x|, products times the inverses (exact), + bias.  Replaces the same reference
  * call as nnx_conv3d_direct_small_cin in the fp32-split precision, and the first
- * Conv3d of two-channel networks (mx.conv3d via _unbiased_convolution,
+ * Conv3d of two- and four-channel networks (mx.conv3d via _unbiased_convolution,
  * src/nnunet_mlx/model/network.py:240-269). */
-int nnx_conv3d_direct_small_cin_split(const float* d_x, int cin /* 1 or 2 */,
+int nnx_conv3d_direct_small_cin_split(const float* d_x, int cin /* 1, 2 or 4 */,
                                       const float* d_weight /* (Cout,3,3,3,cin) */, float scale,
                                       const float* d_bias, float* d_y, int batch,
                                       const int* size, int cout, void* stream);

@@ -1460,15 +1460,16 @@ __device__ __forceinline__ float row_sum16(float v) {
   return v;
 }
 
-// Waves a SIMD the first convolution is built for: 4 (at most 128 registers) where its
-// registers fit without spills (one input channel, at most 32 outputs), else the compiler's
-// choice.
+// Waves a SIMD the first convolution is built for, where its registers fit without spills:
+// 4 (at most 128 registers) for one input channel and at most 32 outputs, 2 (256) for four
+// input channels and at most 48 outputs, else the compiler's choice.
 template <int COUT, int CIN>
-constexpr int kDirX3Waves = (CIN == 1 && COUT <= 32) ? 4 : 1;
+constexpr int kDirX3Waves = (CIN == 1 && COUT <= 32) ? 4 : (CIN == 4 && COUT <= 48) ? 2 : 1;
 
-// The same convolution with split-fp16 products on MFMA: the weights of 16 output
-// channels form one 16 x 32 A fragment (27 taps zero-padded to 32), the taps of 16 voxels
-// one 32 x 16 B fragment, hi*hi + hi*lo + lo*hi with float32 accumulation.  The raw input
+// The same convolution with split-fp16 products on MFMA for CIN = 1, 2 or 4 input
+// channels: the weights of 16 output channels form 16 x 32 A fragments (27 * CIN (tap,
+// channel) products zero-padded to whole K steps of 32), the taps of 16 voxels 32 x 16 B
+// fragments, hi*hi + hi*lo + lo*hi with float32 accumulation.  The raw input
 // has no normalised range, so each tile scales its halo by a power of two from the tile's
 // own max |x| (weights by `wscale`, a power of two from max |w|) before the split and the
 // products by the inverses (exact); + bias after.  Tiles of kDirX3Tz x kDirX3Ty x kDirX3Tx
@@ -1494,7 +1495,8 @@ __global__ __launch_bounds__(256, (kDirX3Waves<COUT, CIN>)) void direct_cin1_x3_
   constexpr int K = 27 * CIN, KS = (K + 31) / 32;    // taps x channels, 32 per MFMA step
   constexpr int kLoads = (kHalo + 255) / 256;
   // the tile's scaled halo split once into fp16 hi and lo planes
-  __shared__ _Float16 halo_hi[kHalo], halo_lo[kHalo];
+  __shared__ __align__(16) _Float16 halo_hi[kHalo];
+  __shared__ __align__(16) _Float16 halo_lo[kHalo];
   __shared__ float red[4][NB * 16], red2[4][NB * 16], wcnt[4];
   __shared__ float wmax[2][4];  // per-wave maxima of |x|, double-buffered over tiles
   const int tid = threadIdx.x;
@@ -1506,27 +1508,53 @@ __global__ __launch_bounds__(256, (kDirX3Waves<COUT, CIN>)) void direct_cin1_x3_
   // A fragments: lane (n = 16 nb + row, k = 32 s + 8 slot + q) holds wscale * W[n][k] split,
   // k = tap * CIN + channel (the (C_out, kD, kH, kW, C_in) layout); bias of the lane's 4
   // output channels 16 nb + 4 slot + r
-  h8 A[NB][KS][2];
+  // with several channels a tap the fragments of all K steps would not fit in registers
+  // next to the accumulators: they are kept in LDS and read one K step at a time
+  constexpr bool kALds = CIN > 2;
+  __shared__ h8 a_lds[kALds ? NB * KS * 2 * 64 : 1];
+  h8 A[kALds ? 1 : NB][kALds ? 1 : KS][2];
   f4 bn[NB];
 #pragma unroll
   for (int nb = 0; nb < NB; ++nb) {
     const int n = nb * 16 + row;
 #pragma unroll
-    for (int st = 0; st < KS; ++st)
+    for (int st = 0; st < KS; ++st) {
+      h8 fh, fl;
 #pragma unroll
       for (int q = 0; q < 8; ++q) {
         const int k = st * 32 + slot * 8 + q;
         const float v = (n < cout && k < K) ? w[n * K + k] * wscale : 0.f;
         _Float16 hh, ll;
         to_operand<kSplit3>(v, hh, ll);
-        A[nb][st][0][q] = hh;
-        A[nb][st][1][q] = ll;
+        fh[q] = hh;
+        fl[q] = ll;
       }
+      if constexpr (kALds) {
+        a_lds[((nb * KS + st) * 2 + 0) * 64 + lane] = fh;
+        a_lds[((nb * KS + st) * 2 + 1) * 64 + lane] = fl;
+      } else {
+        A[nb][st][0] = fh;
+        A[nb][st][1] = fl;
+      }
+    }
     const int n0 = nb * 16 + slot * 4;
     bn[nb] = f4{0.f, 0.f, 0.f, 0.f};
     if (has_bias && n0 < cout) bn[nb] = f4{bias[n0], bias[n0 + 1], bias[n0 + 2], bias[n0 + 3]};
   }
   const float inv_w = 1.f / wscale;
+  static_assert(TX == 16 && TY == 4, "a wave's voxels are one z-plane of the tile");
+  // 4 channels: this lane's taps of K step st are 8 st + 2 slot + u (u = 0, 1); padded taps
+  // (>= 27) read tap 0's voxel against zero weights
+  int toff4[CIN == 4 ? KS : 1][2];
+  if constexpr (CIN == 4) {
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const int tap = 8 * st + 2 * slot + u;
+        toff4[st][u] = tap < 27 ? ((tap / 9) * HY + (tap / 3) % 3) * HX + tap % 3 : 0;
+      }
+  }
 
   // tiles tpb * blockIdx.x .. of this batch item, one after the other; each tile's halo
   // is loaded into registers while the previous tile computes, and its maximum |x| is
@@ -1593,26 +1621,46 @@ __global__ __launch_bounds__(256, (kDirX3Waves<COUT, CIN>)) void direct_cin1_x3_
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int mb = 0; mb < MB; ++mb) {
-      // B fragment: lane (voxel v = 64 wave + 16 mb + row, taps 8 slot + q)
-      const int v = wave * 64 + mb * 16 + row;
-      const int base = ((v / (TX * TY)) * HY + (v / TX) % TY) * HX + v % TX;
+    for (int st = 0; st < KS; ++st) {
+      h8 As[NB][2];
 #pragma unroll
-      for (int st = 0; st < KS; ++st) {
+      for (int nb = 0; nb < NB; ++nb)
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+          if constexpr (kALds) As[nb][p] = a_lds[((nb * KS + st) * 2 + p) * 64 + lane];
+          else As[nb][p] = A[nb][st][p];
+        }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb) {
+        // B fragment: lane (voxel v = 64 wave + 16 mb + row, taps 8 slot + q)
+        // (a wave's 64 voxels are one z-plane of the tile: TY x TX = 4 x 16)
+        const int base = (wave * HY + mb) * HX + row;
         h8 B[2];
+        if constexpr (CIN == 4) {
+          // two taps of 4 channels: one 8-byte read per tap and plane
+          h4 th[2], tl[2];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) {
-          const int k = st * 32 + slot * 8 + q;
-          const int tap = k / CIN, hc = k - tap * CIN;
-          const int off = k < K ? ((tap / 9) * HY + (tap / 3) % 3) * HX + tap % 3 : 0;
-          B[0][q] = k < K ? halo_hi[(base + off) * CIN + hc] : (_Float16)0.f;
-          B[1][q] = k < K ? halo_lo[(base + off) * CIN + hc] : (_Float16)0.f;
+          for (int u = 0; u < 2; ++u) {
+            th[u] = *reinterpret_cast<const h4*>(halo_hi + (base + toff4[st][u]) * 4);
+            tl[u] = *reinterpret_cast<const h4*>(halo_lo + (base + toff4[st][u]) * 4);
+          }
+          B[0] = __builtin_shufflevector(th[0], th[1], 0, 1, 2, 3, 4, 5, 6, 7);
+          B[1] = __builtin_shufflevector(tl[0], tl[1], 0, 1, 2, 3, 4, 5, 6, 7);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 8; ++q) {
+            const int k = st * 32 + slot * 8 + q;
+            const int tap = k / CIN, hc = k - tap * CIN;
+            const int off = k < K ? ((tap / 9) * HY + (tap / 3) % 3) * HX + tap % 3 : 0;
+            B[0][q] = k < K ? halo_hi[(base + off) * CIN + hc] : (_Float16)0.f;
+            B[1][q] = k < K ? halo_lo[(base + off) * CIN + hc] : (_Float16)0.f;
+          }
         }
 #pragma unroll
         for (int nb = 0; nb < NB; ++nb) {
-          acc[mb][nb] = mfma16x16x32h(A[nb][st][0], B[0], acc[mb][nb]);
-          acc[mb][nb] = mfma16x16x32h(A[nb][st][0], B[1], acc[mb][nb]);
-          acc[mb][nb] = mfma16x16x32h(A[nb][st][1], B[0], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(As[nb][0], B[0], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(As[nb][0], B[1], acc[mb][nb]);
+          acc[mb][nb] = mfma16x16x32h(As[nb][1], B[0], acc[mb][nb]);
         }
       }
     }
@@ -2551,8 +2599,8 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
                         const int* size, int cout, hipStream_t st, float4* stats, float wscale,
                         int cin) {
   require(x && w && y, "convolution pointers must not be null");
-  require(cin == 1 || (wscale > 0.f && cin == 2),
-          "the direct convolution takes 1 input channel, or 2 with split products");
+  require(cin == 1 || (wscale > 0.f && (cin == 2 || cin == 4)),
+          "the direct convolution takes 1 input channel, or 2 or 4 with split products");
   require(cout >= 4 && cout <= 64 && cout % 4 == 0,
           "one-channel direct convolution supports 4..64 outputs in steps of 4");
   require(batch >= 1 && batch <= 65535, "invalid convolution batch");
@@ -2582,8 +2630,12 @@ void conv3d_direct_cin1(const float* x, const float* w, const float* bias, float
       hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 1>), grid_x3, dim3(256), 0, st, x, w,    \
                          wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
                          (int)tiles, tpb, stats);                                               \
-    else                                                                                       \
+    else if (cin == 2)                                                                         \
       hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 2>), grid_x3, dim3(256), 0, st, x, w,    \
+                         wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
+                         (int)tiles, tpb, stats);                                               \
+    else                                                                                       \
+      hipLaunchKernelGGL((direct_cin1_x3_kernel<4 * Q, 4>), grid_x3, dim3(256), 0, st, x, w,    \
                          wscale, bias, y, size[0], size[1], size[2], tiles_y, tiles_x,          \
                          (int)tiles, tpb, stats);                                               \
     break;

@@ -249,11 +249,11 @@ void declare_convnorm(nnx_model* m, ConvNorm& c, const std::string& prefix, int 
   const bool shape_ok = cin2 == 0 && k[0] == 3 && k[1] == 3 && k[2] == 3 && s[0] == 1 &&
                         s[1] == 1 && s[2] == 1 && cout % 4 == 0 && cout <= 64;
   c.direct = cin1 == 1 && shape_ok;
-  // 2 input channels: the direct kernel with split products, for the network's first
-  // convolution only (decided when packing, once the first convolution is known).  With 4
-  // channels its four MFMA steps per voxel tile made it slower than the float32-product
-  // implicit GEMM (247 against 230 ms per 4 x 155 x 240 x 240 five-fold case).
-  c.direct_multi = cin1 == 2 && shape_ok;
+  // 2 or 4 input channels: the direct kernel with split products, for the network's first
+  // convolution only (decided when packing, once the first convolution is known); with 4
+  // channels 3.4 ms against 10.1 ms for the float32-product implicit GEMM per 32-view
+  // 128^3 launch.
+  c.direct_multi = (cin1 == 2 || cin1 == 4) && shape_ok;
 }
 
 const int kUnit[3] = {1, 1, 1};
@@ -1181,7 +1181,8 @@ int nnx_conv3d_direct_small_cin_split(const float* d_x, int cin, const float* d_
                                       const int* size, int cout, void* stream) {
   return guarded([&] {
     require(size != nullptr, "null argument");
-    require(cin == 1 || cin == 2, "the split direct convolution takes 1 or 2 input channels");
+    require(cin == 1 || cin == 2 || cin == 4,
+            "the split direct convolution takes 1, 2 or 4 input channels");
     require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
     conv3d_direct_cin1(d_x, d_weight, d_bias, d_y, batch, size, cout, as_stream(stream), nullptr,
                        scale, cin);

@@ -27,7 +27,7 @@ from nnunet_mlx.model.topology import NetworkSpec, PlainConvUNetSpec, ResidualEn
 # logits tolerance (max-abs <= 1e-3, relative L2 <= 1e-5 against the float32 oracle):
 # "fp32" multiplies in float32 on fp32 MFMA; "fp32-split" (the default, ~2.5x faster
 # convolutions) computes the 3-D convolutions as hi*hi + hi*lo + lo*hi of fp16-split
-# operands with float32 accumulation (a first convolution with 1 or 2 input channels scales
+# operands with float32 accumulation (a first convolution with 1, 2 or 4 input channels scales
 # each input tile by a power of two before the split; other first convolutions keep float32
 # products).  "bf16" rounds the hidden 3-D convolutions' (and the transposed convolutions')
 # weights and inputs to bf16 and multiplies once, with float32 accumulation and float32 norm

@@ -216,12 +216,16 @@ def test_direct_single_channel_conv(lib, size, cout):
     ((16, 16, 16), 32, 1.0, 1), ((5, 7, 9), 8, 1.0, 1), ((9, 20, 11), 12, 3e4, 1),
     ((4, 8, 8), 64, 1e-30, 1),
     # two channels: ragged tiles, and channel amplitudes 1 and 3e4 sharing one tile scale
-    ((7, 9, 19), 32, (1.0, 3e4), 2), ((16, 16, 16), 32, 1.0, 2), ((3, 5, 33), 4, (3e4, 1e-3), 2)])
+    ((7, 9, 19), 32, (1.0, 3e4), 2), ((16, 16, 16), 32, 1.0, 2), ((3, 5, 33), 4, (3e4, 1e-3), 2),
+    # four channels (two taps of four channels a K step, the last step padded), including
+    # the 36..48-output and the >48-output builds
+    ((16, 16, 16), 32, 1.0, 4), ((7, 9, 19), 48, (1.0, 3e4, 1e-3, 5.0), 4),
+    ((5, 6, 17), 64, (2.0, 1.0, 1.0, 3e4), 4), ((3, 5, 33), 4, 1.0, 4)])
 def test_direct_single_channel_conv_split(lib, size, cout, amplitude, cin):
     """Split products on MFMA hold the float32 bar of the split kernels at any input range
     (each tile scales its input by a power of two): raw CT-like magnitudes beyond the fp16
-    range, tiny values, and tiles mixing both; with two input channels the channels of one
-    tile share its scale."""
+    range, tiny values, and tiles mixing both; with two or four input channels the channels
+    of one tile share its scale."""
     print(f"direct split conv {size} {cout} {amplitude} cin={cin}", flush=True)
     rng = np.random.default_rng(11)
     amp = np.broadcast_to(np.asarray(amplitude, dtype=np.float64), (cin,))
