@@ -1917,7 +1917,30 @@ struct TcArgs {
   int ntn, nwg;
   int tpb;  // row tiles per workgroup
   float out_scale;
+  // pending InstanceNorm (+ LeakyReLU) of the input: (mean, scale, beta, 0) per (b, c), for
+  // batch item b = row / vox, vox a multiple of kTcRows (null: the input is final)
+  const float4* nrm;
+  int act;
+  float slope;
+  int64_t vox;
 };
+
+// The pending normalisation of input channels c..c+3 of batch item b (zero parameters for
+// channels past C_in, whose zero loads then stay zero).
+__device__ __forceinline__ NormLine tc_norm_line(const TcArgs& a, int64_t b, int c) {
+  NormLine nl;
+  nl.on = true;
+  nl.act = a.act != 0;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (c + q < a.cin) v = a.nrm[b * a.cin + c + q];
+    nl.m[q] = v.x;
+    nl.s[q] = v.y;
+    nl.b[q] = v.z;
+  }
+  return nl;
+}
 
 constexpr int kTcRows = 64, kTcCols = 128, kTcKBlock = 64, kTcRowHalves = kTcKBlock + 8;
 constexpr int kTcTileStride = kTcCols + 1;  // floats per staged output row
@@ -1992,12 +2015,17 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
         }
         lines[j] = v;
       }
+      // the pending normalisation of this thread's channel quad (the same for all its
+      // lines; a row tile lies in one batch item, vox being a multiple of the tile rows)
+      NormLine nl{};
+      if (a.nrm) nl = tc_norm_line(a, m0 / a.vox, kb + (tid & 15) * 4);
       __syncthreads();  // the previous block's fragments have been read
 #pragma unroll
       for (int j = 0; j < kLines; ++j) {
         const int i = tid + 256 * j;
         const int r = i >> 4, c4 = (i & 15) * 4;
-        const f4 v = lines[j];
+        f4 v = lines[j];
+        if (a.nrm && m0 + r < a.M) v = norm_apply4(v, nl, a.slope);
         h4 hv, lv;
 #pragma unroll
         for (int q = 0; q < 4; ++q) {
@@ -2739,9 +2767,13 @@ void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin,
   launch_check("tconv3d_split_pack_weight");
 }
 
+bool tconv_norm_on_load(const int* in_size) {
+  return (int64_t)in_size[0] * in_size[1] * in_size[2] % kTcRows == 0;
+}
+
 void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const float* bias,
                 float* y, int batch, const int* in_size, int cout, const int* ksize,
-                hipStream_t st, int arith) {
+                hipStream_t st, int arith, const PendingNorm& norm) {
   require(x && packed && y, "transposed-convolution pointers must not be null");
   require(cin >= 1 && cout >= 1, "invalid transposed-convolution channel counts");
   require(arith == kSplit3 || arith == kBf16, "unknown transposed-convolution arithmetic");
@@ -2765,6 +2797,12 @@ void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const 
   a.ih = in_size[1];
   a.iw = in_size[2];
   a.out_scale = 1.0f / scale;
+  a.nrm = norm.params;
+  a.act = norm.act ? 1 : 0;
+  a.slope = norm.slope;
+  a.vox = (int64_t)in_size[0] * in_size[1] * in_size[2];
+  require(!a.nrm || a.vox % kTcRows == 0,
+          "a pending input norm needs whole row tiles per batch item (tconv_norm_on_load)");
   const int64_t ovox = (int64_t)in_size[0] * ksize[0] * in_size[1] * ksize[1] * in_size[2] * ksize[2];
   require(ovox * cout < (1LL << 31), "transposed-convolution output item too large");
   a.ntn = (int)ceil_div(a.ncols, kTcCols);

@@ -181,13 +181,18 @@ void tconv_pack_weight(const float* d_w, int cout, const int* ksize, int cin, fl
                        hipStream_t st);
 void tconv3d_gemm(const float* x, int cin, const float* packed, const float* bias, float* y,
                   int batch, const int* in_size, int cout, const int* ksize, hipStream_t st);
-// Split-fp16 transposed convolution (stride == kernel), weights scaled like conv3d_x3.
+// Split-fp16 transposed convolution (stride == kernel), weights scaled like conv3d_x3.  With
+// `norm` the input's pending InstanceNorm (+ LeakyReLU) is applied as its rows are staged
+// (the same float32 operations as the apply pass); see tconv_norm_on_load.
 int64_t tconv_x3_packed_bytes(int cout, const int* ksize, int cin);
 void tconv_x3_pack_weight(const float* d_w, int cout, const int* ksize, int cin, float scale,
                           void* d_packed, hipStream_t st, int arith = kArithSplit3);
 void tconv3d_x3(const float* x, int cin, const void* packed, float scale, const float* bias,
                 float* y, int batch, const int* in_size, int cout, const int* ksize,
-                hipStream_t st, int arith = kArithSplit3);
+                hipStream_t st, int arith = kArithSplit3, const PendingNorm& norm = {});
+// Whether tconv3d_x3 can take a pending norm for an input of this spatial size (its row
+// tiles must not straddle batch items).
+bool tconv_norm_on_load(const int* in_size);
 // Class-logit restoration: half-pixel trilinear (edge-clamped, float64) resampling of
 // channels-last logits (src[0], src[1], src[2], classes) to dst, then first-maximum argmax
 // into uint16 labels (dst[0], dst[1], dst[2]).  `half`: float16 logits, values rounded to

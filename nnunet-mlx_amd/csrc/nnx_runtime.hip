@@ -558,7 +558,8 @@ struct Runner {
   }
 
   // The decoder.  Its last stage feeds the segmentation head, which normalises on load;
-  // every other stage's last output feeds a transposed convolution and is applied.
+  // every other stage's last output feeds a transposed convolution, which normalises on load
+  // when split and otherwise takes an applied tensor.
   void decode(std::vector<Act>& skips, std::vector<Shape3>& skip_shapes, float* d_out) {
     const int S = m->stages;
     Act hidden = skips[S - 1];
@@ -566,7 +567,8 @@ struct Runner {
     for (int d = 0; d < S - 1; ++d) {
       const int src = S - 1 - d;
       const Upsample& u = m->up[d];
-      require(!hidden.norm.params, "transposed convolution inputs are applied tensors");
+      require(!hidden.norm.params || u.split,
+              "only the split transposed convolution normalises its input on load");
       Shape3 us;
       for (int i = 0; i < 3; ++i) us.d[i] = hs.d[i] * u.k[i];
       const Shape3& ss = skip_shapes[src - 1];
@@ -574,7 +576,7 @@ struct Runner {
       if (!plan->planning) {
         if (u.split)
           tconv3d_x3(hidden.data, u.cin, u.packed.ptr, u.scale, pdev(m, u.pb), upbuf, n, hs.d,
-                     u.cout, u.k, st, u.arith);
+                     u.cout, u.k, st, u.arith, hidden.norm);
         else
           tconv3d_gemm(hidden.data, u.cin, u.packed.as<float>(), pdev(m, u.pb), upbuf, n, hs.d,
                        u.cout, u.k, st);
@@ -594,7 +596,10 @@ struct Runner {
       const size_t nb = m->dec[d].size();
       for (size_t j = 0; j < nb; ++j) {
         Shape3 o;
-        const bool defer = j + 1 < nb || d == S - 2;
+        // the stage's output feeds the next transposed convolution (which normalises on
+        // load when split and the stage's voxels fill its row tiles) or, for the last
+        // stage, the segmentation head
+        const bool defer = j + 1 < nb || d == S - 2 || (m->up[d + 1].split && tconv_norm_on_load(ss.d));
         a = run_convnorm(m->dec[d][j], a, j == 0 ? skips[src - 1] : Act{}, cur, &o, defer);
         cur = o;
       }
@@ -621,8 +626,11 @@ struct Runner {
       const size_t nb = m->enc[s].size();
       for (size_t j = 0; j < nb; ++j) {
         Shape3 o;
-        // the bottleneck's output feeds the first transposed convolution
-        const bool defer = !(s == S - 1 && j + 1 == nb);
+        // the bottleneck's output feeds the first transposed convolution, which normalises
+        // on load when split and the bottleneck's voxels fill its row tiles
+        const bool last = s == S - 1 && j + 1 == nb;
+        const bool defer = !last || (S > 1 && m->up[0].split &&
+                                     tconv_norm_on_load(conv_out(cur, m->enc[s][j]).d));
         h = run_convnorm(m->enc[s][j], h, Act{}, cur, &o, defer);
         cur = o;
       }
