@@ -1506,10 +1506,9 @@ __global__ __launch_bounds__(256, (kDirX3Waves<COUT, CIN>)) void direct_cin1_x3_
   const bool has_bias = bias != nullptr;
 
   // A fragments: lane (n = 16 nb + row, k = 32 s + 8 slot + q) holds wscale * W[n][k] split,
-  // k = tap * CIN + channel (the (C_out, kD, kH, kW, C_in) layout); bias of the lane's 4
-  // output channels 16 nb + 4 slot + r
-  // with several channels a tap the fragments of all K steps would not fit in registers
-  // next to the accumulators: they are kept in LDS and read one K step at a time
+  // k = tap * CIN + channel (the (C_out, kD, kH, kW, C_in) layout), in registers, or with 4
+  // channels (whose four K steps would not fit next to the accumulators) in LDS, read one K
+  // step at a time; bias of the lane's 4 output channels 16 nb + 4 slot + r
   constexpr bool kALds = CIN > 2;
   __shared__ h8 a_lds[kALds ? NB * KS * 2 * 64 : 1];
   h8 A[kALds ? 1 : NB][kALds ? 1 : KS][2];
