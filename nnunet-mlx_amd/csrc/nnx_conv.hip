@@ -1941,8 +1941,11 @@ __device__ __forceinline__ NormLine tc_norm_line(const TcArgs& a, int64_t b, int
   return nl;
 }
 
-constexpr int kTcRows = 64, kTcCols = 128, kTcKBlock = 64, kTcRowHalves = kTcKBlock + 8;
-constexpr int kTcTileStride = kTcCols + 1;  // floats per staged output row
+// A-plane rows of 80 halves (10 x 16 bytes): the 16-byte fragment reads of a 32-lane half
+// (rows r = 0..15, slots s and s + 1) hit (10 r + s) mod 32, all distinct.  Staged output
+// rows of 132 floats keep every 4-column run 16-byte aligned for one 16-byte read.
+constexpr int kTcRows = 64, kTcCols = 128, kTcKBlock = 64, kTcRowHalves = kTcKBlock + 16;
+constexpr int kTcTileStride = kTcCols + 4;  // floats per staged output row
 
 // KREG > 0: the workgroup's weight fragments (at most KREG k-steps of 32 channels) are
 // loaded into registers once and serve all its row tiles; KREG = 0: read per k-step.
@@ -2111,8 +2114,8 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
         const int64_t base = row_base[r];
         const int off = col_off[cl];
         if (base >= 0 && off >= 0) {
-          const float* tv = tile + r * kTcTileStride + cl;
-          *reinterpret_cast<f4*>(a.y + base * a.cout + off) = f4{tv[0], tv[1], tv[2], tv[3]};
+          *reinterpret_cast<f4*>(a.y + base * a.cout + off) =
+              *reinterpret_cast<const f4*>(tile + r * kTcTileStride + cl);
         }
       }
     } else {
