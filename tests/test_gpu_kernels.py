@@ -248,6 +248,21 @@ def test_direct_single_channel_conv_split(lib, size, cout, amplitude, cin):
     assert np.abs(got - ref).max() <= 1e-5 * np.abs(ref).max(), msg
 
 
+def test_direct_split_conv_rejects_other_channel_counts(lib):
+    """The split first convolution takes 1, 2 or 4 input channels; 3 is refused before any
+    launch and the output keeps its contents."""
+    x = torch.zeros((1, 8, 8, 8, 3), dtype=torch.float32, device="cuda")
+    w = torch.zeros((32, 3, 3, 3, 3), dtype=torch.float32, device="cuda")
+    y = torch.full((1, 8, 8, 8, 32), 7.0, dtype=torch.float32, device="cuda")
+    rc = lib.nnx_conv3d_direct_small_cin_split(x.data_ptr(), 3, w.data_ptr(), 1.0, None,
+                                               y.data_ptr(), 1, _native.ints((8, 8, 8)), 32,
+                                               stream())
+    assert rc == _native.NNX_ERR_INVALID
+    assert "1, 2 or 4 input channels" in _native.last_error(), _native.last_error()
+    torch.cuda.synchronize()
+    assert bool((y == 7.0).all())
+
+
 def _norm_ref64(x, in_bias, gamma, beta, eps, act, slope, residual):
     v = x.astype(np.float64)
     if in_bias is not None:
