@@ -99,32 +99,31 @@ __global__ __launch_bounds__(512) void accumulate_kernel(
         t[v] = pred[((int64_t)v * pvox + srow + sx) * K + k];
       }
     }
+    // the Gaussian weight and the accumulator's (and normaliser's) old values are requested
+    // with the predictions, so the read-modify-write waits for one round of loads
+    const int64_t dst = qrow + x;
+    float g, a_old, n_old = 0.f;
+    if constexpr (kHalf) {
+      g = __half2float(reinterpret_cast<const __half*>(gaussian)[prow + x]);
+      a_old = __half2float(reinterpret_cast<const __half*>(acc)[dst * K + k]);
+      if (k == 0) n_old = __half2float(reinterpret_cast<const __half*>(norm)[dst]);
+    } else {
+      g = reinterpret_cast<const float*>(gaussian)[prow + x];
+      a_old = reinterpret_cast<const float*>(acc)[dst * K + k];
+      if (k == 0) n_old = reinterpret_cast<const float*>(norm)[dst];
+    }
     float s = t[0];
 #pragma unroll
     for (int v = 1; v < 8; ++v)
       if (v < nviews) s = add_rn(s, t[v]);
     if (nviews > 1) s = __fdiv_rn(s, count);
-    float g;
-    if constexpr (kHalf)
-      g = __half2float(reinterpret_cast<const __half*>(gaussian)[prow + x]);
-    else
-      g = reinterpret_cast<const float*>(gaussian)[prow + x];
     const float w = mul_rn(s, g);
-    const int64_t dst = qrow + x;
     if constexpr (kHalf) {
-      __half* a = reinterpret_cast<__half*>(acc) + dst * K + k;
-      *a = __float2half_rn(add_rn(__half2float(*a), w));
-      if (k == 0) {
-        __half* nrm = reinterpret_cast<__half*>(norm) + dst;
-        *nrm = __float2half_rn(add_rn(__half2float(*nrm), g));
-      }
+      reinterpret_cast<__half*>(acc)[dst * K + k] = __float2half_rn(add_rn(a_old, w));
+      if (k == 0) reinterpret_cast<__half*>(norm)[dst] = __float2half_rn(add_rn(n_old, g));
     } else {
-      float* a = reinterpret_cast<float*>(acc) + dst * K + k;
-      *a = add_rn(*a, w);
-      if (k == 0) {
-        float* nrm = reinterpret_cast<float*>(norm) + dst;
-        *nrm = add_rn(*nrm, g);
-      }
+      reinterpret_cast<float*>(acc)[dst * K + k] = add_rn(a_old, w);
+      if (k == 0) reinterpret_cast<float*>(norm)[dst] = add_rn(n_old, g);
     }
   }
 }
