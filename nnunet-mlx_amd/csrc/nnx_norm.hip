@@ -253,48 +253,61 @@ __global__ __launch_bounds__(256) void norm_merge_slices_kernel(float4* __restri
   }
 }
 
-// Pass 2: one thread per (b, c) merges the slices' results in slice order.  With `raw`
-// (at most 64 partial rows: no pass 1) it merges the partial rows themselves.
-__global__ __launch_bounds__(64) void norm_merge_final_kernel(const float4* __restrict__ partial,
-                                                              float4* __restrict__ params,
-                                                              const float* __restrict__ beta,
-                                                              const float* __restrict__ gamma,
-                                                              int64_t S, int C, int nparts,
-                                                              int per, int nslices, int raw,
-                                                              float eps) {
-  const int c = blockIdx.x * 64 + threadIdx.x;
+// Pass 2: a wave per (b, c) (four a workgroup): lane l merges entries l, l + 64, ... in
+// order, then the lanes' results merge along a fixed butterfly (lower lane first at every
+// level), and lane 0 writes the parameters.  With `raw` (at most 64 partial rows: no pass 1)
+// the entries are the partial rows themselves, else the slices' results.
+__device__ __forceinline__ double shfl_xor_f64(double v, int o) {
+  const int lo = __shfl_xor((int)(__double_as_longlong(v) & 0xffffffffLL), o);
+  const int hi = __shfl_xor((int)(__double_as_longlong(v) >> 32), o);
+  return __longlong_as_double(((long long)hi << 32) | (unsigned int)lo);
+}
+
+__global__ __launch_bounds__(256) void norm_merge_final_kernel(const float4* __restrict__ partial,
+                                                               float4* __restrict__ params,
+                                                               const float* __restrict__ beta,
+                                                               const float* __restrict__ gamma,
+                                                               int64_t S, int C, int nparts,
+                                                               int per, int nslices, int raw,
+                                                               float eps) {
+  const int lane = threadIdx.x & 63;
+  const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
   const int b = blockIdx.y;
-  if (c >= C) return;
+  if (c >= C) return;  // uniform over the wave; the kernel has no barrier
   const float4* rows = partial + (int64_t)b * nparts * C;
   double n = 0.0, m = 0.0, m2 = 0.0;
-  // eight entries requested per step, then merged in order
   const int count = raw ? nparts : nslices;
-  for (int j0 = 0; j0 < count; j0 += 8) {
-    double en[8], em[8], e2[8];
-#pragma unroll
-    for (int q = 0; q < 8; ++q) {
-      const int j = j0 + q;
-      en[q] = 0.0;
-      em[q] = 0.0;
-      e2[q] = 0.0;
-      if (j < count) {
-        if (raw) {
-          const float4 p = rows[(int64_t)j * C + c];
-          en[q] = p.z;
-          em[q] = p.x;
-          e2[q] = p.y;
-        } else {
-          const int64_t r0 = (int64_t)j * per;
-          const double2 mv = *reinterpret_cast<const double2*>(rows + r0 * C + c);
-          en[q] = rows[(r0 + 1) * C + c].x;
-          em[q] = mv.x;
-          e2[q] = mv.y;
-        }
-      }
+  for (int j = lane; j < count; j += 64) {
+    double en, em, e2;
+    if (raw) {
+      const float4 p = rows[(int64_t)j * C + c];
+      en = p.z;
+      em = p.x;
+      e2 = p.y;
+    } else {
+      const int64_t r0 = (int64_t)j * per;
+      const double2 mv = *reinterpret_cast<const double2*>(rows + r0 * C + c);
+      en = rows[(r0 + 1) * C + c].x;
+      em = mv.x;
+      e2 = mv.y;
     }
-#pragma unroll
-    for (int q = 0; q < 8; ++q) chan_merge(n, m, m2, en[q], em[q], e2[q]);
+    chan_merge(n, m, m2, en, em, e2);
   }
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    const double on = shfl_xor_f64(n, o), om = shfl_xor_f64(m, o), o2 = shfl_xor_f64(m2, o);
+    if (lane & o) {
+      // the partner is the lower lane: its entries come first
+      double pn = on, pm = om, p2 = o2;
+      chan_merge(pn, pm, p2, n, m, m2);
+      n = pn;
+      m = pm;
+      m2 = p2;
+    } else {
+      chan_merge(n, m, m2, on, om, o2);
+    }
+  }
+  if (lane != 0) return;
   const double var = m2 / (double)S;
   float varf = (float)(var > 0.0 ? var : 0.0);
   float scale = 1.0f / sqrtf(varf + eps);
@@ -560,9 +573,9 @@ void instnorm_merge_partials(float4* partials, int nparts, int batch, int64_t sp
   require(nparts >= 1 && batch >= 1 && batch <= 65535 && channels >= 1 && channels <= 512,
           "invalid partial layout");
   ProfScope prof("instnorm_merge", 0.0, 16.0 * (double)batch * nparts * channels, st);
-  const dim3 fgrid((unsigned)ceil_div(channels, 64), batch);
+  const dim3 fgrid((unsigned)ceil_div(channels, 4), batch);  // a wave per (b, c)
   if (nparts <= 64) {
-    hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(64), 0, st, partials, params, beta,
+    hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(256), 0, st, partials, params, beta,
                        gamma, spatial, channels, nparts, 1, nparts, 1, eps);
     launch_check("instnorm merge partials");
     return;
@@ -574,7 +587,7 @@ void instnorm_merge_partials(float4* partials, int nparts, int batch, int64_t sp
   hipLaunchKernelGGL(norm_merge_slices_kernel, dim3(nslices, batch), dim3(256), 0, st, partials,
                      channels, nparts, per);
   launch_check("instnorm merge slices");
-  hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(64), 0, st, partials, params, beta,
+  hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(256), 0, st, partials, params, beta,
                      gamma, spatial, channels, nparts, per, nslices, 0, eps);
   launch_check("instnorm merge partials");
 }
