@@ -42,6 +42,43 @@ VOLUME_SHAPE = (1, 101, 768, 768)
 PATCH = (128, 128, 128)
 
 
+class DevicePeak:
+    """Device memory a workload holds at its peak, in GB: the bytes in use on the GPU
+    (hipMemGetInfo: the library's own allocations, which it keeps for reuse, and torch's
+    cached blocks) above what was in use when the object was made, plus whatever part of
+    torch's cached-allocator peak was released again before the reading."""
+
+    def __init__(self) -> None:
+        import torch
+
+        torch.cuda.synchronize()
+        free, total = torch.cuda.mem_get_info()
+        self.base = total - free
+        torch.cuda.reset_peak_memory_stats()
+
+    def gb(self) -> float:
+        import torch
+
+        torch.cuda.synchronize()
+        free, total = torch.cuda.mem_get_info()
+        released = torch.cuda.max_memory_reserved() - torch.cuda.memory_reserved()
+        return round((total - free - self.base + released) / 1e9, 2)
+
+
+def conv_mfma_frac(classes: dict, precision: str) -> float | None:
+    """Rate of the 3x3x3 convolution kernels (algorithmic float32-product FLOPs over their
+    launch time) as a fraction of the MFMA peak of the arithmetic they issue: 157.3 TFLOP/s
+    for float32 products, a third of the dense fp16 peak for fp16-split (three products per
+    term), the dense bf16 peak for bf16."""
+    conv = [c for n, c in classes.items()
+            if n.startswith(("conv3d_igemm", "conv3d_x3", "conv3d_wino"))]
+    flops = sum(c["flops"] for c in conv)
+    ms = sum(c["ms"] for c in conv)
+    peak = {"fp32": PEAK_FP32_MFMA_TFLOPS, "fp32-split": PEAK_FP16_MFMA_TFLOPS / SPLIT_PRODUCTS,
+            "bf16": PEAK_FP16_MFMA_TFLOPS, "bf16-mixed": PEAK_FP16_MFMA_TFLOPS}[precision]
+    return round(flops / (ms * 1e-3) / 1e12 / peak, 4) if ms else None
+
+
 def liver_spec():
     from nnunet_mlx.model.topology import PlainConvUNetSpec
 
@@ -631,6 +668,7 @@ def ensemble_workload(args) -> int:
                                        (1, 3, 4, 6, 6, 6, 6), (1,) * 6)
         patch, seeds, axes, precision = (128, 160, 160), (4,), (), "bf16-mixed"
         volume = synthetic_ct()
+    peak = DevicePeak()
     nets = []
     for seed in seeds:
         net = build_network(spec, precision=precision)
@@ -652,6 +690,7 @@ def ensemble_workload(args) -> int:
             labels = sw.average_fold_labels(nets, d_volume, return_device=True, **kwargs)
         torch.cuda.synchronize()
         step_s = (time.perf_counter() - t0) / args.steps
+    device_peak_gb = peak.gb()
     kernels, roofline = kernel_table(prof.classes, steps=args.steps, traffic=False)
     steps = [len(s) for s in sw.compute_steps([max(a, b) for a, b in zip(volume.shape[1:], patch)],
                                               patch, step_fraction=0.5)]
@@ -678,6 +717,8 @@ def ensemble_workload(args) -> int:
                                f"{tiles * len(nets) * 2 ** len(axes)} forwards",
                    "label_counts": torch.bincount(labels.reshape(-1).to(torch.int64),
                                                   minlength=spec.num_classes).tolist()},
+        "conv3d_mfma_frac": conv_mfma_frac(prof.classes, precision),
+        "device_peak_gb": device_peak_gb,
         "kernels": kernels, "roofline": roofline, "cpu_baseline": baseline,
     }
     for net in nets:
@@ -702,6 +743,7 @@ def raw_case_workload(args) -> int:
 
     torch.cuda.set_device(0)
     raw = synthetic_raw_ct()
+    peak = DevicePeak()
     with tempfile.TemporaryDirectory(prefix="nnx-bench-") as tmp:
         folder = write_random_model_folder(Path(tmp) / "liver", liver_spec(), patch_size=PATCH,
                                            seeds=(1,), labels=("liver", "tumor"))
@@ -734,6 +776,7 @@ def raw_case_workload(args) -> int:
             stages[k] = stages.get(k, 0.0) + v / args.steps
     torch.cuda.synchronize()
     step_s = (time.perf_counter() - t0) / args.steps
+    device_peak_gb = peak.gb()
     voxels = int(np.prod(raw.shape[1:]))
     line = {
         "metric": "raw-case voxels/s, liver CT 512x512x120 int16 -> labels on the raw grid "
@@ -751,6 +794,7 @@ def raw_case_workload(args) -> int:
                    "preprocessed_shape": list(details["preprocessed_shape"]),
                    "label_counts": np.bincount(labels.ravel(), minlength=3).tolist()},
         "stages_s": {k: round(v, 4) for k, v in stages.items()},
+        "device_peak_gb": device_peak_gb,
         "roofline": None, "cpu_baseline": None,
     }
     for model in bundle.models:
@@ -831,6 +875,7 @@ def main() -> int:
     shape = (1, *args.shape)
     spec = liver_spec()
     weights = random_weights(spec, seed=1)
+    peak = DevicePeak()
     net = build_network(spec, precision=args.precision)
     net.load_weights(weights)
     print(f"[bench] synthesising volume {shape}", file=sys.stderr, flush=True)
@@ -857,15 +902,11 @@ def main() -> int:
     counts = np.bincount(labels.cpu().numpy().view(np.uint16).ravel(), minlength=3)
     print(f"[bench] {step_s:.3f} s per case; label counts {counts.tolist()}", file=sys.stderr, flush=True)
 
+    device_peak_gb = peak.gb()
     classes = prof.classes
     kernels, roofline = kernel_table(classes, steps=args.steps)
-    conv = [c for n, c in classes.items() if n.startswith(("conv3d_igemm", "conv3d_x3", "conv3d_wino"))]
-    conv_flops = sum(c["flops"] for c in conv)
-    conv_ms = sum(c["ms"] for c in conv)
     # 3x3x3 convolution rate against the float32-class MFMA peak of the arithmetic used
-    conv_peak = {"fp32": PEAK_FP32_MFMA_TFLOPS, "fp32-split": PEAK_FP16_MFMA_TFLOPS / SPLIT_PRODUCTS,
-                 "bf16": PEAK_FP16_MFMA_TFLOPS, "bf16-mixed": PEAK_FP16_MFMA_TFLOPS}[args.precision]
-    conv_frac = conv_flops / (conv_ms * 1e-3) / 1e12 / conv_peak if conv_ms else None
+    conv_frac = conv_mfma_frac(classes, args.precision)
 
     alt = None
     if not args.no_alt:
@@ -876,13 +917,18 @@ def main() -> int:
         alt_net.share_workspace(net)
         sw.average_fold_labels((alt_net,), volume, return_device=True, **kwargs)
         torch.cuda.synchronize()
-        t0 = time.perf_counter()
-        alt_labels = sw.average_fold_labels((alt_net,), volume, return_device=True, **kwargs)
-        torch.cuda.synchronize()
-        alt_s = time.perf_counter() - t0
+        with _native.KernelProfile() as alt_prof:
+            t0 = time.perf_counter()
+            alt_labels = sw.average_fold_labels((alt_net,), volume, return_device=True, **kwargs)
+            torch.cuda.synchronize()
+            alt_s = time.perf_counter() - t0
         agree = float((alt_labels == labels).float().mean())
+        alt_conv = conv_mfma_frac(alt_prof.classes, other)
         alt = {"precision": other, "value": round(voxels / alt_s, 1),
-               "ms_per_step": round(alt_s * 1e3, 2), "label_agreement": round(agree, 7)}
+               "ms_per_step": round(alt_s * 1e3, 2), "label_agreement": round(agree, 7),
+               "conv3d_mfma_frac": alt_conv,
+               "conv3d_mfma_peak_tflops": PEAK_FP32_MFMA_TFLOPS if other == "fp32"
+               else round(PEAK_FP16_MFMA_TFLOPS / SPLIT_PRODUCTS, 1)}
         alt_net.close()
         del alt_labels
 
@@ -926,8 +972,9 @@ def main() -> int:
         },
         "ms_per_forward": round(step_s * 1e3 / nforwards, 3),
         "ms_per_tile": round(step_s * 1e3 / ntiles, 2),
-        "conv3d_mfma_frac": round(conv_frac, 4) if conv_frac else None,
+        "conv3d_mfma_frac": conv_frac,
         "pcie_inclusive_voxels_per_s": round(pcie, 1) if pcie else None,
+        "device_peak_gb": device_peak_gb,
         "other_precision": alt,
         "roofline": roofline,
         "cpu_baseline": baseline,

@@ -183,23 +183,28 @@ __global__ __launch_bounds__(256) void norm_merge_kernel(const float2* __restric
 
 // Same merge for partials that carry their own counts (per-tile partials written by the
 // convolution epilogue: (mean, M2, n, 0) at partial[(b * nparts + i) * C + c]), in two passes.
-// Pass 1: block (j, b) merges rows [j * per, (j + 1) * per) of item b, the last block
-// (j = gridDim.x - 1) every row from (gridDim.x - 1) * per to nparts, so with per >= 2 every
-// slice has at least two rows to hold its result; a thread takes
+// Pass 1: block (j, b) of S = gridDim.x blocks merges rows [slice_row(j), slice_row(j + 1))
+// of item b, slice_row(j) = floor(j * nparts / S): balanced slices (their lengths differ by
+// at most one row), each at least two rows long when nparts >= 2 S, so every slice has two
+// rows to hold its result; a thread takes
 // channel cb + t % CB of every G-th row (CB = min(C, 256) channels a pass, G = 256 / CB
 // row groups), so each row is read as one contiguous run; the groups are merged through
 // LDS, and the slice's (mean, M2) in float64 and its count are written over the slice's
 // own first two rows (read by this block only, and no longer needed).
+__device__ __forceinline__ int64_t slice_row(int j, int nparts, int nslices) {
+  return (int64_t)j * nparts / nslices;
+}
+
 __global__ __launch_bounds__(256) void norm_merge_slices_kernel(float4* __restrict__ partial, int C,
-                                                                int nparts, int per) {
+                                                                int nparts) {
   __shared__ double sn[256], sm[256], s2[256];
   const int j = blockIdx.x, b = blockIdx.y;
   const int t = threadIdx.x;
   const int CB = C < 256 ? C : 256;
   const int G = 256 / CB;
   const int g = t / CB;
-  const int r0 = j * per;
-  const int r1 = j + 1 == (int)gridDim.x ? nparts : r0 + per;
+  const int r0 = (int)slice_row(j, nparts, gridDim.x);
+  const int r1 = (int)slice_row(j + 1, nparts, gridDim.x);
   float4* rows = partial + (int64_t)b * nparts * C;
   // (mean, M2) as a double pair and the count, per channel of this pass
   double res_m[2], res_2[2];
@@ -268,7 +273,7 @@ __global__ __launch_bounds__(256) void norm_merge_final_kernel(const float4* __r
                                                                const float* __restrict__ beta,
                                                                const float* __restrict__ gamma,
                                                                int64_t S, int C, int nparts,
-                                                               int per, int nslices, int raw,
+                                                               int nslices, int raw,
                                                                float eps) {
   const int lane = threadIdx.x & 63;
   const int c = blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -285,7 +290,7 @@ __global__ __launch_bounds__(256) void norm_merge_final_kernel(const float4* __r
       em = p.x;
       e2 = p.y;
     } else {
-      const int64_t r0 = (int64_t)j * per;
+      const int64_t r0 = slice_row(j, nparts, nslices);
       const double2 mv = *reinterpret_cast<const double2*>(rows + r0 * C + c);
       en = rows[(r0 + 1) * C + c].x;
       em = mv.x;
@@ -576,19 +581,18 @@ void instnorm_merge_partials(float4* partials, int nparts, int batch, int64_t sp
   const dim3 fgrid((unsigned)ceil_div(channels, 4), batch);  // a wave per (b, c)
   if (nparts <= 64) {
     hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(256), 0, st, partials, params, beta,
-                       gamma, spatial, channels, nparts, 1, nparts, 1, eps);
+                       gamma, spatial, channels, nparts, nparts, 1, eps);
     launch_check("instnorm merge partials");
     return;
   }
-  // ~2048 blocks in all; slices of per = floor(nparts / nslices) >= 2 rows (a slice's result
-  // takes its first two rows), the last slice also taking the remainder
+  // ~2048 blocks in all; nslices <= nparts / 2 balanced slices of at least two rows each (a
+  // slice's result takes its first two rows)
   const int nslices = (int)std::max<int64_t>(1, std::min<int64_t>(ceil_div(2048, batch), nparts / 2));
-  const int per = nparts / nslices;
   hipLaunchKernelGGL(norm_merge_slices_kernel, dim3(nslices, batch), dim3(256), 0, st, partials,
-                     channels, nparts, per);
+                     channels, nparts);
   launch_check("instnorm merge slices");
   hipLaunchKernelGGL(norm_merge_final_kernel, fgrid, dim3(256), 0, st, partials, params, beta,
-                     gamma, spatial, channels, nparts, per, nslices, 0, eps);
+                     gamma, spatial, channels, nparts, nslices, 0, eps);
   launch_check("instnorm merge partials");
 }
 

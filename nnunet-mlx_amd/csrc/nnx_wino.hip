@@ -568,10 +568,12 @@ __global__ void pack_wino_weight_kernel(const float* __restrict__ w, uint4* __re
 
 }  // namespace
 
+// Layers outside this set take the direct split kernel (the route is chosen with it).
 bool conv_wino_supported(const ConvGeom& g, int c1, int c2, int cout) {
   for (int i = 0; i < 3; ++i)
     if (g.k[i] != 3 || g.s[i] != 1) return false;
-  return cout % 32 == 0 && c1 % kWChunk == 0 && c2 % kWChunk == 0 && c1 > 0;
+  return cout % 32 == 0 && c1 % kWChunk == 0 && c2 % kWChunk == 0 && c1 > 0 && c2 >= 0 &&
+         c1 + c2 <= kMaxChannels;
 }
 
 int conv_wino_stats_tiles(const ConvGeom& g) {
@@ -611,7 +613,7 @@ void conv3d_wino(const float* x1, int c1, const float* x2, int c2, const void* p
   require(c2 == 0 || x2, "invalid convolution inputs");
   require(conv_wino_supported(g, c1, c2, cout),
           "the Winograd convolution takes stride-1 3x3x3 layers with C_out % 32 == 0 and input "
-          "channel counts that are multiples of 16");
+          "channel counts that are multiples of 16, at most 1024 input channels in all");
   require(scale > 0.f && std::isfinite(scale), "weight scale must be positive");
   require(!(n1.params && n2.params) || n1.slope == n2.slope,
           "pending normalisations of one convolution must share the LeakyReLU slope");
@@ -651,7 +653,6 @@ void conv3d_wino(const float* x1, int c1, const float* x2, int c2, const void* p
   const double bytes = 4.0 * ((double)g.batch * g.in[0] * g.in[1] * g.in[2] * (c1 + c2) +
                               out_vox * cout);
   ProfScope prof("conv3d_wino", flops, bytes, st);
-  require(c1 + c2 <= kMaxChannels, "too many input channels for the Winograd convolution");
   hipLaunchKernelGGL(wino_x3_kernel, dim3(a.nwg), dim3(kWThreads), 0, st, a);
   launch_check("conv3d_winograd");
 }

@@ -197,9 +197,34 @@ def run(*, weights_path: PathLike, image_paths: Sequence[PathLike], output_dir: 
         save_probabilities=save_probabilities)
 
 
+def source_signature(folder: Path, checkpoint_name: str) -> tuple[tuple, ...]:
+    """Stat records of the files a loaded model was built from: ``plans.json``,
+    ``dataset.json`` and each ``fold_*/<checkpoint_name>/{state.json,weights.safetensors}``
+    (src/nnunet_mlx/medmlx.py:454-469).  Each record is (relative path, device, inode,
+    size, modification time ns, status-change time ns), so a rewrite, a replacement or a
+    ``touch`` of any of them changes the signature without the weights being read again."""
+    files = [folder / "plans.json", folder / "dataset.json"]
+    for fold in sorted(folder.glob(f"fold_*/{checkpoint_name}")):
+        files += [fold / "state.json", fold / "weights.safetensors"]
+    records = []
+    for path in files:
+        try:
+            st = path.stat()
+        except OSError as error:
+            raise ContractError(f"model file missing or unreadable: {path}") from error
+        records.append((path.relative_to(folder).as_posix(), st.st_dev, st.st_ino, st.st_size,
+                        st.st_mtime_ns, st.st_ctime_ns))
+    return tuple(records)
+
+
 class NnUNetModel:
     """One loaded model folder reused for serial cases until closed
-    (src/nnunet_mlx/medmlx.py:486-587)."""
+    (src/nnunet_mlx/medmlx.py:486-587).
+
+    The model folder must stay as it was while the model is loaded: its source signature
+    (``source_signature``) is taken before loading, checked again after loading and before
+    every case, and a difference raises ``ContractError`` (load the model again to pick up
+    the edit)."""
 
     def __init__(self, *, weights_path: PathLike, configuration: str = "3d_fullres",
                  folds: Sequence[int | str] | None = None,
@@ -223,8 +248,13 @@ class NnUNetModel:
                          "checkpoint_name": checkpoint_name, "source_profile": source_profile,
                          "precision": precision, "step_fraction": step_fraction,
                          "use_mirroring": use_mirroring}
+        self._signature = source_signature(self._folder, checkpoint_name)
         bundle = load_model_bundle(self._folder, configuration=configuration,
                                    folds=self._options["folds"], checkpoint_name=checkpoint_name)
+        if source_signature(self._folder, checkpoint_name) != self._signature:
+            for model in bundle.models:
+                model.close()
+            raise ContractError("the model folder was modified during loading; load the model again")
         if not use_mirroring:
             bundle = replace(bundle, mirroring_axes=())
         self._state = (bundle, predictor(bundle, step_fraction=float(step_fraction)))
@@ -239,6 +269,9 @@ class NnUNetModel:
                      grid_of: str = "image_paths") -> dict:
         if self._state is None:
             raise RuntimeError("nnU-Net model is closed")
+        if source_signature(self._folder, self._options["checkpoint_name"]) != self._signature:
+            raise ContractError("the model folder changed after this model was loaded; "
+                                "load the model again")
         return segment_case(prepared=self._state, grid_of=grid_of, weights_path=self._folder,
                             image_paths=image_paths, output_dir=output_dir, overwrite=overwrite,
                             save_probabilities=save_probabilities, **self._options)

@@ -76,11 +76,16 @@ def item_input(name: str, item: int) -> np.ndarray:
 
 def probe(logits: np.ndarray) -> dict[str, np.ndarray]:
     """Probes of one item's channels-last logits (Z, Y, X, K): every 8th voxel per axis from
-    offset 3, the 16^3 corner block (zero-padding region of every convolution), and the
-    float64 per-class sums and sums of squares over the whole output."""
+    offset 3; every 7th voxel per axis from offsets (1, 2, 5) ("residues": 7 is prime to
+    every power of two, so the sample holds each (z mod 2^a, y mod 2^b, x mod 2^c) position
+    of the convolution kernels' output boxes and tiles, which the 8-stride sample, always at
+    box position (3, 3, 3) of a 4x8x8 box, does not); the 16^3 corner block (zero-padding
+    region of every convolution); and the float64 per-class sums and sums of squares over
+    the whole output."""
     v = np.asarray(logits, dtype=np.float32)
     return {
         "strided": np.ascontiguousarray(v[3::8, 3::8, 3::8]),
+        "residues": np.ascontiguousarray(v[1::7, 2::7, 5::7]),
         "corner": np.ascontiguousarray(v[:16, :16, :16]),
         "sums": v.astype(np.float64).sum(axis=(0, 1, 2)),
         "squares": (v.astype(np.float64) ** 2).sum(axis=(0, 1, 2)),

@@ -215,3 +215,39 @@ def test_default_batch_respects_the_activation_limit():
     assert sw.default_tiles_per_batch([SimpleNamespace(spec=liver)], (16, 16, 16), 8) == 4
     # at least one tile, however large the patch
     assert sw.default_tiles_per_batch([SimpleNamespace(spec=liver)], (512, 512, 512), 8) == 1
+
+
+def test_source_signature_tracks_every_model_file(tmp_path):
+    """The loaded-model signature covers plans.json, dataset.json and each fold's state and
+    weights (src/nnunet_mlx/medmlx.py:454-469): a touch of any one of them changes it, a
+    missing one raises, and files outside that set do not count."""
+    import os
+
+    from nnunet_mlx.medmlx import source_signature
+
+    folder = tmp_path / "model"
+    files = ["plans.json", "dataset.json"]
+    for fold in ("fold_0", "fold_all"):
+        files += [f"{fold}/checkpoint_final/state.json",
+                  f"{fold}/checkpoint_final/weights.safetensors"]
+    for name in files:
+        (folder / name).parent.mkdir(parents=True, exist_ok=True)
+        (folder / name).write_text("x")
+    (folder / "notes.txt").write_text("not a model file")
+    (folder / "fold_0" / "checkpoint_best").mkdir()
+    (folder / "fold_0" / "checkpoint_best" / "state.json").write_text("{}")
+    base = source_signature(folder, "checkpoint_final")
+    assert [r[0] for r in base] == files[:2] + sorted(files[2:])
+    assert source_signature(folder, "checkpoint_final") == base
+    (folder / "notes.txt").write_text("edited")
+    os.utime(folder / "fold_0" / "checkpoint_best" / "state.json", ns=(1, 1))
+    assert source_signature(folder, "checkpoint_final") == base
+    for name in files:
+        st = (folder / name).stat()
+        os.utime(folder / name, ns=(st.st_atime_ns, st.st_mtime_ns + 10**9))
+        now = source_signature(folder, "checkpoint_final")
+        assert now != base, name
+        base = now
+    (folder / files[-1]).unlink()
+    with pytest.raises(ContractError, match="missing"):
+        source_signature(folder, "checkpoint_final")

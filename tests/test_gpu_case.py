@@ -182,6 +182,32 @@ def test_loaded_model_and_named_model_agree_with_run(tmp_path):
         model.run(image_path=tmp_path / "b.nii.gz", output_dir=tmp_path / "closed")
 
 
+@pytest.mark.parametrize("changed", ["plans.json", "fold_0/checkpoint_final/weights.safetensors"])
+def test_loaded_model_rejects_changed_sources_and_a_reload_picks_them_up(tmp_path, changed):
+    """A loaded model refuses to run once a file it was built from has been touched
+    (src/nnunet_mlx/medmlx.py:534,565; tests/test_medmlx.py:369-391); loading again
+    serves the folder as it now is."""
+    import os
+
+    from nnunet_mlx import medmlx
+    from nnunet_mlx.errors import ContractError
+
+    folder = ct_model_folder(tmp_path / "model")
+    synthetic_ct(tmp_path / "a.nii.gz", seed=4)
+    print(f"raw case: loaded model, then {changed} touched", flush=True)
+    with medmlx.load_model(weights_path=folder) as model:
+        model.run(image_paths=[tmp_path / "a.nii.gz"], output_dir=tmp_path / "before")
+        target = folder / changed
+        st = target.stat()
+        os.utime(target, ns=(st.st_atime_ns, st.st_mtime_ns + 1_000_000_000))
+        with pytest.raises(ContractError, match="changed"):
+            model.run(image_paths=[tmp_path / "a.nii.gz"], output_dir=tmp_path / "stale")
+    assert not (tmp_path / "stale").exists() or not any((tmp_path / "stale").iterdir())
+    with medmlx.load_model(weights_path=folder) as model:
+        result = model.run(image_paths=[tmp_path / "a.nii.gz"], output_dir=tmp_path / "fresh")
+    assert (tmp_path / "fresh").is_dir() and nifti.read_nifti(result["outputs"]["mask"]).array.size
+
+
 def test_cli_predicts_an_upstream_folder(tmp_path, monkeypatch):
     """``nnunet-mlx predict -m`` converts an upstream results folder (cached) and predicts
     the input folder; the labels equal run() on the converted folder."""

@@ -185,6 +185,9 @@ def test_conv3d_winograd_rejects_unsupported_layers(lib):
     for c1, c2, cout, scale, needle in [(12, 0, 32, 1.0, "multiples of 16"),
                                         (32, 0, 24, 1.0, "multiples of 16"),
                                         (32, 8, 32, 1.0, "multiples of 16"),
+                                        # both inputs on the grid, 1040 channels in all: past
+                                        # the kernel's 1024-channel parameter table
+                                        (528, 512, 32, 1.0, "at most 1024"),
                                         (32, 0, 32, 0.0, "scale")]:
         rc = lib.nnx_conv3d_winograd(x.data_ptr(), c1, x.data_ptr() if c2 else None, c2,
                                      packed.data_ptr(), scale, None, y.data_ptr(), 1, size, cout,
