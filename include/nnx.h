@@ -51,7 +51,11 @@ const char* nnx_version(void);
  * nnx_conv3d_split.  A first convolution with 1, 2 or 4 input channels uses split products
  * too, with a per-tile power-of-two scale of the raw input (nnx_conv3d_direct_small_cin_split);
  * other first convolutions keep float32 products.  Meets the float32 logits tolerance;
- * hidden activations must stay below 65504 in magnitude (they are normalised, so they do). */
+ * hidden activations must stay below 65504 in magnitude at layers on the direct split kernels
+ * and below 8188 at the Winograd layers (the input transform sums up to 8 of them before the
+ * split).  They are InstanceNorm outputs, so with ordinary affine parameters they do; a
+ * checkpoint whose activations exceed the range makes the forward fail with a ContractError
+ * that names the layer (nnx_set_layer_checks), never a silent result. */
 #define NNX_PRECISION_FP32_SPLIT 1
 /* bf16 operands with float32 accumulation (the pancreas config's bf16): the 3-D
  * convolutions after the first one and the transposed convolutions round their weights
@@ -173,6 +177,17 @@ int nnx_sw_predict_custom(nnx_forward_fn const* forwards, void* const* users, in
 void nnx_sw_release(void);
 
 /* ---- kernel families (device pointers, caller-owned) ----------------------------- */
+
+/* Layer checks on (1) or off (0) for every later forward of this process: after each
+ * convolution, transposed convolution and head the stream is synchronised and the layer's
+ * output scanned, and the first layer with non-finite values fails the forward with
+ * NNX_ERR_NONFINITE and an error naming its parameter (NNX_CHECK_LAYERS=1 in the environment
+ * turns them on for the whole process).  The host uses them to name the layer after a
+ * forward has produced non-finite logits; they serialise the forward.
+ * Replaces nothing in the reference, whose float32 path has no operand range: it names the
+ * layer where the split-fp16 precisions meet theirs (its inputs beyond 65504, or beyond
+ * 8188 at a Winograd layer, whose input transform adds up to 8 of them). */
+int nnx_set_layer_checks(int enable);
 
 /* Count non-finite float32 values; *d_count (device uint32) is overwritten.
  * Replaces the finite checks of _validate_request (src/nnunet_mlx/prediction/sliding_window.py:470-477). */

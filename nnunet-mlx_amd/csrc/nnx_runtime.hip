@@ -2,6 +2,7 @@
 // ResidualEncoderUNet with BasicBlockD/BottleneckD), parameter loading and repacking,
 // the activation workspace, the forward pass and the GPU-resident sliding window, and
 // every extern "C" entry point of include/nnx.h.
+#include <atomic>
 #include <algorithm>
 #include <cmath>
 #include <cstdlib>
@@ -422,16 +423,20 @@ Shape3 conv_out(const Shape3& in, const ConvNorm& c) {
   return o;
 }
 
-// Layer checks (NNX_CHECK_LAYERS=1 in the environment): after every convolution, transposed
-// convolution and head the stream is synchronised and the layer's output is scanned for
-// non-finite values; the first such layer fails the forward with its parameter name and the
-// batch geometry.  A diagnostic for wrong results; off by default (it serialises the forward).
+// Layer checks (NNX_CHECK_LAYERS=1 in the environment, or nnx_set_layer_checks(1)): after
+// every convolution, transposed convolution and head the stream is synchronised and the
+// layer's output is scanned for non-finite values; the first such layer fails the forward
+// with its parameter name and the batch geometry.  A diagnostic, off by default (it
+// serialises the forward): the host turns it on to name the layer when a forward has
+// produced non-finite logits.
+std::atomic<bool> g_layer_checks{false};
+
 bool layer_checks_enabled() {
-  static const bool on = [] {
+  static const bool env = [] {
     const char* v = std::getenv("NNX_CHECK_LAYERS");
     return v != nullptr && v[0] == '1';
   }();
-  return on;
+  return env || g_layer_checks.load(std::memory_order_relaxed);
 }
 
 void check_layer(const std::string& name, const float* buf, int64_t n, int batch, hipStream_t st) {
@@ -1009,6 +1014,10 @@ int nnx_model_share_workspace(nnx_model* model, nnx_model* owner) {
     if (!owner->ws) owner->ws = std::make_shared<Workspace>();
     model->ws = owner->ws;
   });
+}
+
+int nnx_set_layer_checks(int enable) {
+  return guarded([&] { g_layer_checks.store(enable != 0, std::memory_order_relaxed); });
 }
 
 int nnx_forward(nnx_model* model, const float* d_in, float* d_out, int n, const int* spatial,

@@ -119,6 +119,7 @@ _SIGNATURES: dict[str, tuple[Any, list[Any]]] = {
          c_void_p, c_void_p, c_void_p, c_void_p],
     ),
     "nnx_sw_release": (None, []),
+    "nnx_set_layer_checks": (ctypes.c_int, [ctypes.c_int]),
     "nnx_count_nonfinite": (ctypes.c_int, [c_void_p, ctypes.c_int64, c_void_p, c_void_p]),
     "nnx_instnorm_workspace_bytes": (ctypes.c_size_t, [ctypes.c_int, ctypes.c_int64, ctypes.c_int]),
     "nnx_instnorm_lrelu": (
@@ -338,6 +339,28 @@ def check(status: int, what: str = "") -> None:
     if status in (NNX_ERR_INVALID, NNX_ERR_NONFINITE):
         raise ContractError(message)
     raise NativeError(message)
+
+
+def name_nonfinite_layer(error: ContractError, rerun) -> None:
+    """A forward produced non-finite logits (``error``): run it again (``rerun``) with the
+    library's layer checks on (nnx_set_layer_checks) and raise ContractError naming the first
+    layer whose output held non-finite values.  With finite inputs and weights that is a layer
+    whose input activations left the split-fp16 operand range.  Re-raises ``error`` when no
+    layer check fires."""
+    lib = load()
+    check(lib.nnx_set_layer_checks(1), "nnx_set_layer_checks")
+    try:
+        rerun()
+    except ContractError as located:
+        if "layer check" not in str(located):
+            raise
+        raise ContractError(
+            f"non-finite logits: {located}.  The split-fp16 precisions take layer inputs below "
+            "65504 in magnitude (8188 at Winograd layers, whose input transform sums 8 of "
+            "them); build this network with precision='fp32'") from error
+    finally:
+        lib.nnx_set_layer_checks(0)
+    raise error
 
 
 def ints(values) -> ctypes.Array:

@@ -183,7 +183,17 @@ class NativeNetwork:
         tiles = values.contiguous()
         out = torch.empty((*tiles.shape[:-1], self.spec.num_classes), dtype=torch.float32,
                           device=tiles.device)
-        return self.forward_into(tiles, out)
+        self.forward_into(tiles, out)
+        # non-finite logits from finite inputs and weights: name the layer where they arose
+        count = torch.empty(1, dtype=torch.int32, device=tiles.device)
+        _native.check(self._lib.nnx_count_nonfinite(
+            _native.ptr(out), out.numel(), _native.ptr(count),
+            _native.stream_handle(tiles.device)), "nnx_count_nonfinite")
+        if int(count.item()) != 0:
+            _native.name_nonfinite_layer(
+                ContractError("the network forward produced non-finite logits"),
+                lambda: self.forward_into(tiles, torch.empty_like(out)))
+        return out
 
     def eval(self) -> NativeNetwork:
         return self

@@ -15,6 +15,10 @@ from nnunet_mlx.named_models import (READINESS, PathLike, input_channels, model_
 MODEL = {
     "id": "nnunet-autopet", "label": "nnU-Net AutoPET II", "task": "segmentation",
     "readiness": READINESS, "run": "nnunet_mlx.named_models.autopet:run",
+    # Measured MI355X device peak (library workspace + torch allocations) for a 2x284x400x400
+    # case, five folds, 8 mirror views, 32 views a forward (bench.py --workload autopet-sw);
+    # larger inputs need more.
+    "peak_memory_gb": 51.4,
     "summary": "Tumor lesion segmentation of co-registered CT and SUV PET volumes.",
     "labels": {"1": "tumor"},
 }

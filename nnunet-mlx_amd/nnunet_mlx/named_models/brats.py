@@ -16,6 +16,10 @@ from nnunet_mlx.named_models import (READINESS, PathLike, input_channels, model_
 MODEL = {
     "id": "nnunet-brats2021", "label": "nnU-Net BraTS 2021", "task": "segmentation",
     "readiness": READINESS, "run": "nnunet_mlx.named_models.brats:run",
+    # Measured MI355X device peak (library workspace + torch allocations) for a 4x155x240x240
+    # case, five folds, 8 mirror views, 32 views a forward (bench.py --workload brats-sw);
+    # larger inputs need more.
+    "peak_memory_gb": 62.4,
     "summary": "Dataset002_BRATS19 with its original BAMF labels.",
     "labels": {"1": "edema", "2": "nonenhancing", "3": "empty", "4": "enhancing"},
 }

@@ -12,6 +12,10 @@ MODEL = {
     "id": "nnunet-liver", "label": "nnU-Net liver CT", "task": "segmentation",
     "readiness": READINESS, "run": "nnunet_mlx.named_models.liver:run",
     "cohort": "nnunet_mlx.named_models.liver:load_model",
+    # Measured MI355X device peak (library workspace + torch allocations) for a 512x512x120
+    # liver CT preprocessed to 300x534x534, 8 mirror views, 32 views a forward (bench.py
+    # --workload liver-raw-case); larger inputs need more.
+    "peak_memory_gb": 63.3,
     "summary": "Liver and liver cancer segmentation of one CT volume.",
     "labels": {"1": "liver", "2": "cancer"},
 }

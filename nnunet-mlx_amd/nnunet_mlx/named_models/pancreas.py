@@ -11,6 +11,10 @@ from nnunet_mlx.named_models import READINESS, PathLike, model_folder, segment_f
 MODEL = {
     "id": "nnunet-pancreas", "label": "Pancreas segmentation", "task": "segmentation",
     "readiness": READINESS, "run": "nnunet_mlx.named_models.pancreas:run",
+    # Measured MI355X device peak (library workspace + torch allocations) for a 101x768x768
+    # CT, ResEnc-L in bf16-mixed, 32 patches a forward (bench.py --workload pancreas-sw);
+    # larger inputs need more.
+    "peak_memory_gb": 75.4,
     "summary": "PancCTMultiTalentV2 pancreas and cancer segmentation.",
     "labels": {"1": "pancreas", "2": "cancer"},
 }

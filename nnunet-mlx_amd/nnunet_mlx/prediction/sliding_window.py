@@ -260,10 +260,20 @@ def _run(models, request: _Request, *, want_logits: bool, want_labels: bool):
             if m.spec.num_classes != request.num_classes:
                 raise ContractError("model output channels do not match num_classes")
         handles = (ctypes.c_void_p * len(models))(*[m.handle.value for m in models])
-        with torch.cuda.device(request.device):
-            _native.check(lib.nnx_sw_predict(
-                handles, len(models), ctypes.byref(request.config), _native.ptr(request.volume),
-                _native.ptr(logits), _native.ptr(labels), stream), "nnx_sw_predict")
+
+        def native_loop() -> None:
+            with torch.cuda.device(request.device):
+                _native.check(lib.nnx_sw_predict(
+                    handles, len(models), ctypes.byref(request.config),
+                    _native.ptr(request.volume), _native.ptr(logits), _native.ptr(labels),
+                    stream), "nnx_sw_predict")
+
+        try:
+            native_loop()
+        except ContractError as error:
+            if "non-finite logits" not in str(error):
+                raise
+            _native.name_nonfinite_layer(error, native_loop)
     else:
         _run_callables(models, request, logits, labels)
     return logits, labels

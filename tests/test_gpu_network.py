@@ -196,3 +196,37 @@ def test_forward_rejects_items_beyond_the_activation_limit(device):
     with pytest.raises(ContractError, match="2\\^31"):
         net(x)
     net.close()
+
+
+def test_activations_beyond_the_split_range_name_the_layer():
+    """A checkpoint whose activations leave the split-fp16 operand range (an InstanceNorm
+    gamma of 1e4 after an outlier voxel: normalised activations near 1e5 at the input of the
+    second convolution, beyond fp16's 65504) makes the fp32-split forward and sliding window
+    raise a ContractError that names the first layer with non-finite output, never a silent
+    result; the fp32 precision takes the same checkpoint and holds the float32 bar."""
+    from nnunet_mlx.errors import ContractError
+    from nnunet_mlx.prediction import sliding_window as sw
+
+    spec = PlainConvUNetSpec(1, 2, (32, 64), K3 * 2, ((1, 1, 1), (2, 2, 2)), (2, 2), (2,))
+    weights = random_weights(spec, seed=3)
+    weights["enc0.block0.norm.weight"] = np.full(32, 1e4, dtype=np.float32)
+    x = np.random.default_rng(5).standard_normal((2, 16, 16, 16, 1)).astype(np.float32)
+    x[:, 8, 8, 8, 0] = 1e4
+    print("split range: gamma 1e4 after an outlier voxel, 16^3 batch 2", flush=True)
+    net = build_network(spec)  # fp32-split
+    net.load_weights(weights)
+    with pytest.raises(ContractError, match=r"enc0\.block1\.conv\.weight.*precision='fp32'"):
+        net(torch.from_numpy(x).cuda())
+    volume = np.ascontiguousarray(x[0].transpose(3, 0, 1, 2))
+    with pytest.raises(ContractError, match=r"enc0\.block1\.conv\.weight"):
+        sw.predict_device_logits(net, volume, patch_size=(16, 16, 16), num_classes=2)
+    net.close()
+    ref = OracleNetwork(spec, weights)(x)
+    fp32 = build_network(spec, precision="fp32")
+    fp32.load_weights(weights)
+    got = fp32(torch.from_numpy(x).cuda()).cpu().numpy()
+    fp32.close()
+    msg = report("split range, fp32 precision", got, ref)
+    print(msg, flush=True)
+    assert np.isfinite(got).all() and rel_l2(got, ref) <= 1e-5, msg
+    assert np.abs(got - ref).max() <= 1e-3 * max(1.0, np.abs(ref).max()), msg

@@ -47,3 +47,13 @@ def test_model_entry_points(installed):
     assert got["models"] == {name: name for name in ("nnunet-liver", "nnunet-brats2021",
                                                      "nnunet-autopet", "nnunet-pancreas")}
     assert got["package"].startswith(str(target))
+
+
+def test_named_models_state_their_device_peak():
+    """Every named model carries the registry's peak_memory_gb (the reference's MODEL key,
+    src/nnunet_mlx/named_models/liver.py:18), here the measured MI355X device peak."""
+    from nnunet_mlx.named_models import autopet, brats, liver, pancreas
+
+    for module in (liver, brats, autopet, pancreas):
+        peak = module.MODEL["peak_memory_gb"]
+        assert isinstance(peak, float) and 0 < peak < 288, (module.__name__, peak)
