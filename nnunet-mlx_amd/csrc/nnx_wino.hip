@@ -76,6 +76,8 @@ struct WinoArgs {
   int cout, ntn;
   int nbz, nby, nbx;
   int nwg;
+  int nbox;   // batch * nbz * nby * nbx (boxes of one column block)
+  int nvirt;  // nbox * ntn: (column block, box) pairs, column block slowest
   float out_scale;
   float4* stats;
   const float4* nrm0;
@@ -144,6 +146,97 @@ __device__ __forceinline__ f4 wino_norm(f4 v, const float4 (&p)[4], float s) {
     r[q] = fmaxf(s * t, t);
   }
   return r;
+}
+
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// The end of a box's epilogue, shared by both kernels.  yo[k][oz] holds, for column
+// c = tid % 32 and tile (tid / 32) + 16 k of the box, the four (oy, ox) outputs of z output
+// oz.  The values go to the output tile in LDS (row per box voxel, stride kTileStride) and
+// leave as 16-byte channel runs; the box's InstanceNorm partials per column (mean over the
+// valid voxels, then the centred sum of squares) are reduced from the registers: a thread's
+// 16 voxels, the two lanes of a wave holding the column, then the eight waves through the
+// two 256-float arrays after the tile.  Barriers wait for LDS only.
+__device__ __forceinline__ void wino_epilogue_tail(const WinoArgs& a, const f4 (&yo)[2][2],
+                                                   float* otile, int tid, int lane, int wave,
+                                                   int b, int nt, int bzi, int byi, int bxi) {
+  const int oz0 = bzi * 4, oy0 = byi * 8, ox0 = bxi * 8;
+  const int c = tid & 31;
+  auto voxel = [&](int k, int oz, int e) {
+    const int tile = (tid >> 5) + 16 * k;
+    const int tz = tile >> 4, ty = (tile >> 2) & 3, tx = tile & 3;
+    return ((2 * tz + oz) * 8 + 2 * ty + (e >> 1)) * 8 + 2 * tx + (e & 1);
+  };
+#pragma unroll
+  for (int k = 0; k < 2; ++k)
+#pragma unroll
+    for (int oz = 0; oz < 2; ++oz)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) otile[voxel(k, oz, e) * kTileStride + c] = yo[k][oz][e];
+  // a box wholly inside the volume (uniform over the workgroup) skips the voxel checks
+  const bool full = oz0 + 4 <= a.D && oy0 + 8 <= a.H && ox0 + 8 <= a.W;
+  auto valid = [&](int v) {
+    return oz0 + (v >> 6) < a.D && oy0 + ((v >> 3) & 7) < a.H && ox0 + (v & 7) < a.W;
+  };
+  float* red = otile + 256 * kTileStride;  // [wave][column] sums, then centred squares
+  const int nz = min(4, a.D - oz0), ny = min(8, a.H - oy0), nx = min(8, a.W - ox0);
+  const float cnt = (float)(nz * ny * nx);
+  if (a.stats) {
+    float sm = 0.f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int oz = 0; oz < 2; ++oz)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (full || valid(voxel(k, oz, e))) sm += yo[k][oz][e];
+    sm += __shfl_xor(sm, 32);
+    if (lane < 32) red[wave * 32 + c] = sm;
+  }
+  lds_barrier();  // the tile and the sums
+  if (a.stats) {
+    float tot = 0.f;
+#pragma unroll
+    for (int w = 0; w < kWThreads / 64; ++w) tot += red[w * 32 + c];
+    const float mean = tot / cnt;
+    float m2 = 0.f;
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+#pragma unroll
+      for (int oz = 0; oz < 2; ++oz)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          if (full || valid(voxel(k, oz, e))) {
+            const float d = yo[k][oz][e] - mean;
+            m2 = fmaf(d, d, m2);
+          }
+    m2 += __shfl_xor(m2, 32);
+    if (lane < 32) red[256 + wave * 32 + c] = m2;
+    lds_barrier();
+    if (tid < 32) {
+      float tm = 0.f;
+#pragma unroll
+      for (int w = 0; w < kWThreads / 64; ++w) tm += red[256 + w * 32 + c];
+      const int tiles = a.nbz * a.nby * a.nbx;
+      const int tile_s = (bzi * a.nby + byi) * a.nbx + bxi;
+      a.stats[((int64_t)b * tiles + tile_s) * a.cout + nt * 32 + c] = make_float4(mean, tm, cnt, 0.f);
+    }
+  }
+  // stores: 256 voxels x 8 runs of 4 channels
+  const int64_t bvox = (int64_t)b * a.D * a.H * a.W;
+#pragma unroll
+  for (int k = 0; k < 256 * 8 / kWThreads; ++k) {
+    const int idx = tid + k * kWThreads;
+    const int v = idx >> 3, qd = idx & 7;
+    if (full || valid(v)) {
+      const int z = oz0 + (v >> 6), yy = oy0 + ((v >> 3) & 7), xx = ox0 + (v & 7);
+      const float* src = otile + v * kTileStride + 4 * qd;
+      *reinterpret_cast<f4*>(a.y + (bvox + ((int64_t)z * a.H + yy) * a.W + xx) * a.cout +
+                             nt * 32 + 4 * qd) = f4{src[0], src[1], src[2], src[3]};
+    }
+  }
 }
 
 __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
@@ -431,84 +524,336 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
       yo[k][1] = yo[k][1] + bias_c;
     }
   }
-  __syncthreads();
-  float* otile = reinterpret_cast<float*>(s_raw);  // [box voxel (z, y, x)][column], stride 36
+  __syncthreads();  // every thread's partial reads are done: the tile may overwrite them
+  wino_epilogue_tail(a, yo, reinterpret_cast<float*>(s_raw), tid, lane, wave, b, nt, bzi, byi,
+                     bxi);
+}
+
+// ---- persistent variant ------------------------------------------------------------
+// One workgroup a CU loops over boxes.  The eight XCDs take contiguous ranges of the
+// (column block, box) pairs, column block slowest, and the G workgroups of an XCD interleave
+// over its range, so an XCD's L2 holds one column block's packed weights and neighbouring
+// boxes' halos.  The box arithmetic is the kernel above's, in the same order (the results
+// are bit-identical); what changes is the overlap between boxes: the last chunk of a box
+// issues the next box's first halo DMA and its B-operand refills load the next box's first
+// four steps, so the next box starts with its halo and weights landed instead of waiting for
+// them (~8k cycles a box).  The epilogue therefore keeps out of the raw halo buffers (its
+// partials, two rounds of 16 tiles, and its output tile live in the z-planes and the
+// parameter table, whose next box's values are loaded after it), its barriers wait for LDS
+// only, and the bias is read at box start.
+struct WinoBox {
+  int nt, b, bzi, byi, bxi;
+};
+
+__device__ __forceinline__ WinoBox wino_box(const WinoArgs& a, int v) {
+  WinoBox r;
+  r.nt = v / a.nbox;
+  int box = v - r.nt * a.nbox;
+  r.bxi = box % a.nbx;
+  box /= a.nbx;
+  r.byi = box % a.nby;
+  box /= a.nby;
+  r.bzi = box % a.nbz;
+  r.b = box / a.nbz;
+  return r;
+}
+
+
+__global__ __launch_bounds__(kWThreads, 1) void wino_x3p_kernel(WinoArgs a) {
+  __shared__ __align__(16) f4 s_raw[2 * kRawSlots];  // two raw halo buffers
+  __shared__ __align__(16) f4 s_z[kZSlots];          // z-planes; epilogue partials and tile
+  __shared__ __align__(16) f4 s_prm[kMaxChannels];   // parameters; epilogue partials
+  // the bias of the current box's column block (read in the epilogue from LDS: a global
+  // read there would wait for the next box's halo DMA)
+  __shared__ float s_bias[32];
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  // this workgroup's (column block, box) pairs: XCD blockIdx % 8 takes a contiguous range,
+  // its G workgroups interleave over it (the grid is a multiple of 8)
+  const int xcd = blockIdx.x & 7, G = gridDim.x >> 3;
+  const int vq = a.nvirt >> 3, vr = a.nvirt & 7;
+  const int vbeg = xcd < vr ? xcd * (vq + 1) : vr * (vq + 1) + (xcd - vr) * vq;
+  const int vend = vbeg + vq + (xcd < vr ? 1 : 0);
+  int v = vbeg + (int)(blockIdx.x >> 3);
+  if (v >= vend) return;  // uniform over the workgroup, before any barrier
+  const int xz = wave >> 1, p = wave & 1;
+  const float sg = p ? -1.f : 1.f;
+  __builtin_assume(a.chunks > 0);
+  constexpr int kPairs = 32 * 32 / kWThreads;
+
+  // halo line offsets of a box inside its batch item (-1 outside the volume or the halo)
+  auto box_vofs = [&](int tid, const WinoBox& bx, int (&vofs)[kRawRounds])
+      __attribute__((always_inline)) {
+    const int iz0 = bx.bzi * 4 - 1, iy0 = bx.byi * 8 - 1, ix0 = bx.bxi * 8 - 1;
 #pragma unroll
-  for (int k = 0; k < kPairs; ++k) {
-    const int idx = tid + k * kWThreads;
-    const int tile = idx >> 5, c = idx & 31;
-    const int tz = tile >> 4, ty = (tile >> 2) & 3, tx = tile & 3;
-#pragma unroll
-    for (int oz = 0; oz < 2; ++oz)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int oy = e >> 1, ox = e & 1;
-        const int v = ((2 * tz + oz) * 8 + 2 * ty + oy) * 8 + 2 * tx + ox;
-        otile[v * kTileStride + c] = yo[k][oz][e];
+    for (int r = 0; r < kRawRounds; ++r) {
+      const int line = r * kWThreads + tid;
+      int o = -1;
+      if (line < kRawLines) {
+        const int hv = line >> 2;
+        const int hz = hv / 100, rem = hv - hz * 100;
+        const int hy = rem / 10, hx = rem - hy * 10;
+        const int z = iz0 + hz, yy = iy0 + hy, xx = ix0 + hx;
+        if ((unsigned)z < (unsigned)a.D && (unsigned)yy < (unsigned)a.H &&
+            (unsigned)xx < (unsigned)a.W)
+          o = (z * a.H + yy) * a.W + xx;
       }
-  }
-  __syncthreads();
-  // a box wholly inside the volume (uniform over the workgroup) skips the voxel checks
-  const bool full = oz0 + 4 <= a.D && oy0 + 8 <= a.H && ox0 + 8 <= a.W;
-  auto valid = [&](int v) {
-    return oz0 + (v >> 6) < a.D && oy0 + ((v >> 3) & 7) < a.H && ox0 + (v & 7) < a.W;
-  };
-  // InstanceNorm partials of the box per column: mean over the valid voxels, then the
-  // centred sum of squares (thread = column c, part p of 8)
-  auto box_stats = [&](auto all) __attribute__((always_inline)) {
-    constexpr bool kAll = decltype(all)::value;
-    constexpr int kParts = kWThreads / 32;
-    float* red = otile + 256 * kTileStride;  // kWThreads floats
-    const int c = tid & 31, pidx = tid >> 5;
-    const int nz = min(4, a.D - oz0), ny = min(8, a.H - oy0), nx = min(8, a.W - ox0);
-    const float cnt = (float)(nz * ny * nx);
-    float s = 0.f;
-#pragma unroll 8
-    for (int v = pidx; v < 256; v += kParts)
-      if (kAll || valid(v)) s += otile[v * kTileStride + c];
-    red[tid] = s;
-    __syncthreads();
-    float mean = 0.f;
-#pragma unroll
-    for (int k = 0; k < kParts; ++k) mean += red[k * 32 + c];
-    mean = mean / cnt;
-    __syncthreads();
-    float m2 = 0.f;
-#pragma unroll 8
-    for (int v = pidx; v < 256; v += kParts)
-      if (kAll || valid(v)) {
-        const float d = otile[v * kTileStride + c] - mean;
-        m2 = fmaf(d, d, m2);
-      }
-    red[tid] = m2;
-    __syncthreads();
-    if (pidx == 0) {
-      float tot = 0.f;
-#pragma unroll
-      for (int k = 0; k < kParts; ++k) tot += red[k * 32 + c];
-      const int tiles = a.nbz * a.nby * a.nbx;
-      const int tile_s = (bzi * a.nby + byi) * a.nbx + bxi;
-      a.stats[((int64_t)b * tiles + tile_s) * a.cout + nt * 32 + c] = make_float4(mean, tot, cnt, 0.f);
+      vofs[r] = o;
     }
   };
-  if (a.stats) {
-    if (full)
-      box_stats(std::true_type{});
-    else
-      box_stats(std::false_type{});
-  }
-  // stores: 256 voxels x 8 runs of 4 channels
+  // chunk `chunk` of item b's halo lines into buffer `buf` (live = false: the zero line)
+  auto fetch = [&](int tid, int b, const int (&vofs)[kRawRounds], int chunk, int buf, bool live)
+      __attribute__((always_inline)) {
+    const bool first = chunk < a.chunks0;
+    const float* src = first ? a.x0 : a.x1;
+    const int C = first ? a.c0 : a.c1;
+    const int64_t bv = (int64_t)b * a.D * a.H * a.W;
+    const float* base = src + bv * C + (first ? chunk : chunk - a.chunks0) * kWChunk + (tid & 3) * 4;
+    f4* dst = s_raw + buf * kRawSlots + wave * 64;
 #pragma unroll
-  for (int k = 0; k < 256 * 8 / kWThreads; ++k) {
-    const int idx = tid + k * kWThreads;
-    const int v = idx >> 3, qd = idx & 7;
-    if (full || valid(v)) {
-      const int z = oz0 + (v >> 6), yy = oy0 + ((v >> 3) & 7), xx = ox0 + (v & 7);
-      const float* src = otile + v * kTileStride + 4 * qd;
-      *reinterpret_cast<f4*>(a.y + (bvox + ((int64_t)z * a.H + yy) * a.W + xx) * a.cout +
-                             nt * 32 + 4 * qd) = f4{src[0], src[1], src[2], src[3]};
+    for (int r = 0; r < kRawRounds; ++r) {
+      const float* in = base + (int64_t)(vofs[r] < 0 ? 0 : vofs[r]) * C;
+      const float* g = live && vofs[r] >= 0 ? in : g_wino_zero;
+      __builtin_amdgcn_global_load_lds(
+          g, (__attribute__((address_space(3))) void*)(dst + r * kWThreads), 16, 0, 0);
     }
+  };
+  auto load_prm = [&](int tid, int b) __attribute__((always_inline)) {
+    for (int c = tid; c < a.c0 + a.c1; c += kWThreads) {
+      const float4* pp = c < a.c0 ? a.nrm0 : a.nrm1;
+      const int C = c < a.c0 ? a.c0 : a.c1;
+      const int cc = c < a.c0 ? c : c - a.c0;
+      float4 pv = make_float4(0.f, 1.f, 0.f, 0.f);
+      if (pp) pv = pp[(int64_t)b * C + cc];
+      s_prm[c] = f4{pv.x, pv.y, pv.z, 0.f};
+    }
+  };
+  // packed U words of column block ntb, chunk, step (local position) for this lane
+  auto uaddr = [&](int lane, int ntb, int chunk, int step) {
+    return a.u + (((int64_t)ntb * a.chunks + chunk) * 64 + xz * 16 + p * kSteps + step) * 128 + lane;
+  };
+
+  // loop-carried state: the halo offsets of the box whose first chunk is in flight, the
+  // B-operand ring, the bias of the current column block
+  int vofs[kRawRounds];
+  uint4 uh[kRing], ul[kRing];
+  {
+    const int tid = threadIdx.x;
+    const WinoBox first = wino_box(a, v);
+    box_vofs(tid, first, vofs);
+    load_prm(tid, first.b);
+    fetch(tid, first.b, vofs, 0, 0, true);
+#pragma unroll
+    for (int s0 = 0; s0 < kRing; ++s0) {
+      const uint4* up = uaddr(tid & 63, first.nt, 0, s0);
+      uh[s0] = up[0];
+      ul[s0] = up[64];
+    }
+    if (tid < 32) s_bias[tid] = a.bias ? a.bias[first.nt * 32 + tid] : 0.f;
   }
+
+  for (;;) {
+    // per-lane values rebuilt from an opaque copy each box, so that nothing derived from
+    // them is hoisted out of the box loop and held through it
+    int tid = threadIdx.x;
+    asm volatile("" : "+v"(tid));
+    const int lane = tid & 63;
+    const WinoBox cur = wino_box(a, v);
+    const int vnext = v + G;
+    const bool more = vnext < vend;
+    const int vn = more ? vnext : v;  // the next box (this one again after the last)
+    const int nnt = vn / a.nbox;
+    const int iz0 = cur.bzi * 4 - 1, iy0 = cur.byi * 8 - 1, ix0 = cur.bxi * 8 - 1;
+    const bool interior = iz0 >= 0 && iz0 + 6 <= a.D && iy0 >= 0 && iy0 + 10 <= a.H &&
+                          ix0 >= 0 && ix0 + 10 <= a.W;
+    const int t = lane & 31, tzl = t >> 4, tyl = (t >> 2) & 3, txl = t & 3, g8 = lane >> 5;
+    const unsigned zb_lds = (unsigned)(uintptr_t)(
+        (__attribute__((address_space(3))) f4*)s_z + ((xz * 2 + tzl) * kZPlane + (2 * tyl) * kZRow +
+                                                      (2 * txl) * 4 + 2 * g8));
+    auto transform_column = [&](auto inner, int chunk, int buf, int col)
+        __attribute__((always_inline)) {
+      const int hy = col / 40, rem = col - hy * 40;
+      const int hx = rem >> 2, cq = rem & 3;
+      const bool first = chunk < a.chunks0;
+      const float sl = (first ? a.act0 : a.act1) != 0 ? a.slope : 1.f;
+      float4 pm[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const f4 pq = s_prm[chunk * kWChunk + cq * 4 + q];
+        pm[q] = make_float4(pq[0], pq[1], pq[2], 0.f);
+      }
+      const f4* raw = s_raw + buf * kRawSlots + (hy * 10 + hx) * 4 + cq;
+      f4 d[6];
+#pragma unroll
+      for (int hz = 0; hz < 6; ++hz) d[hz] = raw[hz * 400];
+      if constexpr (decltype(inner)::value) {
+#pragma unroll
+        for (int hz = 0; hz < 6; ++hz) d[hz] = wino_norm(d[hz], pm, sl);
+      } else {
+        const bool inyx =
+            (unsigned)(iy0 + hy) < (unsigned)a.H && (unsigned)(ix0 + hx) < (unsigned)a.W;
+#pragma unroll
+        for (int hz = 0; hz < 6; ++hz) {
+          const f4 tq = wino_norm(d[hz], pm, sl);
+          const bool inside = inyx && (unsigned)(iz0 + hz) < (unsigned)a.D;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) d[hz][e] = inside ? tq[e] : 0.f;
+        }
+      }
+      f4* dst = s_z + hy * kZRow + hx * 4 + cq;
+#pragma unroll
+      for (int tz = 0; tz < 2; ++tz) {
+        const f4 d0 = d[2 * tz], d1 = d[2 * tz + 1], d2 = d[2 * tz + 2], d3 = d[2 * tz + 3];
+        dst[(0 * 2 + tz) * kZPlane] = d0 - d2;
+        dst[(1 * 2 + tz) * kZPlane] = d1 + d2;
+        dst[(2 * 2 + tz) * kZPlane] = d2 - d1;
+        dst[(3 * 2 + tz) * kZPlane] = d1 - d3;
+      }
+    };
+
+    f16v acc[2][4];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj)
+#pragma unroll
+      for (int x = 0; x < 4; ++x)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[jj][x][r] = 0.f;
+
+    // the three products of steps s0, s0 + 1, then their ring refills kRing steps ahead:
+    // past the chunk's last step the next chunk's, past the box's last chunk the next box's
+    // first chunk's (column block nnt)
+    auto products = [&](int s0, const float (&q)[4][8], int chunk) __attribute__((always_inline)) {
+      h8 ah[2], al[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int xx = (s0 + k) & 3;
+        float vv[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if (xx == 0) vv[e] = q[0][e] - q[2][e];
+          else if (xx == 1) vv[e] = q[1][e] + q[2][e];
+          else if (xx == 2) vv[e] = q[2][e] - q[1][e];
+          else vv[e] = q[1][e] - q[3][e];
+        }
+        split8(vv, ah[k], al[k]);
+      }
+      const int xy = s0 >> 2, x0 = s0 & 3;
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        acc[xy][x0 + k] = mfma32(ah[k], *reinterpret_cast<const h8*>(&uh[(s0 + k) % kRing]),
+                                 acc[xy][x0 + k]);
+#pragma unroll
+      for (int k = 0; k < 2; ++k)
+        acc[xy][x0 + k] = mfma32(ah[k], *reinterpret_cast<const h8*>(&ul[(s0 + k) % kRing]),
+                                 acc[xy][x0 + k]);
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        const int st = s0 + k, slot_r = st % kRing;
+        acc[xy][x0 + k] = mfma32(al[k], *reinterpret_cast<const h8*>(&uh[slot_r]), acc[xy][x0 + k]);
+        const int ns = st + kRing;
+        const bool wrap = ns >= kSteps && chunk + 1 >= a.chunks;
+        const uint4* up = uaddr(lane, wrap ? nnt : cur.nt,
+                                ns < kSteps ? chunk : (wrap ? 0 : chunk + 1), ns & (kSteps - 1));
+        uh[slot_r] = up[0];
+        ul[slot_r] = up[64];
+      }
+    };
+
+    for (int chunk = 0; chunk < a.chunks; ++chunk) {
+      const int buf = chunk & 1;
+      __builtin_amdgcn_s_waitcnt(0);  // this thread's halo lines and B operands have landed
+      __syncthreads();                 // every thread's; the z-planes are free
+      if (tid < 400) {
+        if (interior)
+          transform_column(std::true_type{}, chunk, buf, tid);
+        else
+          transform_column(std::false_type{}, chunk, buf, tid);
+      }
+      // the next chunk's halo into the other buffer; after the box's last chunk the next
+      // box's first chunk (the zero line after the last box)
+      if (chunk + 1 < a.chunks) {
+        fetch(tid, cur.b, vofs, chunk + 1, buf ^ 1, true);
+      } else {
+        // (from an opaque copy of the thread index: computed here, not hoisted to the box
+        // start and held through the chunk loop)
+        int tid_n = tid;
+        asm volatile("" : "+v"(tid_n));
+        const WinoBox nb = wino_box(a, vn);
+        box_vofs(tid_n, nb, vofs);
+        fetch(tid_n, nb.b, vofs, 0, buf ^ 1, more);
+      }
+      lds_barrier();
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        f4 va[8], vb[8];
+        zrow_pair(zb_lds + (j == 0 ? 2 * p : 1) * kZRow * 16,
+                  zb_lds + (j == 0 ? 2 - p : 2 + p) * kZRow * 16, va, vb);
+        float q[4][8];
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+          for (int h = 0; h < 2; ++h)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              q[c][4 * h + e] = j == 0 ? va[2 * c + h][e] - vb[2 * c + h][e]
+                                       : fmaf(sg, vb[2 * c + h][e], va[2 * c + h][e]);
+        products(4 * j, q, chunk);
+        products(4 * j + 2, q, chunk);
+      }
+    }
+
+    // ---- epilogue in the z-planes and the parameter table only
+    lds_barrier();  // every wave is past its last z-plane read and parameter read
+    auto part = [&](int w, int tile, int c) -> f4& {
+      const int i = (w * 16 + tile) * 32 + c;  // 16 tiles a round
+      return i < kZSlots ? s_z[i] : s_prm[i - kZSlots];
+    };
+    const int col = lane & 31;
+    f4 yo[kPairs][2];
+#pragma unroll
+    for (int h = 0; h < kPairs; ++h) {
+#pragma unroll
+      for (int r = 8 * h; r < 8 * h + 8; ++r) {
+        float xo[2][2];
+#pragma unroll
+        for (int jj = 0; jj < 2; ++jj) {
+          const float m0 = acc[jj][0][r], m1 = acc[jj][1][r], m2 = acc[jj][2][r], m3 = acc[jj][3][r];
+          xo[jj][0] = (m0 + m1) + m2;
+          xo[jj][1] = (m1 - m2) - m3;
+        }
+        const f4 pv = p == 0 ? f4{xo[0][0] + xo[1][0], xo[0][1] + xo[1][1], xo[1][0], xo[1][1]}
+                             : f4{xo[0][0], xo[0][1], -(xo[0][0] + xo[1][0]), -(xo[0][1] + xo[1][1])};
+        part(wave, 8 * (r >> 2) + 4 * g8 + (r & 3) - 16 * h, col) = pv;
+      }
+      lds_barrier();
+      {
+        const int tile = tid >> 5, c = tid & 31;
+        f4 pz[4];
+#pragma unroll
+        for (int z = 0; z < 4; ++z) pz[z] = part(2 * z, tile, c) + part(2 * z + 1, tile, c);
+        const f4 y0 = (pz[0] + pz[1]) + pz[2];
+        const f4 y1 = (pz[1] - pz[2]) - pz[3];
+        yo[h][0] = y0 * a.out_scale;
+        yo[h][1] = y1 * a.out_scale;
+        if (a.bias) {
+          const float bc = s_bias[c];
+          yo[h][0] = yo[h][0] + bc;
+          yo[h][1] = yo[h][1] + bc;
+        }
+      }
+      lds_barrier();
+    }
+    wino_epilogue_tail(a, yo, reinterpret_cast<float*>(s_z), tid, lane, wave, cur.b, cur.nt,
+                       cur.bzi, cur.byi, cur.bxi);
+    if (!more) break;
+    // the next box: its bias, and its item's parameters once every thread has read the tile
+    // and the partials out of the parameter table
+    if (nnt != cur.nt && tid < 32) s_bias[tid] = a.bias ? a.bias[nnt * 32 + tid] : 0.f;
+    v = vnext;
+    lds_barrier();
+    load_prm(tid, wino_box(a, v).b);
+  }
+  // the last (zero-line) DMA lands before the workgroup's LDS is released
+  __builtin_amdgcn_s_waitcnt(0);
 }
 
 // U[cout][cin][xi] = sum_{a,b,e} G[xz][a] G[xy][b] G[xx][e] w[cout][a][b][e][cin] in float64,
@@ -567,6 +912,29 @@ __global__ void pack_wino_weight_kernel(const float* __restrict__ w, uint4* __re
 }
 
 }  // namespace
+
+// Compute units of the current device, rounded down to a multiple of the 8 XCDs (the
+// persistent kernel's grid: one workgroup a CU).
+static int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  hip_check(hipGetDevice(&dev), "hipGetDevice");
+  if (dev < 0 || dev >= 64) dev = 0;
+  if (cached[dev] == 0) {
+    int n = 0;
+    hip_check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev),
+              "hipDeviceGetAttribute");
+    cached[dev] = n >= 8 ? n / 8 * 8 : 8;
+  }
+  return cached[dev];
+}
+
+// NNX_WINO_PERSISTENT=0 keeps every Winograd layer on the one-box-a-workgroup kernel (read
+// at each launch, for comparisons).
+static bool wino_persistent_enabled() {
+  const char* e = std::getenv("NNX_WINO_PERSISTENT");
+  return !(e && e[0] == '0');
+}
 
 // Layers outside this set take the direct split kernel (the route is chosen with it).
 bool conv_wino_supported(const ConvGeom& g, int c1, int c2, int cout) {
@@ -653,7 +1021,14 @@ void conv3d_wino(const float* x1, int c1, const float* x2, int c2, const void* p
   const double bytes = 4.0 * ((double)g.batch * g.in[0] * g.in[1] * g.in[2] * (c1 + c2) +
                               out_vox * cout);
   ProfScope prof("conv3d_wino", flops, bytes, st);
-  hipLaunchKernelGGL(wino_x3_kernel, dim3(a.nwg), dim3(kWThreads), 0, st, a);
+  const int cus = device_cus();
+  if (a.chunks % 2 == 0 && wino_persistent_enabled() && a.nwg >= 4 * cus) {
+    a.nbox = a.nwg / a.ntn;
+    a.nvirt = a.nwg;
+    hipLaunchKernelGGL(wino_x3p_kernel, dim3(cus), dim3(kWThreads), 0, st, a);
+  } else {
+    hipLaunchKernelGGL(wino_x3_kernel, dim3(a.nwg), dim3(kWThreads), 0, st, a);
+  }
   launch_check("conv3d_winograd");
 }
 

@@ -173,6 +173,66 @@ def test_conv3d_winograd_matches_float64(lib, case):
     assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
 
 
+PERSISTENT_CASES = [
+    # batch, in_size, c1, c2, cout: at least 4 workgroups a CU (the persistent kernel's range)
+    (2, (32, 64, 64), 32, 0, 32),
+    (8, (20, 40, 36), 32, 32, 64),   # two inputs, two column blocks, ragged x boxes
+    (4, (17, 33, 31), 64, 0, 96),    # ragged boxes on every axis, three column blocks
+]
+
+
+def _winograd_run(lib, case, persistent: bool, seed: int = 3):
+    import os
+
+    batch, size, c1, c2, cout = case
+    rng = np.random.default_rng(seed)
+    x1 = (rng.standard_normal((batch, *size, c1)) * 3.0).astype(np.float32)
+    x2 = rng.standard_normal((batch, *size, c2)).astype(np.float32) if c2 else None
+    w = (rng.standard_normal((cout, 3, 3, 3, c1 + c2)) / np.sqrt((c1 + c2) * 27)).astype(np.float32)
+    bias = rng.standard_normal(cout).astype(np.float32)
+    scale = lib.nnx_winograd_weight_scale(float(np.abs(w).max()))
+    packed = torch.empty(lib.nnx_conv3d_winograd_packed_bytes(cout, c1, c2), dtype=torch.uint8,
+                         device="cuda")
+    _native.check(lib.nnx_conv3d_winograd_pack_weight(dev(w).data_ptr(), cout, c1, c2, scale,
+                                                      packed.data_ptr(), stream()))
+    dx1, db = dev(x1), dev(bias)
+    dx2 = dev(x2) if c2 else None
+    y = torch.full((batch, *size, cout), float("nan"), dtype=torch.float32, device="cuda")
+    old = os.environ.get("NNX_WINO_PERSISTENT")
+    os.environ["NNX_WINO_PERSISTENT"] = "1" if persistent else "0"
+    try:
+        _native.check(lib.nnx_conv3d_winograd(
+            dx1.data_ptr(), c1, dx2.data_ptr() if c2 else None, c2, packed.data_ptr(), scale,
+            db.data_ptr(), y.data_ptr(), batch, _native.ints(size), cout, stream()))
+        torch.cuda.synchronize()
+    finally:
+        if old is None:
+            del os.environ["NNX_WINO_PERSISTENT"]
+        else:
+            os.environ["NNX_WINO_PERSISTENT"] = old
+    return host(y), x1, x2, w, bias
+
+
+@pytest.mark.parametrize("case", PERSISTENT_CASES, ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}")
+def test_conv3d_winograd_persistent_kernel_is_bit_identical(lib, case):
+    """The persistent Winograd kernel (a workgroup a CU looping over boxes, the next box's
+    halo and weights requested during the current box's last chunk) computes every box
+    with the one-box kernel's arithmetic: its output equals that kernel's bit for bit, and
+    holds the float32 bar against float64 on the first case."""
+    print(f"winograd persistent case {case}", flush=True)
+    got, x1, x2, w, bias = _winograd_run(lib, case, persistent=True)
+    ref_kernel, *_ = _winograd_run(lib, case, persistent=False)
+    assert np.isfinite(got).all()
+    assert np.array_equal(got.view(np.uint32), ref_kernel.view(np.uint32)), \
+        f"{int((got != ref_kernel).sum())} values differ"
+    if case == PERSISTENT_CASES[0]:
+        ref = _conv_ref64(x1, w, (1, 1, 1)) + bias.astype(np.float64)
+        msg = report("winograd persistent", got, ref)
+        print(msg, flush=True)
+        assert rel_l2(got, ref) <= 1e-5, msg
+        assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
+
+
 def test_conv3d_winograd_rejects_unsupported_layers(lib):
     """Channel counts off the 16 / 32 grid, a second input off the grid and a bad weight
     scale are refused before any launch, with valid buffers so that the layer check (not a
