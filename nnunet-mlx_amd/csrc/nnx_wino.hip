@@ -21,7 +21,8 @@
 //   1. the raw 6 x 10 x 10 input halo was fetched by global_load_lds_dwordx4 into one of two
 //      LDS buffers during the previous chunk;
 //   2. 400 threads apply the pending InstanceNorm (+ LeakyReLU) of the input to in-volume
-//      voxels and write the z-transform (4 xz x 2 tile rows of z) as 8 padded planes, laid
+//      voxels (inputs without one, such as the transposed convolution's output in a decoder
+//      convolution, skip it) and write the z-transform (4 xz x 2 tile rows of z) as 8 padded planes, laid
 //      out so that the 32 tiles of a half-wave read 32 different 16-byte bank groups; then
 //      the next chunk's halo DMA is issued;
 //   3. per y-row of its positions, each wave reads two z-transformed rows of its tile patch,
@@ -331,7 +332,9 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
     f4 d[6];
 #pragma unroll
     for (int hz = 0; hz < 6; ++hz) d[hz] = raw[hz * 400];
-    if constexpr (decltype(inner)::value) {
+    if constexpr (decltype(inner)::value == 2) {
+      // no pending norm: the raw values (the padding lines read the zero line)
+    } else if constexpr (decltype(inner)::value == 1) {
 #pragma unroll
       for (int hz = 0; hz < 6; ++hz) d[hz] = wino_norm(d[hz], pm, s);
     } else {
@@ -358,10 +361,12 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
   };
   auto transform = [&](int chunk, int buf) __attribute__((always_inline)) {
     if (tid < 400) {
-      if (interior)
-        transform_column(std::true_type{}, chunk, buf, tid);
+      if ((chunk < a.chunks0 ? a.nrm0 : a.nrm1) == nullptr)
+        transform_column(std::integral_constant<int, 2>{}, chunk, buf, tid);
+      else if (interior)
+        transform_column(std::integral_constant<int, 1>{}, chunk, buf, tid);
       else
-        transform_column(std::false_type{}, chunk, buf, tid);
+        transform_column(std::integral_constant<int, 0>{}, chunk, buf, tid);
     }
   };
 
@@ -685,7 +690,9 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3p_kernel(WinoArgs a) {
       f4 d[6];
 #pragma unroll
       for (int hz = 0; hz < 6; ++hz) d[hz] = raw[hz * 400];
-      if constexpr (decltype(inner)::value) {
+      if constexpr (decltype(inner)::value == 2) {
+        // no pending norm: the raw values (the padding lines read the zero line)
+      } else if constexpr (decltype(inner)::value == 1) {
 #pragma unroll
         for (int hz = 0; hz < 6; ++hz) d[hz] = wino_norm(d[hz], pm, sl);
       } else {
@@ -763,10 +770,12 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3p_kernel(WinoArgs a) {
       __builtin_amdgcn_s_waitcnt(0);  // this thread's halo lines and B operands have landed
       __syncthreads();                 // every thread's; the z-planes are free
       if (tid < 400) {
-        if (interior)
-          transform_column(std::true_type{}, chunk, buf, tid);
+        if ((chunk < a.chunks0 ? a.nrm0 : a.nrm1) == nullptr)
+          transform_column(std::integral_constant<int, 2>{}, chunk, buf, tid);
+        else if (interior)
+          transform_column(std::integral_constant<int, 1>{}, chunk, buf, tid);
         else
-          transform_column(std::false_type{}, chunk, buf, tid);
+          transform_column(std::integral_constant<int, 0>{}, chunk, buf, tid);
       }
       // the next chunk's halo into the other buffer; after the box's last chunk the next
       // box's first chunk (the zero line after the last box)
