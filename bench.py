@@ -363,11 +363,12 @@ def _short_kernel(name: str) -> str:
 
 def kernel_class_of(short: str) -> str | None:
     """Map a rocprof kernel name to the profiling class bench.py reports
-    (igemm_kernel<MB, NB, WM, WN, ...> -> conv3d_igemm_m{16*MB*WM}n{16*NB*WN}, and the
-    split-fp16 kernels igemm_x3s_kernel / igemm_x3_kernel -> conv3d_x3s_* / conv3d_x3_*)."""
+    (igemm_kernel<MB, NB, WM, WN, ...> -> conv3d_igemm_m{16*MB*WM}n{16*NB*WN}, the
+    split-fp16 kernels igemm_x3s_kernel / igemm_x3_kernel -> conv3d_x3s_* / conv3d_x3_*, and
+    both Winograd kernels, one box a workgroup and persistent, -> conv3d_wino)."""
     import re
 
-    if short.startswith("wino_x3_kernel"):
+    if short.startswith(("wino_x3_kernel", "wino_x3p_kernel")):
         return "conv3d_wino"
     m = re.match(r"igemm(_x3s|_x3)?_kernel<(\d+), (\d+), (\d+), (\d+)([^>]*)>", short)
     if not m:
