@@ -320,11 +320,16 @@ __global__ __launch_bounds__(256) void norm_merge_final_kernel(const float4* __r
   params[(int64_t)b * C + c] = make_float4((float)m, scale, beta ? beta[c] : 0.f, 0.f);
 }
 
+// y = act(fma(x (+ bias) - mean, scale, beta) (+ residual)) over a (B, S, C) tensor, VW
+// channels a vector.  Grid-stride over an item's vectors with kUnroll vectors in flight per
+// thread (all loads issued before the arithmetic); a thread's channel index advances by
+// the grid stride modulo C, so no division per element.  y may alias x.
 template <int VW>
 __global__ __launch_bounds__(256) void norm_apply_kernel(
     const float* x, float* y, const float4* __restrict__ params, const float* __restrict__ in_bias,
     const float* residual, int64_t SC, int C, int act, float slope) {
   typedef typename Vec<VW>::type V;
+  constexpr int kUnroll = 4;
   extern __shared__ float smem[];  // C * 4: mean, scale, beta, input bias
   float* s_mean = smem;
   float* s_scale = smem + C;
@@ -344,17 +349,15 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(
   const float* rs = residual ? residual + (int64_t)b * SC : nullptr;
   const int64_t nvec = SC / VW;
   const bool has_bias = in_bias != nullptr;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nvec;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int64_t e = i * VW;
-    const int c0 = (int)(e % C);
-    V xv = *reinterpret_cast<const V*>(xs + e);
-    V rv;
-    if (rs) rv = *reinterpret_cast<const V*>(rs + e);
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  int c0 = (int)((i * VW) % C);            // channel of this thread's current vector
+  const int dc = (int)((stride * VW) % C);  // its advance per grid stride
+  auto apply = [&](V xv, V rv, int cb) {
     V out;
 #pragma unroll
     for (int q = 0; q < VW; ++q) {
-      const int c = c0 + q;
+      const int c = cb + q;
       float v = lane_of<VW>(xv, q);
       if (has_bias) v = v + s_bias[c];
       float r = fmaf(v - s_mean[c], s_scale[c], s_beta[c]);
@@ -362,33 +365,59 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(
       if (act) r = fmaxf(slope * r, r);
       if constexpr (VW == 1) out = r; else out[q] = r;
     }
-    *reinterpret_cast<V*>(ys + e) = out;
+    return out;
+  };
+  for (; i + (kUnroll - 1) * stride < nvec; i += kUnroll * stride) {
+    V xv[kUnroll], rv[kUnroll];
+    int cb[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t e = (i + u * stride) * VW;
+      xv[u] = *reinterpret_cast<const V*>(xs + e);
+      if (rs) rv[u] = *reinterpret_cast<const V*>(rs + e);
+      cb[u] = c0;
+      c0 += dc;
+      if (c0 >= C) c0 -= C;
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      *reinterpret_cast<V*>(ys + (i + u * stride) * VW) = apply(xv[u], rs ? rv[u] : xv[u], cb[u]);
+  }
+  for (; i < nvec; i += stride) {
+    const int64_t e = i * VW;
+    const V xv = *reinterpret_cast<const V*>(xs + e);
+    const V rv = rs ? *reinterpret_cast<const V*>(rs + e) : xv;
+    *reinterpret_cast<V*>(ys + e) = apply(xv, rv, c0);
+    c0 += dc;
+    if (c0 >= C) c0 -= C;
   }
 }
 
+// Average pooling with kernel = stride (kd, kh, kw) of an NDHWC tensor.  Block (x, y, z) =
+// (run of 256 (output x, channel group) pairs, output y, item * od + output z); a thread
+// sums its window of VW-channel vectors in (a, e, f) order, then multiplies by 1 / (kd kh kw).
+template <int VW>
 __global__ __launch_bounds__(256) void avgpool_kernel(const float* __restrict__ x,
-                                                      float* __restrict__ y, int64_t nout,
-                                                      int D, int H, int W, int C, int kd, int kh,
-                                                      int kw) {
+                                                      float* __restrict__ y, int D, int H, int W,
+                                                      int C, int kd, int kh, int kw) {
+  typedef typename Vec<VW>::type V;
   const int od = D / kd, oh = H / kh, ow = W / kw;
+  const int cg = C / VW;
+  const int ix = blockIdx.x * 256 + threadIdx.x;
+  if (ix >= ow * cg) return;
+  const int xx = ix / cg, c = (ix - xx * cg) * VW;
+  const int yy = blockIdx.y;
+  const int zz = blockIdx.z % od;
+  const int64_t b = blockIdx.z / od;
   const float inv = 1.0f / (float)(kd * kh * kw);
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < nout;
-       i += (int64_t)gridDim.x * blockDim.x) {
-    const int c = (int)(i % C);
-    int64_t v = i / C;
-    const int xx = (int)(v % ow);
-    v /= ow;
-    const int yy = (int)(v % oh);
-    v /= oh;
-    const int zz = (int)(v % od);
-    const int64_t b = v / od;
-    float s = 0.f;
-    for (int a = 0; a < kd; ++a)
-      for (int e = 0; e < kh; ++e)
-        for (int f = 0; f < kw; ++f)
-          s += x[((((b * D) + zz * kd + a) * H + yy * kh + e) * (int64_t)W + xx * kw + f) * C + c];
-    y[i] = s * inv;
-  }
+  V s;
+  if constexpr (VW == 1) s = 0.f; else s = V{0.f, 0.f, 0.f, 0.f};
+  for (int a = 0; a < kd; ++a)
+    for (int e = 0; e < kh; ++e)
+      for (int f = 0; f < kw; ++f)
+        s += *reinterpret_cast<const V*>(
+            x + ((((b * D) + zz * kd + a) * H + yy * kh + e) * (int64_t)W + xx * kw + f) * C + c);
+  *reinterpret_cast<V*>(y + (((b * od + zz) * oh + yy) * (int64_t)ow + xx) * C + c) = s * inv;
 }
 
 // Centred crop / zero pad of an NDHWC tensor: out[b, z, y, x, c] = in[b, z + oz, y + oy,
@@ -624,12 +653,22 @@ void avgpool3d(const float* x, float* y, int batch, const int* in_size, int chan
   require(x && y, "pooling pointers must not be null");
   for (int i = 0; i < 3; ++i)
     require(kernel[i] >= 1 && in_size[i] >= kernel[i], "invalid pooling geometry");
-  const int64_t nout = (int64_t)batch * (in_size[0] / kernel[0]) * (in_size[1] / kernel[1]) *
-                       (in_size[2] / kernel[2]) * channels;
-  const int64_t blocks = std::min<int64_t>(ceil_div(nout, 256), 65536);
+  const int od = in_size[0] / kernel[0], oh = in_size[1] / kernel[1], ow = in_size[2] / kernel[2];
+  const int64_t nout = (int64_t)batch * od * oh * ow * channels;
+  require((int64_t)batch * od <= 65535 && oh <= 65535, "pooling output too large for the grid");
+  const int vw = channels % 4 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(y) % 16 == 0
+                     ? 4
+                     : 1;
+  const dim3 grid((unsigned)ceil_div((int64_t)ow * (channels / vw), 256), (unsigned)oh,
+                  (unsigned)(batch * od));
   ProfScope prof("avgpool3d", 0.0, 4.0 * (double)nout * (1 + kernel[0] * kernel[1] * kernel[2]), st);
-  hipLaunchKernelGGL(avgpool_kernel, dim3((unsigned)blocks), dim3(256), 0, st, x, y, nout,
-                     in_size[0], in_size[1], in_size[2], channels, kernel[0], kernel[1], kernel[2]);
+  if (vw == 4)
+    hipLaunchKernelGGL(avgpool_kernel<4>, grid, dim3(256), 0, st, x, y, in_size[0], in_size[1],
+                       in_size[2], channels, kernel[0], kernel[1], kernel[2]);
+  else
+    hipLaunchKernelGGL(avgpool_kernel<1>, grid, dim3(256), 0, st, x, y, in_size[0], in_size[1],
+                       in_size[2], channels, kernel[0], kernel[1], kernel[2]);
   launch_check("avgpool3d");
 }
 

@@ -556,14 +556,21 @@ def test_conv1x1_seg_head(lib):
     assert rel_l2(host(y), ref) <= 1e-6
 
 
-def test_avgpool3d(lib):
+@pytest.mark.parametrize("channels,kernel,size", [
+    (5, (2, 2, 2), (8, 6, 4)),        # one channel a thread
+    (32, (2, 2, 2), (8, 12, 200)),    # 4-channel vectors, rows longer than a block
+    (8, (2, 1, 1), (6, 5, 7)),        # anisotropic (the last ResEnc stage's stride)
+])
+def test_avgpool3d(lib, channels, kernel, size):
     rng = np.random.default_rng(6)
-    x = rng.standard_normal((2, 8, 6, 4, 5)).astype(np.float32)
-    y = torch.empty((2, 4, 3, 2, 5), dtype=torch.float32, device="cuda")
+    x = rng.standard_normal((2, *size, channels)).astype(np.float32)
+    out = [n // k for n, k in zip(size, kernel)]
+    y = torch.full((2, *out, channels), float("nan"), dtype=torch.float32, device="cuda")
     dx = dev(x)
-    _native.check(lib.nnx_avgpool3d(dx.data_ptr(), y.data_ptr(), 2, _native.ints((8, 6, 4)), 5,
-                                    _native.ints((2, 2, 2)), stream()))
-    ref = x.reshape(2, 4, 2, 3, 2, 2, 2, 5).astype(np.float64).mean(axis=(2, 4, 6))
+    _native.check(lib.nnx_avgpool3d(dx.data_ptr(), y.data_ptr(), 2, _native.ints(size), channels,
+                                    _native.ints(kernel), stream()))
+    ref = x.reshape(2, out[0], kernel[0], out[1], kernel[1], out[2], kernel[2],
+                    channels).astype(np.float64).mean(axis=(2, 4, 6))
     assert np.abs(host(y) - ref).max() < 1e-6
 
 
