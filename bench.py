@@ -471,6 +471,75 @@ def summarize_profiles(directory: str) -> None:
         lines.append(f"| `{cls}` | {n} | {f/n:.4g} | {w/n:.4g} | {(f+w)/n:.4g} |")
     TRAFFIC_FILE.write_text("\n".join(lines) + "\n")
     print(f"wrote {out / 'kernel_stats_liver.md'} and {TRAFFIC_FILE}")
+    if (base / "sq" / "p1" / "p_counter_collection.csv").is_file():
+        summarize_sq_counters(base / "sq", out / "sq_counters_liver.md")
+
+
+SQ_PASSES = (
+    "SQ_WAVES SQ_BUSY_CYCLES SQ_WAVE_CYCLES SQ_INSTS_VALU SQ_INSTS_MFMA SQ_INSTS_LDS "
+    "SQ_VALU_MFMA_BUSY_CYCLES SQ_ACTIVE_INST_VALU GRBM_GUI_ACTIVE",
+    "SQ_WAIT_INST_LDS SQ_WAIT_INST_ANY SQ_WAIT_ANY SQ_ACTIVE_INST_LDS SQ_LDS_BANK_CONFLICT "
+    "SQ_ACTIVE_INST_ANY SQ_INSTS_VMEM SQ_ACTIVE_INST_VMEM",
+)
+
+
+def summarize_sq_counters(base: Path, target: Path) -> None:
+    """Per-dispatch averages of two rocprofv3 --pmc passes of SQ counters (p1/, p2/ under
+    `base`) for the kernels with the most GRBM_GUI_ACTIVE cycles."""
+    import csv
+    from collections import defaultdict
+
+    per = defaultdict(lambda: defaultdict(float))  # (kernel) -> counter -> summed value
+    dispatches = defaultdict(set)
+    for sub in ("p1", "p2"):
+        for r in csv.DictReader(open(base / sub / "p_counter_collection.csv")):
+            k = _short_kernel(r["Kernel_Name"])
+            per[k][r["Counter_Name"]] += float(r["Counter_Value"])
+            dispatches[(k, sub)].add(int(r["Dispatch_Id"]))
+    rows = []
+    for k, c in per.items():
+        n1, n2 = len(dispatches[(k, "p1")]), len(dispatches[(k, "p2")])
+        if not n1 or not n2 or not c.get("SQ_WAVES"):
+            continue
+        avg = {name: v / (n1 if name in SQ_PASSES[0].split() else n2) for name, v in c.items()}
+        rows.append((k, n1, avg))
+    rows.sort(key=lambda r: -r[2].get("GRBM_GUI_ACTIVE", 0.0) * r[1])
+    lines = [
+        "# SQ counters, liver-shape sliding window (121 tiles x 8 views, one case)",
+        "",
+        "Commands (repo root on the MI355X box), one pass per line, each on its own run:",
+        "",
+        f"    rocprofv3 --pmc {SQ_PASSES[0]} -f csv -d gpurun_out/sq/p1 -o p -- \\",
+        "        python3 -u bench.py --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt",
+        f"    rocprofv3 --pmc {SQ_PASSES[1]} -f csv -d gpurun_out/sq/p2 -o p -- \\",
+        "        python3 -u bench.py --warmup 0 --steps 1 --no-cpu-baseline --no-pcie --no-alt",
+        "",
+        "Per-dispatch averages over the case's launches of each kernel. Per-wave counts divide by",
+        "SQ_WAVES; the wait and VALU-active shares divide by SQ_WAVE_CYCLES (both summed over",
+        "waves). GRBM_GUI_ACTIVE reads 8 x the kernel's duration in cycles (summed over the 8",
+        "XCDs), so per-SIMD and per-CU shares divide by GRBM_GUI_ACTIVE / 8 x 1024 SIMDs or x 256",
+        "CUs.",
+        "",
+        f"{SOURCES_LINE}{kernel_sources_digest()}.",
+        "",
+        "| kernel | dispatches | waves | VALU / wave | MFMA / wave | LDS / wave | VMEM / wave | "
+        "MFMA busy / SIMD cycles | LDS bank-conflict cycles / CU cycles | wait-any / wave cycles "
+        "| VALU active / wave cycles |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for k, n, a in rows[:8]:
+        waves = a["SQ_WAVES"]
+        cyc = a["GRBM_GUI_ACTIVE"] / 8.0
+        lines.append(
+            f"| `{k}` | {n} | {waves:.3g} | {a['SQ_INSTS_VALU'] / waves:.0f} | "
+            f"{a['SQ_INSTS_MFMA'] / waves:.1f} | {a['SQ_INSTS_LDS'] / waves:.0f} | "
+            f"{a['SQ_INSTS_VMEM'] / waves:.1f} | "
+            f"{a['SQ_VALU_MFMA_BUSY_CYCLES'] / (cyc * 1024):.3f} | "
+            f"{a['SQ_LDS_BANK_CONFLICT'] / (cyc * 256):.3f} | "
+            f"{a['SQ_WAIT_ANY'] / a['SQ_WAVE_CYCLES']:.3f} | "
+            f"{a['SQ_ACTIVE_INST_VALU'] / a['SQ_WAVE_CYCLES']:.3f} |")
+    target.write_text("\n".join(lines) + "\n")
+    print(f"wrote {target}")
 
 
 def measured_traffic(kernel_class: str) -> float | None:
