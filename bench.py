@@ -542,6 +542,86 @@ def summarize_sq_counters(base: Path, target: Path) -> None:
     print(f"wrote {target}")
 
 
+CONFIG_WORKLOADS = ("brats-sw", "autopet-sw", "pancreas-sw")
+
+
+def summarize_configs(directory: str) -> None:
+    """Write profiles/bench_configurations.md from the bench lines cfg/<W>.json and the
+    kernel traces cfg/prof_<W>/<W>_kernel_stats.csv under `directory` (W = each multi-fold or
+    bf16 workload), plus a device-peak table that also takes cfg/liver-sw.json and
+    cfg/liver-raw-case.json when present."""
+    import csv
+
+    base = Path(directory) / "cfg"
+    lines = [
+        "# Configuration benchmarks: BraTS, AutoPET and pancreas shapes (one MI355X)",
+        "",
+        "Commands (repo root on the MI355X box), per workload W in brats-sw, autopet-sw, pancreas-sw:",
+        "",
+        "    python -u bench.py --workload W --steps 1 --warmup 1 > gpurun_out/cfg/W.json",
+        "    rocprofv3 --kernel-trace --stats -f csv -d gpurun_out/cfg/prof_W -o W -- \\",
+        "        python3 -u bench.py --workload W --steps 1 --warmup 1 --no-cpu-baseline",
+        "    python bench.py --summarize-configs gpurun_out",
+        "",
+        "Kernel-trace calls count the warm-up and the timed case (2 cases); average = per launch.",
+        "",
+        f"{SOURCES_LINE}{kernel_sources_digest()}.",
+    ]
+    peaks = []
+    for w in CONFIG_WORKLOADS:
+        rec = json.loads((base / f"{w}.json").read_text().strip().splitlines()[-1])
+        roof, cpu = rec["roofline"], rec["cpu_baseline"]
+        lines += [
+            "", f"## {w}", "",
+            f"Workload: {rec['config']['workload']}", "",
+            f"* value: **{rec['value']:.4g} voxels/s** ({rec['ms_per_step'] / 1e3:.3f} s per case), "
+            f"dtype {rec['dtype']}",
+            f"* roofline (dominant kernel `{roof['kernel']}`): achieved {roof['achieved']} "
+            f"{roof['unit']} of {roof['peak']} (frac {roof['frac']}, issued {roof.get('issued_frac')})",
+        ]
+        if cpu:
+            lines.append(f"* cpu_baseline: {cpu['value']:.4g} {cpu['unit']} on {cpu['cores']} cores "
+                         f"({cpu['kind']}): {cpu['sample']}")
+        lines += [f"* label counts: {rec['config']['label_counts']}", "",
+                  "| kernel | calls | total ms | average us | % |", "|---|---:|---:|---:|---:|"]
+        for r in list(csv.DictReader(open(base / f"prof_{w}" / f"{w}_kernel_stats.csv")))[:10]:
+            lines.append(f"| `{_short_kernel(r['Name'])}` | {r['Calls']} | "
+                         f"{float(r['TotalDurationNs']) / 1e6:.1f} | {float(r['AverageNs']) / 1e3:.1f} | "
+                         f"{float(r['Percentage']):.2f} |")
+        peaks.append((w, rec))
+    described = {
+        "liver-sw": "liver-sw (1x101x768x768, 1 fold, float32 accumulation)",
+        "liver-raw-case": "liver-raw-case (512x512x120 int16 CT -> 300x534x534, float16 "
+                          "accumulation, restoration)",
+        "brats-sw": "brats-sw (4x155x240x240, 5 folds)",
+        "autopet-sw": "autopet-sw (2x284x400x400, 5 folds)",
+        "pancreas-sw": "pancreas-sw (1x101x768x768, ResEnc-L bf16-mixed)",
+    }
+    for w in ("liver-raw-case", "liver-sw"):
+        if (base / f"{w}.json").is_file():
+            peaks.insert(0, (w, json.loads((base / f"{w}.json").read_text().strip().splitlines()[-1])))
+    lines += [
+        "", "", "## Device memory peaks", "",
+        "`device_peak_gb` of each workload's bench line: the bytes in use on the GPU (hipMemGetInfo:",
+        "the library's kept workspace and torch's cached blocks) above what was in use before the",
+        "workload allocated anything, plus whatever part of torch's cached-allocator peak was released",
+        "before the reading. Liver lines from",
+        "`python -u bench.py --steps 2 --warmup 1 --no-cpu-baseline --no-pcie --no-alt > gpurun_out/cfg/liver-sw.json`",
+        "and `python -u bench.py --workload liver-raw-case --steps 2 --warmup 1 > "
+        "gpurun_out/cfg/liver-raw-case.json`. All at the default 32 views (4 mirrored tiles) a forward.",
+        "",
+        "| workload | s per case | device peak GB |",
+        "|---|---:|---:|",
+    ]
+    for w, rec in peaks:
+        lines.append(f"| {described[w]} | {rec['ms_per_step'] / 1e3:.3f} | {rec['device_peak_gb']} |")
+    lines += ["", "These are the `peak_memory_gb` values of the named models (liver from the raw-case "
+              "line, which runs what `named_models.liver.run` runs)."]
+    target = ROOT / "profiles" / "bench_configurations.md"
+    target.write_text("\n".join(lines) + "\n")
+    print(f"wrote {target}")
+
+
 def measured_traffic(kernel_class: str) -> float | None:
     """HBM bytes per launch of `kernel_class` from the committed counter summary, or None
     when the summary is missing or was measured on other kernel sources than these."""
@@ -887,6 +967,9 @@ def main() -> int:
                              "(torch.neg) whose HBM counters calibrate FETCH_SIZE/WRITE_SIZE")
     parser.add_argument("--summarize-profiles", metavar="DIR",
                         help="write the profiles/ summaries from rocprofv3 CSV output in DIR and exit")
+    parser.add_argument("--summarize-configs", metavar="DIR",
+                        help="write profiles/bench_configurations.md from the configuration bench "
+                             "lines and kernel traces under DIR/cfg and exit")
     parser.add_argument("--precision", choices=tuple(DTYPES), default="fp32-split",
                         help="convolution arithmetic: fp16-split products (3 per term) on fp16 "
                              "MFMA (default), or float32 products on fp32 MFMA; both float32 I/O "
@@ -911,6 +994,9 @@ def main() -> int:
     args = parser.parse_args()
     if args.summarize_profiles:
         summarize_profiles(args.summarize_profiles)
+        return 0
+    if args.summarize_configs:
+        summarize_configs(args.summarize_configs)
         return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: this build has no multi-GPU path "
