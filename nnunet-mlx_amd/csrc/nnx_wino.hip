@@ -159,10 +159,12 @@ __device__ __forceinline__ void lds_barrier() {
 // leave as 16-byte channel runs; the box's InstanceNorm partials per column (mean over the
 // valid voxels, then the centred sum of squares) are reduced from the registers: a thread's
 // 16 voxels, the two lanes of a wave holding the column, then the eight waves through the
-// two 256-float arrays after the tile.  Barriers wait for LDS only.
-__device__ __forceinline__ void wino_epilogue_tail(const WinoArgs& a, const f4 (&yo)[2][2],
-                                                   float* otile, int tid, int lane, int wave,
-                                                   int b, int nt, int bzi, int byi, int bxi) {
+// two 256-float arrays after the tile.  Barriers wait for LDS only.  kFull: the box lies
+// wholly inside the volume (no per-voxel checks).
+template <bool kFull>
+__device__ __forceinline__ void wino_epilogue_tail_t(const WinoArgs& a, const f4 (&yo)[2][2],
+                                                     float* otile, int tid, int lane, int wave,
+                                                     int b, int nt, int bzi, int byi, int bxi) {
   const int oz0 = bzi * 4, oy0 = byi * 8, ox0 = bxi * 8;
   const int c = tid & 31;
   auto voxel = [&](int k, int oz, int e) {
@@ -176,8 +178,6 @@ __device__ __forceinline__ void wino_epilogue_tail(const WinoArgs& a, const f4 (
     for (int oz = 0; oz < 2; ++oz)
 #pragma unroll
       for (int e = 0; e < 4; ++e) otile[voxel(k, oz, e) * kTileStride + c] = yo[k][oz][e];
-  // a box wholly inside the volume (uniform over the workgroup) skips the voxel checks
-  const bool full = oz0 + 4 <= a.D && oy0 + 8 <= a.H && ox0 + 8 <= a.W;
   auto valid = [&](int v) {
     return oz0 + (v >> 6) < a.D && oy0 + ((v >> 3) & 7) < a.H && ox0 + (v & 7) < a.W;
   };
@@ -192,15 +192,19 @@ __device__ __forceinline__ void wino_epilogue_tail(const WinoArgs& a, const f4 (
       for (int oz = 0; oz < 2; ++oz)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (full || valid(voxel(k, oz, e))) sm += yo[k][oz][e];
+          if (kFull || valid(voxel(k, oz, e))) sm += yo[k][oz][e];
     sm += __shfl_xor(sm, 32);
     if (lane < 32) red[wave * 32 + c] = sm;
   }
   lds_barrier();  // the tile and the sums
   if (a.stats) {
+    // the eight waves' sums read together, then added in wave order
+    float rv[kWThreads / 64];
+#pragma unroll
+    for (int w = 0; w < kWThreads / 64; ++w) rv[w] = red[w * 32 + c];
     float tot = 0.f;
 #pragma unroll
-    for (int w = 0; w < kWThreads / 64; ++w) tot += red[w * 32 + c];
+    for (int w = 0; w < kWThreads / 64; ++w) tot += rv[w];
     const float mean = tot / cnt;
     float m2 = 0.f;
 #pragma unroll
@@ -209,7 +213,7 @@ __device__ __forceinline__ void wino_epilogue_tail(const WinoArgs& a, const f4 (
       for (int oz = 0; oz < 2; ++oz)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
-          if (full || valid(voxel(k, oz, e))) {
+          if (kFull || valid(voxel(k, oz, e))) {
             const float d = yo[k][oz][e] - mean;
             m2 = fmaf(d, d, m2);
           }
@@ -217,27 +221,43 @@ __device__ __forceinline__ void wino_epilogue_tail(const WinoArgs& a, const f4 (
     if (lane < 32) red[256 + wave * 32 + c] = m2;
     lds_barrier();
     if (tid < 32) {
+#pragma unroll
+      for (int w = 0; w < kWThreads / 64; ++w) rv[w] = red[256 + w * 32 + c];
       float tm = 0.f;
 #pragma unroll
-      for (int w = 0; w < kWThreads / 64; ++w) tm += red[256 + w * 32 + c];
+      for (int w = 0; w < kWThreads / 64; ++w) tm += rv[w];
       const int tiles = a.nbz * a.nby * a.nbx;
       const int tile_s = (bzi * a.nby + byi) * a.nbx + bxi;
       a.stats[((int64_t)b * tiles + tile_s) * a.cout + nt * 32 + c] = make_float4(mean, tm, cnt, 0.f);
     }
   }
-  // stores: 256 voxels x 8 runs of 4 channels
-  const int64_t bvox = (int64_t)b * a.D * a.H * a.W;
+  // stores: 256 voxels x 8 runs of 4 channels; thread tid stores run tid % 8 of voxel
+  // (z, y, x) = (k, (tid / 64) % 8, (tid / 8) % 8) of the box in round k, so only z moves
+  // between its rounds (one 64-bit address, then a plane stride)
+  const int qd = tid & 7, vyx = (tid >> 3) & 63;
+  const int yy = oy0 + (vyx >> 3), xx = ox0 + (vyx & 7);
+  const int64_t base =
+      (((int64_t)b * a.D + oz0) * a.H * a.W + (int64_t)yy * a.W + xx) * a.cout + nt * 32 + 4 * qd;
+  const int64_t zstride = (int64_t)a.H * a.W * a.cout;
+  static_assert(256 * 8 / kWThreads == 4 && kWThreads == 512, "one box z-plane a round");
 #pragma unroll
-  for (int k = 0; k < 256 * 8 / kWThreads; ++k) {
-    const int idx = tid + k * kWThreads;
-    const int v = idx >> 3, qd = idx & 7;
-    if (full || valid(v)) {
-      const int z = oz0 + (v >> 6), yy = oy0 + ((v >> 3) & 7), xx = ox0 + (v & 7);
+  for (int k = 0; k < 4; ++k) {
+    const int v = k * 64 + vyx;
+    if (kFull || valid(v)) {
       const float* src = otile + v * kTileStride + 4 * qd;
-      *reinterpret_cast<f4*>(a.y + (bvox + ((int64_t)z * a.H + yy) * a.W + xx) * a.cout +
-                             nt * 32 + 4 * qd) = f4{src[0], src[1], src[2], src[3]};
+      *reinterpret_cast<f4*>(a.y + base + k * zstride) = f4{src[0], src[1], src[2], src[3]};
     }
   }
+}
+
+__device__ __forceinline__ void wino_epilogue_tail(const WinoArgs& a, const f4 (&yo)[2][2],
+                                                   float* otile, int tid, int lane, int wave,
+                                                   int b, int nt, int bzi, int byi, int bxi) {
+  // uniform over the workgroup
+  if (bzi * 4 + 4 <= a.D && byi * 8 + 8 <= a.H && bxi * 8 + 8 <= a.W)
+    wino_epilogue_tail_t<true>(a, yo, otile, tid, lane, wave, b, nt, bzi, byi, bxi);
+  else
+    wino_epilogue_tail_t<false>(a, yo, otile, tid, lane, wave, b, nt, bzi, byi, bxi);
 }
 
 __global__ __launch_bounds__(kWThreads, 1) void wino_x3_kernel(WinoArgs a) {
@@ -818,8 +838,8 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3p_kernel(WinoArgs a) {
     };
     const int col = lane & 31;
     f4 yo[kPairs][2];
-#pragma unroll
-    for (int h = 0; h < kPairs; ++h) {
+    // this wave's partials of round h (p is uniform over the wave: one branch, no selects)
+    auto write_parts = [&](int h, auto P) __attribute__((always_inline)) {
 #pragma unroll
       for (int r = 8 * h; r < 8 * h + 8; ++r) {
         float xo[2][2];
@@ -829,10 +849,20 @@ __global__ __launch_bounds__(kWThreads, 1) void wino_x3p_kernel(WinoArgs a) {
           xo[jj][0] = (m0 + m1) + m2;
           xo[jj][1] = (m1 - m2) - m3;
         }
-        const f4 pv = p == 0 ? f4{xo[0][0] + xo[1][0], xo[0][1] + xo[1][1], xo[1][0], xo[1][1]}
-                             : f4{xo[0][0], xo[0][1], -(xo[0][0] + xo[1][0]), -(xo[0][1] + xo[1][1])};
+        f4 pv;
+        if constexpr (decltype(P)::value == 0)
+          pv = f4{xo[0][0] + xo[1][0], xo[0][1] + xo[1][1], xo[1][0], xo[1][1]};
+        else
+          pv = f4{xo[0][0], xo[0][1], -(xo[0][0] + xo[1][0]), -(xo[0][1] + xo[1][1])};
         part(wave, 8 * (r >> 2) + 4 * g8 + (r & 3) - 16 * h, col) = pv;
       }
+    };
+#pragma unroll
+    for (int h = 0; h < kPairs; ++h) {
+      if (p == 0)
+        write_parts(h, std::integral_constant<int, 0>{});
+      else
+        write_parts(h, std::integral_constant<int, 1>{});
       lds_barrier();
       {
         const int tile = tid >> 5, c = tid & 31;
