@@ -136,6 +136,15 @@ __device__ __forceinline__ void zrow_pair(unsigned a, unsigned b, f4 (&va)[8], f
       : "memory");
 }
 
+// For lanes 0-31: x + (lane + 32's x), by v_permlane32_swap (lanes 32-63 of the first
+// operand trade places with lanes 0-31 of the second) instead of an LDS permute.  Lanes
+// 32-63 get x + x (unused).
+__device__ __forceinline__ float add_upper_half(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                  false);
+  return x + __uint_as_float(r[1]);
+}
+
 // The InstanceNorm apply pass's operations: r = fma(x - mean, scale, beta), then
 // max(s * r, r) with s = the LeakyReLU slope under the activation and s = 1 (the identity,
 // exactly) without it.
@@ -193,7 +202,7 @@ __device__ __forceinline__ void wino_epilogue_tail_t(const WinoArgs& a, const f4
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           if (kFull || valid(voxel(k, oz, e))) sm += yo[k][oz][e];
-    sm += __shfl_xor(sm, 32);
+    sm = add_upper_half(sm);
     if (lane < 32) red[wave * 32 + c] = sm;
   }
   lds_barrier();  // the tile and the sums
@@ -217,7 +226,7 @@ __device__ __forceinline__ void wino_epilogue_tail_t(const WinoArgs& a, const f4
             const float d = yo[k][oz][e] - mean;
             m2 = fmaf(d, d, m2);
           }
-    m2 += __shfl_xor(m2, 32);
+    m2 = add_upper_half(m2);
     if (lane < 32) red[256 + wave * 32 + c] = m2;
     lds_barrier();
     if (tid < 32) {
