@@ -630,6 +630,7 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
 // ---------------------------------------------------------------------------------
 typedef _Float16 h8 __attribute__((ext_vector_type(8)));
 typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ f4 mfma16x16x32h(h8 a, h8 b, f4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -659,6 +660,36 @@ __device__ __forceinline__ void to_operand(float v, _Float16& hi, _Float16& lo) 
     lo = (_Float16)0.f;
   } else {
     split_half(v, hi, lo);
+  }
+}
+
+// to_operand of four values.  kSplit3: hi by v_cvt_pk_f16_f32 (nearest even, two values an
+// instruction) and lo by one v_fma_mix{lo,hi}_f16 each: fma(hi, -1, v) is v - hi, exact in
+// float32 (hi is v's nearest fp16), rounded once to fp16, i.e. the same bits as
+// split_half's fp16(v - float(hi)) in 1.5 instructions a value instead of 4.
+template <int AR>
+__device__ __forceinline__ void to_operand4(const f4& v, h4& hv, h4& lv) {
+  if constexpr (AR == kBf16) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      _Float16 hh, ll;
+      to_operand<kBf16>(v[q], hh, ll);
+      hv[q] = hh;
+      lv[q] = ll;
+    }
+  } else {
+#pragma unroll
+    for (int q = 0; q < 4; q += 2) {
+      const h2 h = __builtin_convertvector((f2{v[q], v[q + 1]}), h2);
+      h2 l;
+      asm("v_fma_mixlo_f16 %0, %1, -1.0, %2 op_sel_hi:[1,0,0]" : "=v"(l) : "v"(h), "v"(v[q]));
+      asm("v_fma_mixhi_f16 %0, %1, -1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]"
+          : "+v"(l) : "v"(h), "v"(v[q + 1]));
+      hv[q] = h[0];
+      hv[q + 1] = h[1];
+      lv[q] = l[0];
+      lv[q + 1] = l[1];
+    }
   }
 }
 
@@ -816,13 +847,7 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
         f4 val = stage[j];
         if (nl_staged.on && vofs[j] >= 0) val = norm_apply4(val, nl_staged, a.slope);
         h4 hv, lv;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          _Float16 hh, ll;
-          to_operand<AR>(val[q], hh, ll);
-          hv[q] = hh;
-          lv[q] = ll;
-        }
+        to_operand4<AR>(val, hv, lv);
         *reinterpret_cast<h4*>(hi_plane + line * 4) = hv;
         if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
       }
@@ -1019,13 +1044,7 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3s_kernel(IgemmArgs a) 
         if (line < nlines) {
           if (nl.on && in[j]) val[j] = norm_apply4(val[j], nl, a.slope);
           h4 hv, lv;
-#pragma unroll
-          for (int q = 0; q < 4; ++q) {
-            _Float16 hh, ll;
-            to_operand<AR>(val[j][q], hh, ll);
-            hv[q] = hh;
-            lv[q] = ll;
-          }
+          to_operand4<AR>(val[j], hv, lv);
           *reinterpret_cast<h4*>(hi_plane + line * 4) = hv;
           if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo_plane + line * 4) = lv;
         }
@@ -2029,13 +2048,7 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
         f4 v = lines[j];
         if (a.nrm && m0 + r < a.M) v = norm_apply4(v, nl, a.slope);
         h4 hv, lv;
-#pragma unroll
-        for (int q = 0; q < 4; ++q) {
-          _Float16 hh, ll;
-          to_operand<AR>(v[q], hh, ll);
-          hv[q] = hh;
-          lv[q] = ll;
-        }
+        to_operand4<AR>(v, hv, lv);
         *reinterpret_cast<h4*>(hi + r * kTcRowHalves + c4) = hv;
         if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo + r * kTcRowHalves + c4) = lv;
       }
