@@ -321,15 +321,17 @@ __global__ __launch_bounds__(256) void norm_merge_final_kernel(const float4* __r
 }
 
 // y = act(fma(x (+ bias) - mean, scale, beta) (+ residual)) over a (B, S, C) tensor, VW
-// channels a vector.  Grid-stride over an item's vectors with kUnroll vectors in flight per
-// thread (all loads issued before the arithmetic); a thread's channel index advances by
-// the grid stride modulo C, so no division per element.  y may alias x.
+// channels a vector.  A workgroup streams runs of kRun = 4 * 256 consecutive vectors of one
+// item (thread t takes vectors t, t + 256, t + 512, t + 768 of the run, all four loads
+// issued before the arithmetic), runs gridDim.x apart; the channel of each vector follows
+// from the run's first channel (advanced by the run stride modulo C) and the thread's four
+// fixed offsets, and the parameters come from LDS.  y may alias x.
 template <int VW>
 __global__ __launch_bounds__(256) void norm_apply_kernel(
     const float* x, float* y, const float4* __restrict__ params, const float* __restrict__ in_bias,
     const float* residual, int64_t SC, int C, int act, float slope) {
   typedef typename Vec<VW>::type V;
-  constexpr int kUnroll = 4;
+  constexpr int kUnroll = 4, kRun = kUnroll * 256;
   extern __shared__ float smem[];  // C * 4: mean, scale, beta, input bias
   float* s_mean = smem;
   float* s_scale = smem + C;
@@ -349,10 +351,14 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(
   const float* rs = residual ? residual + (int64_t)b * SC : nullptr;
   const int64_t nvec = SC / VW;
   const bool has_bias = in_bias != nullptr;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  int c0 = (int)((i * VW) % C);            // channel of this thread's current vector
-  const int dc = (int)((stride * VW) % C);  // its advance per grid stride
+  const int tid = threadIdx.x;
+  // channel offsets of the thread's four vectors within a run, and the run's first channel
+  int cu[kUnroll];
+#pragma unroll
+  for (int u = 0; u < kUnroll; ++u) cu[u] = (int)(((int64_t)(u * 256 + tid) * VW) % C);
+  int64_t run = blockIdx.x;
+  int crun = (int)((run * kRun * VW) % C);
+  const int dcrun = (int)(((int64_t)gridDim.x * kRun * VW) % C);
   auto apply = [&](V xv, V rv, int cb) {
     V out;
 #pragma unroll
@@ -367,29 +373,35 @@ __global__ __launch_bounds__(256) void norm_apply_kernel(
     }
     return out;
   };
-  for (; i + (kUnroll - 1) * stride < nvec; i += kUnroll * stride) {
+  auto chan = [&](int u) {
+    const int c = crun + cu[u];
+    return c >= C ? c - C : c;
+  };
+  for (; (run + 1) * kRun <= nvec; run += gridDim.x) {
+    const int64_t v0 = run * kRun + tid;
     V xv[kUnroll], rv[kUnroll];
-    int cb[kUnroll];
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u) {
-      const int64_t e = (i + u * stride) * VW;
-      xv[u] = *reinterpret_cast<const V*>(xs + e);
-      if (rs) rv[u] = *reinterpret_cast<const V*>(rs + e);
-      cb[u] = c0;
-      c0 += dc;
-      if (c0 >= C) c0 -= C;
+      xv[u] = *reinterpret_cast<const V*>(xs + (v0 + u * 256) * VW);
+      if (rs) rv[u] = *reinterpret_cast<const V*>(rs + (v0 + u * 256) * VW);
     }
 #pragma unroll
     for (int u = 0; u < kUnroll; ++u)
-      *reinterpret_cast<V*>(ys + (i + u * stride) * VW) = apply(xv[u], rs ? rv[u] : xv[u], cb[u]);
+      *reinterpret_cast<V*>(ys + (v0 + u * 256) * VW) = apply(xv[u], rs ? rv[u] : xv[u], chan(u));
+    crun += dcrun;
+    if (crun >= C) crun -= C;
   }
-  for (; i < nvec; i += stride) {
-    const int64_t e = i * VW;
-    const V xv = *reinterpret_cast<const V*>(xs + e);
-    const V rv = rs ? *reinterpret_cast<const V*>(rs + e) : xv;
-    *reinterpret_cast<V*>(ys + e) = apply(xv, rv, c0);
-    c0 += dc;
-    if (c0 >= C) c0 -= C;
+  // the partial last run
+  if (run * kRun < nvec) {
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t v = run * kRun + u * 256 + tid;
+      if (v < nvec) {
+        const V xv = *reinterpret_cast<const V*>(xs + v * VW);
+        const V rv = rs ? *reinterpret_cast<const V*>(rs + v * VW) : xv;
+        *reinterpret_cast<V*>(ys + v * VW) = apply(xv, rv, chan(u));
+      }
+    }
   }
 }
 
@@ -629,22 +641,22 @@ void instnorm_apply_params(const float* x, float* y, int batch, int64_t spatial,
                            const float4* params, const float* input_bias, bool act, float slope,
                            const float* residual, hipStream_t st) {
   require(x && y && params, "instance normalisation pointers must not be null");
-  require(channels <= 1024, "instance normalisation supports at most 1024 channels");
+  require(channels >= 1 && channels <= 1024, "instance normalisation supports 1 to 1024 channels");
+  require(batch >= 1 && batch <= 65535, "instance normalisation batch out of range");
   const int vw = channels % 4 == 0 ? 4 : 1;
   const double nelem = (double)batch * spatial * channels;
   ProfScope prof("instnorm_apply", 0.0, 4.0 * nelem * (residual ? 3 : 2), st);
   const int64_t sc = spatial * channels;
   const int64_t nvec = sc / vw;
-  const int64_t blocks = std::min<int64_t>(ceil_div(nvec, 256 * 4), 16384);
+  // blocks a batch item: one run of 1024 vectors each, up to 16384 (then they loop)
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(ceil_div(nvec, 1024), 16384));
   const size_t smem = (size_t)channels * 4 * sizeof(float);
   if (vw == 4)
-    hipLaunchKernelGGL(norm_apply_kernel<4>, dim3((unsigned)std::max<int64_t>(blocks, 1), batch),
-                       dim3(256), smem, st, x, y, params, input_bias, residual, sc, channels,
-                       act ? 1 : 0, slope);
+    hipLaunchKernelGGL(norm_apply_kernel<4>, dim3((unsigned)blocks, batch), dim3(256), smem, st,
+                       x, y, params, input_bias, residual, sc, channels, act ? 1 : 0, slope);
   else
-    hipLaunchKernelGGL(norm_apply_kernel<1>, dim3((unsigned)std::max<int64_t>(blocks, 1), batch),
-                       dim3(256), smem, st, x, y, params, input_bias, residual, sc, channels,
-                       act ? 1 : 0, slope);
+    hipLaunchKernelGGL(norm_apply_kernel<1>, dim3((unsigned)blocks, batch), dim3(256), smem, st,
+                       x, y, params, input_bias, residual, sc, channels, act ? 1 : 0, slope);
   launch_check("instnorm apply");
 }
 
