@@ -2001,9 +2001,40 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
       if (ks < a.ksteps) load_b(BR[ks], ks);
   }
 
-  // row tiles tpb * (logical / ntn) .. of column tile nt, one after the other
+  // rows m0.., channels kb..kb+63: 16 float4 lines per row, 4 per thread
+  constexpr int kLines = kTcRows * (kTcKBlock / 4) / 256;
+  auto load_lines = [&](int64_t m0, int kb, f4 (&lines)[kLines]) {
+#pragma unroll
+    for (int j = 0; j < kLines; ++j) {
+      const int i = tid + 256 * j;
+      const int r = i >> 4, c4 = (i & 15) * 4;
+      const int64_t m = m0 + r;
+      const int c = kb + c4;
+      f4 v = {0.f, 0.f, 0.f, 0.f};
+      if (m < a.M) {
+        const float* src = a.x + m * a.cin + c;
+        if (c + 3 < a.cin) {
+          v = *reinterpret_cast<const f4*>(src);
+        } else {
+#pragma unroll
+          for (int q = 0; q < 4; ++q)
+            if (c + q < a.cin) v[q] = src[q];
+        }
+      }
+      lines[j] = v;
+    }
+  };
+
+  // row tiles tpb * (logical / ntn) .. of column tile nt, one after the other.  KREG > 0
+  // (C_in <= 64: one channel block): the next row tile's lines are requested once this
+  // tile's are in LDS, so they land during this tile's products and stores
   const int64_t t_begin = (int64_t)(logical / a.ntn) * a.tpb;
-  for (int64_t t = t_begin; t < t_begin + a.tpb; ++t) {
+  const int64_t t_end = t_begin + a.tpb;
+  f4 pre[kLines];
+  if constexpr (KREG > 0) {
+    if (t_begin * kTcRows < a.M) load_lines(t_begin * kTcRows, 0, pre);
+  }
+  for (int64_t t = t_begin; t < t_end; ++t) {
     const int64_t m0 = t * kTcRows;
     if (m0 >= a.M) break;
     f4 acc[MB][NB];
@@ -2013,28 +2044,13 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
       for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
 
     for (int kb = 0; kb < a.cin; kb += kTcKBlock) {
-      // rows m0.., channels kb..kb+63: 16 float4 lines per row, 4 per thread, all requested
-      // before the barrier
-      constexpr int kLines = kTcRows * (kTcKBlock / 4) / 256;
+      // all lines requested before the barrier
       f4 lines[kLines];
+      if constexpr (KREG > 0) {
 #pragma unroll
-      for (int j = 0; j < kLines; ++j) {
-        const int i = tid + 256 * j;
-        const int r = i >> 4, c4 = (i & 15) * 4;
-        const int64_t m = m0 + r;
-        const int c = kb + c4;
-        f4 v = {0.f, 0.f, 0.f, 0.f};
-        if (m < a.M) {
-          const float* src = a.x + m * a.cin + c;
-          if (c + 3 < a.cin) {
-            v = *reinterpret_cast<const f4*>(src);
-          } else {
-#pragma unroll
-            for (int q = 0; q < 4; ++q)
-              if (c + q < a.cin) v[q] = src[q];
-          }
-        }
-        lines[j] = v;
+        for (int j = 0; j < kLines; ++j) lines[j] = pre[j];
+      } else {
+        load_lines(m0, kb, lines);
       }
       // the pending normalisation of this thread's channel quad (the same for all its
       // lines; a row tile lies in one batch item, vox being a multiple of the tile rows)
@@ -2053,6 +2069,9 @@ __global__ __launch_bounds__(256, 2) void tconv_x3_kernel(TcArgs a) {
         if constexpr (AR == kSplit3) *reinterpret_cast<h4*>(lo + r * kTcRowHalves + c4) = lv;
       }
       __syncthreads();
+      if constexpr (KREG > 0) {
+        if (t + 1 < t_end && m0 + kTcRows < a.M) load_lines(m0 + kTcRows, 0, pre);
+      }
 #pragma unroll
       for (int ks = 0; ks < kTcKBlock / 32; ++ks) {
         const int kstep = kb / 32 + ks;
