@@ -724,8 +724,10 @@ __device__ __forceinline__ void mma_products(f4 (&acc)[MB][NB], const h8 (&A)[MB
 constexpr int kX3MaxLines = 6;  // halo lines per thread in flight (register staging)
 constexpr int kX3Threads = 256;
 
+// Weights stream one tap group ahead (double-buffered fragments); with two column blocks a
+// wave (150 registers) three workgroups share a CU, with four (182) two.
 template <int MB, int NB, int WM, int WN, int NTG, bool VEC, int AR>
-__global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
+__global__ __launch_bounds__(64 * WM* WN, NB <= 2 ? 3 : 2) void igemm_x3_kernel(IgemmArgs a) {
   extern __shared__ __align__(16) float lds[];
   constexpr int NT = 64 * WM * WN;
   static_assert(NT == kX3Threads, "split kernel variants use 256 threads");
@@ -810,11 +812,10 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
   }
   const int64_t bvox = (int64_t)b * a.id * a.ih * a.iw;
 
-  // two column blocks a wave: a chunk's weight fragments fit in registers at once
-  constexpr bool kPreloadB = NB <= 2;
   // The next chunk's lines are requested without branches (lines outside the volume read
-  // a zero line) and are used only at publish time, where the pending normalisation is
-  // applied, so their loads stay in flight while the current chunk computes.
+  // a zero line) after the chunk's last weight request, so no weight wait (vector-memory
+  // counters complete in issue order) queues behind them; they are used only at publish
+  // time, where the pending normalisation is applied.
   const float* zero = g_zero_line;
   f4 stage[kX3MaxLines];
   NormLine nl_staged;
@@ -878,41 +879,10 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
         if constexpr (AR == kSplit3) A[p][mb][1] = lo8[hbase[mb] + toff[g]];
       }
     };
-    if constexpr (kPreloadB) {
-      // every tap group's weights are requested before the next halo: vector-memory
-      // counters complete in issue order, so no weight wait queues behind the halo loads
-      __syncthreads();  // the previous chunk's fragments have been read
-      publish();
-      __syncthreads();
-      h8 BA[NTG][NB][2];
-#pragma unroll
-      for (int g = 0; g < NTG; ++g)
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const uint4 wh = wc[g * group_stride + nb * 128];
-          BA[g][nb][0] = *reinterpret_cast<const h8*>(&wh);
-          if constexpr (AR == kSplit3) {
-            const uint4 wl = wc[g * group_stride + nb * 128 + 64];
-            BA[g][nb][1] = *reinterpret_cast<const h8*>(&wl);
-          }
-        }
-      // lands while this chunk computes; unconditional (the last chunk re-reads its own
-      // lines), so no control-flow join makes the weight waits cover the halo loads
-      fetch(chunk + 1 < a.chunks ? chunk + 1 : chunk);
-      load_a(0, 0);
-#pragma unroll
-      for (int g = 0; g < NTG; ++g) {
-        const int cur = g & 1;
-        if (g + 1 < NTG) load_a(cur ^ 1, g + 1);
-        mma_products<AR>(acc, A[cur], BA[g]);
-      }
-      continue;
-    }
     load_b(0, 0);  // in flight across the barriers below
     __syncthreads();  // the previous chunk's fragments have been read
     publish();
     __syncthreads();
-    if (chunk + 1 < a.chunks) fetch(chunk + 1);  // lands while this chunk computes
     load_a(0, 0);
 #pragma unroll
     for (int g = 0; g < NTG; ++g) {
@@ -923,6 +893,7 @@ __global__ __launch_bounds__(64 * WM* WN, 2) void igemm_x3_kernel(IgemmArgs a) {
       }
       mma_products<AR>(acc, A[cur], B[cur]);
     }
+    if (chunk + 1 < a.chunks) fetch(chunk + 1);
   }
   igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
                                  ox0, a.out_scale);
