@@ -2556,9 +2556,9 @@ X3Plan plan_x3(const ConvGeom& g, int cout) {
     return p;
   } catch (const Error&) {
   }
-  // N 64 (weights preloaded a chunk at a time) up to 64 output channels, and wherever
-  // N 128 would leave fewer than 4 workgroups a CU; N 128 (half the halo staging per
-  // output channel) otherwise
+  // N 64 (three workgroups a CU) up to 64 output channels, and wherever N 128 would leave
+  // fewer than 4 workgroups a CU; N 128 (half the halo staging per output channel, two
+  // workgroups a CU) otherwise
   p.v = kX3F;
   p.box = choose_box(kX3F, g, false, kX3MaxHalo);
   if (cout > 64) {
