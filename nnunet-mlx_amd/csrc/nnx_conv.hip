@@ -724,10 +724,12 @@ __device__ __forceinline__ void mma_products(f4 (&acc)[MB][NB], const h8 (&A)[MB
 constexpr int kX3MaxLines = 6;  // halo lines per thread in flight (register staging)
 constexpr int kX3Threads = 256;
 
-// Weights stream one tap group ahead (double-buffered fragments); with two column blocks a
-// wave (150 registers) three workgroups share a CU, with four (182) two.
+// Weights stream one tap group ahead (double-buffered fragments).  Three workgroups share a
+// CU: 150 registers with two column blocks a wave; with four the compiler fits 168 by
+// spilling 4 registers outside the chunk loop (2.84 -> 2.60 ms a liver forward against two
+// workgroups a CU at 182 registers).
 template <int MB, int NB, int WM, int WN, int NTG, bool VEC, int AR>
-__global__ __launch_bounds__(64 * WM* WN, NB <= 2 ? 3 : 2) void igemm_x3_kernel(IgemmArgs a) {
+__global__ __launch_bounds__(64 * WM* WN, 3) void igemm_x3_kernel(IgemmArgs a) {
   extern __shared__ __align__(16) float lds[];
   constexpr int NT = 64 * WM * WN;
   static_assert(NT == kX3Threads, "split kernel variants use 256 threads");
@@ -2556,9 +2558,8 @@ X3Plan plan_x3(const ConvGeom& g, int cout) {
     return p;
   } catch (const Error&) {
   }
-  // N 64 (three workgroups a CU) up to 64 output channels, and wherever N 128 would leave
-  // fewer than 4 workgroups a CU; N 128 (half the halo staging per output channel, two
-  // workgroups a CU) otherwise
+  // N 64 up to 64 output channels, and wherever N 128 would leave fewer than 4 workgroups
+  // a CU; N 128 (half the halo staging per output channel) otherwise
   p.v = kX3F;
   p.box = choose_box(kX3F, g, false, kX3MaxHalo);
   if (cout > 64) {
