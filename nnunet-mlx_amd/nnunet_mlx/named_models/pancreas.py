@@ -14,7 +14,7 @@ MODEL = {
     # Measured MI355X device peak (library workspace + torch allocations) for a 101x768x768
     # CT, ResEnc-L in bf16-mixed, 32 patches a forward (bench.py --workload pancreas-sw);
     # larger inputs need more.
-    "peak_memory_gb": 75.4,
+    "peak_memory_gb": 75.3,
     "summary": "PancCTMultiTalentV2 pancreas and cancer segmentation.",
     "labels": {"1": "pancreas", "2": "cancer"},
 }
