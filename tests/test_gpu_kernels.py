@@ -353,6 +353,9 @@ NORM_CASES = [
     (1, (8, 8, 8), 64, True, True, False, True),
     (2, (5, 6, 7), 2, True, True, True, True),
     (1, (32, 32, 32), 128, False, True, True, False),
+    # more than 16384 runs of 1024 vectors an item: workgroups loop over runs, the run's
+    # first channel advancing by 64 modulo 320; a partial last run
+    (1, (55, 61, 63), 320, True, False, True, True),
 ]
 
 
@@ -432,6 +435,9 @@ def test_tconv3d_gemm_matches_float64(lib, case):
     (1, (8, 8, 8), 128, 64, (2, 2, 2)),
     (1, (3, 5, 2), 6, 4, (2, 1, 2)),
     (3, (5, 6, 7), 96, 24, (2, 2, 2)),
+    # two row tiles a workgroup (the next one's lines requested during the current one)
+    # and a partial last tile
+    (2, (39, 41, 47), 64, 32, (2, 2, 2)),
 ], ids=str)
 def test_tconv3d_split_matches_float64(lib, case):
     """Split-fp16 products hold the float32 bar (rel-L2 <= 1e-5) of the transposed conv."""
