@@ -1713,8 +1713,8 @@ __global__ __launch_bounds__(256, (kDirX3Waves<COUT, CIN>)) void direct_cin1_x3_
         }
       if (lane == 0) wcnt[wave] = cnt;
       lds_barrier();
-      if (wave == 0 && row == 0) {
-        // merge weights of waves 1..3 (the same for every channel)
+      if (wave == 0) {
+        // merge weights of waves 1..3 (the same for every channel), then a lane a channel
         float fw[4], gw[4], na = wcnt[0];
 #pragma unroll
         for (int q = 1; q < 4; ++q) {
@@ -1723,22 +1723,17 @@ __global__ __launch_bounds__(256, (kDirX3Waves<COUT, CIN>)) void direct_cin1_x3_
           gw[q] = nq > 0.f ? na * nq / nab : 0.f;
           na = nab;
         }
+        for (int n = lane; n < NB * 16; n += 64) {
+          float mean = red[0][n], m2 = red2[0][n];
 #pragma unroll
-        for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int n = nb * 16 + slot * 4 + r;
-            float mean = red[0][n], m2 = red2[0][n];
-#pragma unroll
-            for (int q = 1; q < 4; ++q) {
-              const float delta = red[q][n] - mean;
-              mean = fmaf(delta, fw[q], mean);
-              m2 += red2[q][n] + delta * delta * gw[q];
-            }
-            if (n < cout)
-              stats[((int64_t)blockIdx.y * ntiles + tile) * cout + n] =
-                  make_float4(mean, m2, na, 0.f);
+          for (int q = 1; q < 4; ++q) {
+            const float delta = red[q][n] - mean;
+            mean = fmaf(delta, fw[q], mean);
+            m2 += red2[q][n] + delta * delta * gw[q];
           }
+          if (n < cout)
+            stats[((int64_t)blockIdx.y * ntiles + tile) * cout + n] = make_float4(mean, m2, na, 0.f);
+        }
       }
     }
     if (tile + 1 < t_end) wave_max(buf ^ 1);
