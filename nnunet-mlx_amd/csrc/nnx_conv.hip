@@ -221,11 +221,12 @@ __device__ __forceinline__ HaloSource halo_source(const IgemmArgs& a, int chunk)
 // addition; optional fused InstanceNorm partials, then the stores.
 // VST: with a.vstore set, the tile is transposed through LDS (rows padded by 4 floats) and
 // written as whole 16-byte words per lane, each voxel's channel run contiguous
-template <int MB, int NB, int WM, int WN, bool VST = false>
-__device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB][NB], float* lds,
-                                               int wm, int wn, int slot, int row, int nbk0, int b,
-                                               int tzi, int tyi, int txi, int oz0, int oy0, int ox0,
-                                               float out_scale) {
+// kFull: the tile lies wholly inside the output volume (no per-voxel checks).
+template <int MB, int NB, int WM, int WN, bool VST, bool kFull>
+__device__ __forceinline__ void igemm_epilogue_t(const IgemmArgs& a, f4 (&acc)[MB][NB], float* lds,
+                                                 int wm, int wn, int slot, int row, int nbk0,
+                                                 int b, int tzi, int tyi, int txi, int oz0,
+                                                 int oy0, int ox0, float out_scale) {
   if (out_scale != 1.0f) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
@@ -249,7 +250,7 @@ __device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB]
     *z = oz0 + vz;
     *yy = oy0 + vy;
     *xx = ox0 + vx;
-    return *z < a.od && *yy < a.oh && *xx < a.ow;
+    return kFull || (*z < a.od && *yy < a.oh && *xx < a.ow);
   };
   if (a.stats) {
     if constexpr (VST) {
@@ -450,6 +451,20 @@ __device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB]
   }
 }
 
+template <int MB, int NB, int WM, int WN, bool VST = false>
+__device__ __forceinline__ void igemm_epilogue(const IgemmArgs& a, f4 (&acc)[MB][NB], float* lds,
+                                               int wm, int wn, int slot, int row, int nbk0, int b,
+                                               int tzi, int tyi, int txi, int oz0, int oy0, int ox0,
+                                               float out_scale) {
+  // uniform over the workgroup
+  if (oz0 + a.bz <= a.od && oy0 + a.by <= a.oh && ox0 + a.bx <= a.ow)
+    igemm_epilogue_t<MB, NB, WM, WN, VST, true>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi,
+                                                txi, oz0, oy0, ox0, out_scale);
+  else
+    igemm_epilogue_t<MB, NB, WM, WN, VST, false>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi,
+                                                 tyi, txi, oz0, oy0, ox0, out_scale);
+}
+
 // ASYNC: both inputs have channel counts that are multiples of 8, so every halo float4 is
 // a whole aligned 16-byte line (or padding).  The halo is double-buffered in LDS and the
 // next chunk is fetched with global_load_lds_dwordx4 (direct to LDS, no registers), one
@@ -612,8 +627,9 @@ __global__ __launch_bounds__(64 * WM* WN, 3) void igemm_kernel(IgemmArgs a) {
     }
   }
 
-  igemm_epilogue<MB, NB, WM, WN>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi, txi, oz0, oy0,
-                                 ox0, 1.0f);
+  // (the checked epilogue only: a whole-tile copy beside it costs this kernel's registers)
+  igemm_epilogue_t<MB, NB, WM, WN, false, false>(a, acc, lds, wm, wn, slot, row, nbk0, b, tzi, tyi,
+                                                 txi, oz0, oy0, ox0, 1.0f);
 }
 
 
