@@ -663,6 +663,24 @@ def kernel_table(classes: dict, steps: int, traffic: bool = True) -> tuple[dict,
                 # outputs in place of 8 x 27 taps
                 entry["frac_fp16_mfma_issued"] = round(
                     entry["tflops"] * SPLIT_PRODUCTS * 64 / 216 / PEAK_FP16_MFMA_TFLOPS, 4)
+            elif name.startswith("tconv3d_x3"):
+                # issued MFMA work of the pointwise GEMM: 3 fp16 products per term (1 bf16
+                # product in the bf16 variant; bf16 and fp16 share the dense peak); the
+                # kernel is bound by its output stream, so its HBM rate goes beside it
+                if name.endswith("_bf16"):
+                    entry["frac_bf16_mfma_issued"] = round(
+                        entry["tflops"] / PEAK_FP16_MFMA_TFLOPS, 4)
+                else:
+                    entry["frac_fp16_mfma_issued"] = round(
+                        entry["tflops"] * SPLIT_PRODUCTS / PEAK_FP16_MFMA_TFLOPS, 4)
+                if c["bytes"]:
+                    entry["gbs"] = round(c["bytes"] / (c["ms"] * 1e-3) / 1e9, 1)
+                    entry["frac_hbm"] = round(entry["gbs"] / PEAK_HBM_GBS, 4)
+            elif name.startswith("conv1x1_head"):
+                # VALU dot products over a voxel's channels: bound by the HBM stream of the
+                # input rows and outputs, so priced against HBM
+                entry["gbs"] = round(c["bytes"] / (c["ms"] * 1e-3) / 1e9, 1)
+                entry["frac_hbm"] = round(entry["gbs"] / PEAK_HBM_GBS, 4)
             else:
                 entry["frac_fp32_mfma"] = round(entry["tflops"] / PEAK_FP32_MFMA_TFLOPS, 4)
         elif c["bytes"]:
@@ -675,7 +693,7 @@ def kernel_table(classes: dict, steps: int, traffic: bool = True) -> tuple[dict,
         achieved = d["flops"] / (d["ms"] * 1e-3) / 1e12
         # the split kernels run on fp16 MFMA: their algorithmic (float32-product) rate is
         # priced against the dense fp16 peak, the issued rate is reported beside it
-        fp16 = dominant.startswith(("conv3d_x3", "conv3d_wino"))
+        fp16 = dominant.startswith(("conv3d_x3", "conv3d_wino", "tconv3d_x3"))
         peak = PEAK_FP16_MFMA_TFLOPS if fp16 else PEAK_FP32_MFMA_TFLOPS
         roofline = {"kernel": dominant, "bound": "mfma", "achieved": round(achieved, 2),
                     "peak": peak, "unit": "TFLOP/s", "frac": round(achieved / peak, 4),
