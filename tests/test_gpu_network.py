@@ -163,6 +163,29 @@ def test_conv_route_matches_oracle(device, monkeypatch, name, algo):
     assert rel_l2(got, ref) <= 1e-5, msg
 
 
+def test_persistent_winograd_forward_is_bit_identical(device, monkeypatch):
+    """The persistent Winograd kernel runs the layers with at least four boxes a CU (here
+    the 64^3 and 32^3 stages at batch 4) with the one-box kernel's arithmetic, including
+    what the plain kernel tests do not reach: pending InstanceNorm + LeakyReLU on load
+    (interior and border boxes, and the transposed convolution's half without one), the
+    concatenated decoder input and the InstanceNorm partials of the epilogue.  The whole
+    forward is therefore bit-identical with the persistent kernel switched off."""
+    spec = liver_spec()
+    weights = random_weights(spec, seed=7, random_affine=True)
+    x = np.random.default_rng(11).standard_normal((4, 64, 64, 64, 1)).astype(np.float32)
+    print("persistent vs one-box Winograd: liver network 64^3 batch 4", flush=True)
+    outs = {}
+    for flag in ("1", "0"):
+        monkeypatch.setenv("NNX_WINO_PERSISTENT", flag)
+        net = build_network(spec, precision="fp32-split")
+        net.load_weights(weights)
+        outs[flag] = net(torch.from_numpy(x).to(device)).cpu().numpy()
+        net.close()
+    assert np.isfinite(outs["1"]).all()
+    assert np.array_equal(outs["1"].view(np.uint32), outs["0"].view(np.uint32)), \
+        f"{int((outs['1'] != outs['0']).sum())} logits differ"
+
+
 def test_forward_rejects_bad_input(device):
     from nnunet_mlx.errors import ContractError
 
