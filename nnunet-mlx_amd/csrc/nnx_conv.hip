@@ -2327,6 +2327,10 @@ ConvGeom make_conv_geom(int batch, const int* in_size, const int* ksize, const i
     g.out[i] = (in_size[i] + 2 * g.p[i] - ksize[i]) / stride[i] + 1;
     require(g.out[i] >= 1, "convolution output would be empty");
   }
+  // the kernels hold a voxel's offset inside its batch item in 32 bits (the output has no
+  // more voxels than the input)
+  require((int64_t)in_size[0] * in_size[1] * in_size[2] < (1LL << 31),
+          "convolution input exceeds 2^31 voxels per batch item");
   return g;
 }
 

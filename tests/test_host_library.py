@@ -59,6 +59,30 @@ def test_error_path_without_gpu():
         _native.check(rc)
 
 
+def test_convolutions_refuse_items_beyond_32_bit_voxel_offsets():
+    """The convolution kernels hold a voxel's offset inside its batch item in 32 bits: a
+    batch item of 2^31 voxels or more is refused by every convolution entry point before
+    any device call (so on a CPU host too); one voxel fewer passes that check (and fails
+    the next one, the null buffers)."""
+    from nnunet_mlx import _native
+
+    lib = _native.load()
+    k3, s1 = _native.ints((3, 3, 3)), _native.ints((1, 1, 1))
+    calls = {
+        "split": lambda size: lib.nnx_conv3d_split(None, 16, None, 0, None, 1.0, None, None, 1,
+                                                   _native.ints(size), 32, k3, s1, None),
+        "winograd": lambda size: lib.nnx_conv3d_winograd(None, 16, None, 0, None, 1.0, None, None,
+                                                         1, _native.ints(size), 32, None),
+        "igemm": lambda size: lib.nnx_conv3d_igemm(None, 16, None, 0, None, None, None, 1,
+                                                   _native.ints(size), 32, k3, s1, None),
+    }
+    for name, call in calls.items():
+        assert call((2048, 1024, 1024)) == _native.NNX_ERR_INVALID, name
+        assert b"2^31 voxels" in lib.nnx_last_error(), name
+        assert call((2047, 1024, 1024)) == _native.NNX_ERR_INVALID, name
+        assert b"2^31 voxels" not in lib.nnx_last_error(), name
+
+
 def test_split_weight_scale_rules():
     """The split-fp16 weight scale is the power of two that puts max |w| in [2^14, 2^15)."""
     from nnunet_mlx import _native
