@@ -77,27 +77,29 @@ const char* nnx_version(void);
 typedef struct nnx_spec {
   int arch;              /* NNX_ARCH_PLAIN or NNX_ARCH_RESIDUAL */
   int spatial_dims;      /* 3 (2-D networks are rejected) */
-  int input_channels;
-  int num_classes;
-  int n_stages;
-  const int* features;      /* n_stages */
-  const int* kernel_sizes;  /* n_stages * 3, odd */
-  const int* strides;       /* n_stages * 3 */
-  const int* encoder_convs; /* n_stages: convs per stage (plain) or blocks per stage (residual) */
-  const int* decoder_convs; /* n_stages - 1 */
+  int input_channels;     /* 1..1024 */
+  int num_classes;        /* 1..1024 */
+  int n_stages;           /* 2..16 */
+  const int* features;      /* n_stages, each 1..1024 (the InstanceNorm's channel limit) */
+  const int* kernel_sizes;  /* n_stages * 3, odd, 1..15 */
+  const int* strides;       /* n_stages * 3, 1..16 */
+  const int* encoder_convs; /* n_stages: convs per stage (plain) or blocks per stage (residual),
+                               1..64 */
+  const int* decoder_convs; /* n_stages - 1, 1..64 */
   int conv_bias;
   int norm_affine;
   float norm_eps;
   float leaky_slope;
-  int stem_channels; /* residual only; 0 means features[0] */
-  const int* bottleneck_channels; /* residual only: n_stages entries for BottleneckD, or NULL
-                                     for BasicBlockD */
+  int stem_channels; /* residual only; 0 means features[0]; at most 1024 */
+  const int* bottleneck_channels; /* residual only: n_stages entries (1..1024) for
+                                     BottleneckD, or NULL for BasicBlockD */
   int precision;     /* NNX_PRECISION_FP32, _FP32_SPLIT, _BF16 or _BF16_MIXED */
 } nnx_spec;
 
 typedef struct nnx_model nnx_model;
 
-/* Build the layer graph of a network; no weights yet.
+/* Build the layer graph of a network; no weights yet.  A field outside the ranges above
+ * returns NNX_ERR_INVALID.
  * Replaces PlainConvUNet/ResidualEncoderUNet __init__ (src/nnunet_mlx/model/network.py:422-451,664-699). */
 int nnx_model_create(const nnx_spec* spec, nnx_model** out);
 

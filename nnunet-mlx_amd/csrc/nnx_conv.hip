@@ -2504,14 +2504,15 @@ void conv3d_igemm(const float* x1, int c1, const float* x2, int c2, const float*
 
 // ---- split-fp16 ("x3") implicit GEMM ----------------------------------------------
 
-float split_weight_scale(float max_abs) {
-  require(std::isfinite(max_abs) && max_abs >= 0.f, "weight magnitude must be finite");
-  if (max_abs == 0.f) return 1.0f;
+float split_weight_scale(double max_abs) {
+  require(std::isfinite(max_abs) && max_abs >= 0.0, "weight magnitude must be finite");
+  if (max_abs == 0.0) return 1.0f;
   // the power of two that brings max |w| into [2^14, 2^15): high halves stay below the
-  // fp16 maximum (65504) and low halves of all but tiny weights stay normal
+  // fp16 maximum (65504) and low halves of all but tiny weights stay normal.  Below 2^-113
+  // the scale stops at 2^127, the largest float power of two (max |w| then lands lower).
   int e;
   std::frexp(max_abs, &e);  // max_abs = m * 2^e, m in [0.5, 1)
-  return std::ldexp(1.0f, 15 - e);
+  return std::ldexp(1.0f, std::min(15 - e, 127));
 }
 
 int conv_x3_groups(const int* ksize) { return (ksize[0] * ksize[1] * ksize[2] + 3) / 4; }

@@ -135,7 +135,7 @@ int conv_stats_tiles(const ConvGeom& g, int cout, int c1, int c2);
 // products per term, float32 accumulation.  `scale` (a power of two from
 // split_weight_scale) multiplies the weights before the split and is undone in the
 // epilogue.  Activations must stay below the fp16 maximum (65504) in magnitude.
-float split_weight_scale(float max_abs);
+float split_weight_scale(double max_abs);
 int64_t conv_x3_packed_bytes(int cout, const int* ksize, int c1, int c2);
 // Operand arithmetic of the split kernels: kArithSplit3 = fp16 hi/lo halves, three
 // products (float32 class); kArithBf16 = bf16 operands (round to nearest even), one

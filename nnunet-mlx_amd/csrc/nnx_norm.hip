@@ -505,7 +505,11 @@ StatsLayout stats_layout(int64_t spatial, int channels) {
 }  // namespace
 
 size_t instnorm_workspace_bytes(int batch, int64_t spatial, int channels) {
+  // the limits instnorm_params enforces; they also keep the byte count below 2^61
+  require(batch >= 1 && spatial >= 1 && channels >= 1, "instance normalisation needs a non-empty tensor");
+  require(batch <= 65535, "instance normalisation batch too large");
   const StatsLayout l = stats_layout(spatial, channels);
+  require(l.nchunks < (1LL << 31), "instance normalisation tensor too large");
   const size_t partial = (size_t)batch * l.nchunks * channels * sizeof(float2);
   const size_t params = (size_t)batch * channels * sizeof(float4);
   return ((partial + 255) / 256) * 256 + params;

@@ -681,7 +681,8 @@ int nonzero_mask_filled(const float* x, int channels, const int64_t* size, const
   require(x && size && start && extent && mask && work, "mask pointers must not be null");
   require(channels >= 1, "mask needs at least one channel");
   for (int a = 0; a < 3; ++a)
-    require(extent[a] >= 1 && start[a] >= 0 && start[a] + extent[a] <= size[a],
+    require(extent[a] >= 1 && start[a] >= 0 && start[a] <= size[a] &&
+                extent[a] <= size[a] - start[a],
             "mask box outside the volume");
   const int64_t total = extent[0] * extent[1] * extent[2];
   int* flag = static_cast<int*>(work);
@@ -718,7 +719,8 @@ void zscore_stats(const float* x, int channels, const int64_t* size, int channel
   require(x && size && start && extent && stats && work, "z-score pointers must not be null");
   require(channel >= 0 && channel < channels, "z-score channel out of range");
   for (int a = 0; a < 3; ++a)
-    require(extent[a] >= 1 && start[a] >= 0 && start[a] + extent[a] <= size[a],
+    require(extent[a] >= 1 && start[a] >= 0 && start[a] <= size[a] &&
+                extent[a] <= size[a] - start[a],
             "z-score box outside the volume");
   const int64_t total = extent[0] * extent[1] * extent[2];
   const float* xc = x + (int64_t)channel * size[0] * size[1] * size[2];
@@ -741,7 +743,8 @@ void box_minmax(const float* x, int channels, const int64_t* size, int channel,
   require(x && size && start && extent && minmax && work, "extrema pointers must not be null");
   require(channel >= 0 && channel < channels, "extrema channel out of range");
   for (int a = 0; a < 3; ++a)
-    require(extent[a] >= 1 && start[a] >= 0 && start[a] + extent[a] <= size[a],
+    require(extent[a] >= 1 && start[a] >= 0 && start[a] <= size[a] &&
+                extent[a] <= size[a] - start[a],
             "extrema box outside the volume");
   const int64_t total = extent[0] * extent[1] * extent[2];
   const float* xc = x + (int64_t)channel * size[0] * size[1] * size[2];
@@ -779,7 +782,8 @@ void crop_normalize_masked(const float* x, int channels, const int64_t* size,
   }
   for (int k = 0; k < 3; ++k) {
     const int64_t n = size[transpose[k]];
-    require(out_size[k] >= 1 && start[k] >= 0 && start[k] + out_size[k] <= n,
+    require(out_size[k] >= 1 && start[k] >= 0 && start[k] <= n &&
+                out_size[k] <= n - start[k],
             "crop window outside the volume");
   }
   ChannelNorms cn{};

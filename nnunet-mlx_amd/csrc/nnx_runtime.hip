@@ -773,10 +773,20 @@ struct ModelForward {
   }
 };
 
+// a * b, refused when the product leaves [0, 2^62) (every buffer size below is one)
+int64_t sw_product(int64_t a, int64_t b, const char* what) {
+  int64_t r = 0;
+  require(!__builtin_mul_overflow(a, b, &r) && r >= 0 && r < (int64_t(1) << 62),
+          std::string("sliding-window ") + what + " too large");
+  return r;
+}
+
 void validate_sw(const nnx_sw_config* c) {
   require(c != nullptr, "sliding-window config must not be null");
   require(c->channels >= 1, "sliding-window input needs at least one channel");
   require(c->num_classes >= 1, "sliding-window inference requires at least one output channel");
+  require(c->channels <= 65535 && c->num_classes <= 65535,
+          "sliding-window channels and classes are limited to 65535");
   require(c->accumulation == NNX_ACCUM_F32 || c->accumulation == NNX_ACCUM_NNUNET_F16,
           "unsupported sliding-window accumulation");
   require(c->ntiles >= 1 && c->tile_offsets, "sliding window needs at least one tile");
@@ -785,13 +795,25 @@ void validate_sw(const nnx_sw_config* c) {
   require(c->tiles_per_batch >= 1, "tiles_per_batch must be positive");
   for (int i = 0; i < 3; ++i) {
     require(c->size[i] >= 1 && c->patch[i] >= 1, "invalid volume or patch size");
+    require(c->padded[i] < (int64_t(1) << 31), "volume dimensions are limited to 2^31 - 1");
     require(c->pad_before[i] >= 0 && c->padded[i] >= c->size[i] + c->pad_before[i],
             "invalid minimum padding");
     require(c->padded[i] >= c->patch[i], "padded image dimension is smaller than the patch");
   }
+  // every buffer the run sizes: accumulators (padded volume x classes), fold total (crop x
+  // classes), a batch of views in and out (patch x channels or classes)
+  const int64_t esz = c->accumulation == NNX_ACCUM_NNUNET_F16 ? 2 : 4;
+  const int64_t padded_vox = sw_product(sw_product(c->padded[0], c->padded[1], "volume"),
+                                        c->padded[2], "volume");
+  sw_product(sw_product(padded_vox, c->num_classes, "volume"), esz, "volume");
+  const int64_t patch_vox =
+      sw_product(sw_product(c->patch[0], c->patch[1], "patch"), c->patch[2], "patch");
+  const int64_t views = sw_product(std::min(c->tiles_per_batch, c->ntiles), c->nviews, "batch");
+  sw_product(sw_product(views, patch_vox, "batch"),
+             (int64_t)std::max(c->channels, c->num_classes) * 4, "batch");
   for (int t = 0; t < c->ntiles; ++t)
     for (int i = 0; i < 3; ++i) {
-      const int o = c->tile_offsets[t * 3 + i];
+      const int64_t o = c->tile_offsets[t * 3 + i];
       require(o >= 0 && o + c->patch[i] <= c->padded[i], "tile offset outside the padded volume");
     }
 }
@@ -873,9 +895,17 @@ int nnx_model_create(const nnx_spec* spec, nnx_model** out) {
                 spec->precision == NNX_PRECISION_BF16 ||
                 spec->precision == NNX_PRECISION_BF16_MIXED,
             "unsupported precision");
+    // upper bounds: no network that could run exceeds them (every normalised layer is
+    // limited to 1024 channels), and they keep the graph and its parameter sizes small
+    constexpr int kMaxWidth = 1024, kMaxStages = 16, kMaxKernel = 15, kMaxStride = 16,
+                  kMaxConvs = 64;
     require(spec->input_channels >= 1 && spec->num_classes >= 1,
             "network needs input channels and at least one output");
+    require(spec->input_channels <= kMaxWidth && spec->num_classes <= kMaxWidth,
+            "input channels and classes are limited to 1024");
     require(spec->n_stages >= 2, "network needs at least two stages");
+    require(spec->n_stages <= kMaxStages, "network has more than 16 stages");
+    require(spec->stem_channels <= kMaxWidth, "stem channels are limited to 1024");
     require(spec->features && spec->kernel_sizes && spec->strides && spec->encoder_convs &&
                 spec->decoder_convs,
             "spec arrays must not be null");
@@ -895,12 +925,18 @@ int nnx_model_create(const nnx_spec* spec, nnx_model** out) {
     m->dec_count.assign(spec->decoder_convs, spec->decoder_convs + S - 1);
     if (spec->arch == NNX_ARCH_RESIDUAL && spec->bottleneck_channels)
       m->bottleneck.assign(spec->bottleneck_channels, spec->bottleneck_channels + S);
-    for (int v : m->features) require(v >= 1, "features must be positive");
-    for (int v : m->ksz) require(v >= 1 && v % 2 == 1, "only positive odd convolution kernels are supported");
-    for (int v : m->strides) require(v >= 1, "strides must be positive");
-    for (int v : m->enc_count) require(v >= 1, "encoder counts must be positive");
-    for (int v : m->dec_count) require(v >= 1, "decoder counts must be positive");
-    for (int v : m->bottleneck) require(v >= 1, "bottleneck channels must be positive");
+    for (int v : m->features)
+      require(v >= 1 && v <= kMaxWidth, "features must lie in 1..1024");
+    for (int v : m->ksz)
+      require(v >= 1 && v % 2 == 1 && v <= kMaxKernel,
+              "only odd convolution kernels of 1..15 are supported");
+    for (int v : m->strides) require(v >= 1 && v <= kMaxStride, "strides must lie in 1..16");
+    for (int v : m->enc_count)
+      require(v >= 1 && v <= kMaxConvs, "encoder counts must lie in 1..64");
+    for (int v : m->dec_count)
+      require(v >= 1 && v <= kMaxConvs, "decoder counts must lie in 1..64");
+    for (int v : m->bottleneck)
+      require(v >= 1 && v <= kMaxWidth, "bottleneck channels must lie in 1..1024");
     m->conv_bias = spec->conv_bias != 0;
     m->norm_affine = spec->norm_affine != 0;
     m->eps = spec->norm_eps;
@@ -1034,6 +1070,7 @@ int nnx_sw_predict(nnx_model* const* folds, int nfolds, const nnx_sw_config* con
                    const float* d_volume, void* d_logits, uint16_t* d_labels, void* stream) {
   return guarded([&] {
     require(folds != nullptr && nfolds >= 1, "fold inference requires at least one model");
+    validate_sw(config);
     std::vector<nnx_forward_fn> fns(nfolds, &ModelForward::call);
     std::vector<void*> users(nfolds);
     for (int f = 0; f < nfolds; ++f) {
@@ -1158,7 +1195,7 @@ int nnx_conv3d_split(const float* d_x1, int c1, const float* d_x2, int c2, const
 }
 
 float nnx_winograd_weight_scale(float max_abs) {
-  if (!std::isfinite(max_abs) || max_abs < 0.f) return 0.f;
+  if (!(max_abs >= 0.f) || !std::isfinite(max_abs)) return 0.f;
   return wino_weight_scale(max_abs);
 }
 

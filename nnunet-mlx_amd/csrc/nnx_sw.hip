@@ -237,9 +237,9 @@ void sw_gather_flip(const float* vol, int channels, const int64_t* size, const i
   require(vol && out, "gather pointers must not be null");
   require(channels >= 1, "gather needs at least one channel");
   const Flips f = make_flips(flips, nviews);
-  const int64_t n = (int64_t)patch[0] * patch[1] * patch[2] * nviews;
   require(patch[1] <= 65535 && patch[0] <= 65535, "patch rows exceed the launch grid");
-  ProfScope prof("sw_gather_flip", 0.0, 4.0 * (double)n / nviews * channels * (1 + nviews), st);
+  const double pvox = (double)patch[0] * patch[1] * patch[2];
+  ProfScope prof("sw_gather_flip", 0.0, 4.0 * pvox * channels * (1 + nviews), st);
   // runs of 4 floats where every view's row starts 16-byte aligned, else single floats
   const int64_t row = (int64_t)patch[2] * channels;
   const bool vec = row % 4 == 0 && reinterpret_cast<uintptr_t>(out) % 16 == 0;
@@ -263,7 +263,8 @@ void sw_accumulate(const float* pred, int nviews, const int* flips, int k, const
   require(pred && gaussian && acc && norm, "accumulate pointers must not be null");
   require(k >= 1, "accumulate needs at least one class");
   for (int i = 0; i < 3; ++i)
-    require(offset[i] >= 0 && offset[i] + patch[i] <= padded[i], "tile outside the padded volume");
+    require(offset[i] >= 0 && (int64_t)offset[i] + patch[i] <= padded[i],
+            "tile outside the padded volume");
   const Flips f = make_flips(flips, nviews);
   const int64_t n = (int64_t)patch[0] * patch[1] * patch[2];
   require(patch[1] <= 65535 && patch[0] <= 65535, "patch rows exceed the launch grid");
@@ -289,7 +290,9 @@ void sw_fold_add(const void* acc, const void* norm, int k, const int64_t* padded
                  void* total, hipStream_t st) {
   require(acc && norm && total, "fold pointers must not be null");
   for (int i = 0; i < 3; ++i)
-    require(crop_lo[i] >= 0 && crop_lo[i] + crop_size[i] <= padded[i], "crop outside the volume");
+    require(crop_lo[i] >= 0 && crop_size[i] >= 0 && crop_lo[i] <= padded[i] &&
+                crop_size[i] <= padded[i] - crop_lo[i],
+            "crop outside the volume");
   const int64_t n = crop_size[0] * crop_size[1] * crop_size[2];
   const double esz = accum == NNX_ACCUM_NNUNET_F16 ? 2.0 : 4.0;
   ProfScope prof("sw_fold_add", 0.0, (double)n * (k * esz + esz + k * esz * (first ? 1 : 2)), st);

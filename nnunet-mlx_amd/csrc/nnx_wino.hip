@@ -997,8 +997,11 @@ int conv_wino_stats_tiles(const ConvGeom& g) {
 }
 
 float wino_weight_scale(float max_abs) {
-  // |U| <= (1.5)^3 max |w|: the scale keeps every split high half below 2^15
-  return split_weight_scale(3.375f * max_abs);
+  // |U| <= (1.5)^3 max |w|: the scale keeps every split high half below 2^15 (the bound in
+  // float32, or in float64 where the float32 product would overflow)
+  require(std::isfinite(max_abs) && max_abs >= 0.f, "weight magnitude must be finite");
+  const float bound = 3.375f * max_abs;
+  return split_weight_scale(std::isfinite(bound) ? (double)bound : 3.375 * (double)max_abs);
 }
 
 int64_t conv_wino_packed_bytes(int cout, int c1, int c2) {
