@@ -116,7 +116,10 @@ int nnx_model_load_param(nnx_model* model, const char* name, const float* host,
                          const int64_t* shape, int ndim);
 
 /* Check that every parameter was loaded exactly once and is finite, repack weights into
- * the MFMA fragment layouts and upload them.  Required before nnx_forward. */
+ * the MFMA fragment layouts and upload them.  Required before nnx_forward.  A call that
+ * fails for missing parameters can be repeated after loading them; one that fails later
+ * (a device error while uploading or packing) leaves the model unusable: every later call
+ * fails with NNX_ERR_INVALID, and the model is destroyed and rebuilt. */
 int nnx_model_finalize(nnx_model* model);
 
 /* Let `model` use the activation workspace of `owner` (fold ensembles keep every fold's

@@ -213,6 +213,9 @@ struct nnx_model {
   std::vector<std::vector<nnx::ConvNorm>> dec;
   std::vector<nnx::SegHead> seg;
   bool finalized = false;
+  // set while nnx_model_finalize uploads (it releases host copies as it goes): a call that
+  // failed part-way leaves the model unusable
+  bool finalize_failed = false;
   std::shared_ptr<nnx::Workspace> ws;
 };
 
@@ -1003,6 +1006,9 @@ int nnx_model_finalize(nnx_model* model) {
     for (const Param& p : model->params)
       if (!p.loaded) missing += (missing.empty() ? "" : ", ") + p.name;
     if (!missing.empty()) fail(NNX_ERR_STATE, "missing parameters: " + missing);
+    require(!model->finalize_failed,
+            "an earlier nnx_model_finalize failed part-way; destroy and rebuild the model");
+    model->finalize_failed = true;
     for (Param& p : model->params) {
       for (float v : p.host) p.max_abs = std::max(p.max_abs, std::fabs(v));
       p.dev.ensure((size_t)p.numel() * sizeof(float));
@@ -1040,6 +1046,7 @@ int nnx_model_finalize(nnx_model* model) {
       tconv_pack_weight(pdev(model, u.pw), u.cout, u.k, u.cin, u.packed.as<float>(), st);
     }
     hip_check(hipStreamSynchronize(st), "weight packing");
+    model->finalize_failed = false;
     model->finalized = true;
   });
 }

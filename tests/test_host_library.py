@@ -250,3 +250,49 @@ def test_box_checks_do_not_wrap():
     assert lib.nnx_sw_fold_add(fake, fake, 3, size, crop_lo, huge, _native.NNX_ACCUM_F32, 1, fake,
                                None) == _native.NNX_ERR_INVALID
     assert b"crop outside the volume" in lib.nnx_last_error()
+
+
+def test_finalize_failed_part_way_leaves_the_model_refusing_retries():
+    """A finalize that fails for missing parameters can be repeated; one that fails while
+    uploading (here: no device on a CPU host, or any device error) releases host copies as
+    it goes, so a retry is refused instead of reading the released copies."""
+    import ctypes
+
+    import numpy as np
+
+    from nnunet_mlx import _native
+
+    lib = _native.load()
+    keep = []
+    s = _native.NnxSpec()
+    s.arch, s.spatial_dims, s.input_channels, s.num_classes, s.n_stages = (
+        _native.NNX_ARCH_PLAIN, 3, 1, 2, 2)
+    for name, values in dict(features=[4, 8], kernel_sizes=[3] * 6, strides=[1, 1, 1, 2, 2, 2],
+                             encoder_convs=[1, 1], decoder_convs=[1]).items():
+        array = _native.ints(values)
+        keep.append(array)
+        setattr(s, name, ctypes.cast(array, _native.c_int_p))
+    s.conv_bias, s.norm_affine, s.norm_eps, s.leaky_slope = 1, 1, 1e-5, 0.01
+    s.precision = _native.NNX_PRECISION_FP32_SPLIT
+    handle = ctypes.c_void_p()
+    _native.check(lib.nnx_model_create(ctypes.byref(s), ctypes.byref(handle)))
+    try:
+        count = ctypes.c_int()
+        _native.check(lib.nnx_model_param_count(handle, ctypes.byref(count)))
+        assert lib.nnx_model_finalize(handle) == _native.NNX_ERR_STATE  # nothing loaded yet
+        for i in range(count.value):
+            name, ndim = ctypes.c_char_p(), ctypes.c_int()
+            shape = (ctypes.c_int64 * 5)()
+            _native.check(lib.nnx_model_param_info(handle, i, ctypes.byref(name), ctypes.byref(ndim),
+                                                   shape))
+            dims = tuple(shape[:ndim.value])
+            data = np.full(dims, 0.5, dtype=np.float32)
+            _native.check(lib.nnx_model_load_param(handle, name.value, data.ctypes.data,
+                                                   _native.i64s(dims), ndim.value))
+        first = lib.nnx_model_finalize(handle)
+        if first == _native.NNX_OK:
+            pytest.skip("a device is present: the upload did not fail")
+        assert lib.nnx_model_finalize(handle) == _native.NNX_ERR_INVALID
+        assert b"failed part-way" in lib.nnx_last_error()
+    finally:
+        lib.nnx_model_destroy(handle)
