@@ -85,9 +85,35 @@ def test_conv3d_igemm_matches_float64(lib, case):
     assert np.abs(got - ref).max() <= 1e-4 * max(1.0, np.abs(ref).max()), msg
 
 
+def _random_conv_cases(seed, n):
+    """Seeded shapes for the sweeps below: ragged channel counts, per-axis kernels of 1 or 3
+    and strides of 1 or 2, volumes from one voxel to a few tiles."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        kernel = tuple(int(k) for k in rng.choice([1, 3], 3, p=[0.25, 0.75]))
+        stride = tuple(int(t) for t in rng.choice([1, 2], 3))
+        size = tuple(int(v) for v in rng.integers(1, 17, 3))
+        c2 = int(rng.choice([0, 0, int(rng.integers(1, 25))]))
+        cases.append((int(rng.integers(1, 4)), size, int(rng.integers(1, 49)), c2,
+                      int(rng.integers(1, 73)), kernel, stride))
+    return cases
+
+
 @pytest.mark.parametrize("case", CONV_CASES, ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}-k{c[5]}-s{c[6]}")
 def test_conv3d_split_matches_float64(lib, case):
     """Split-fp16 products (hi*hi + hi*lo + lo*hi) hold the same float32 bar as the fp32 kernel."""
+    _check_split_conv(lib, case)
+
+
+@pytest.mark.parametrize("case", _random_conv_cases(2026, 12),
+                         ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}-k{c[5]}-s{c[6]}")
+def test_conv3d_split_random_shapes_match_float64(lib, case):
+    """The same bar over a seeded sweep of shapes no hand-picked case above covers."""
+    _check_split_conv(lib, case)
+
+
+def _check_split_conv(lib, case):
     batch, size, c1, c2, cout, kernel, stride = case
     print(f"split conv case {case}", flush=True)
     rng = np.random.default_rng((hash(case) + 7) % 2**32)
@@ -138,10 +164,30 @@ WINOGRAD_CASES = [
 ]
 
 
+def _random_winograd_cases(seed, n):
+    """Seeded Winograd shapes: 16-channel input blocks on one or two inputs, 32-column output
+    blocks, volumes from one voxel to several ragged 4 x 8 x 8 boxes."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 4)), tuple(int(v) for v in rng.integers(1, 21, 3)),
+             16 * int(rng.integers(1, 5)), 16 * int(rng.choice([0, 0, 1, 2])),
+             32 * int(rng.integers(1, 4))) for _ in range(n)]
+
+
 @pytest.mark.parametrize("case", WINOGRAD_CASES, ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}")
 def test_conv3d_winograd_matches_float64(lib, case):
     """Winograd F(2x2x2, 3x3x3) with split-fp16 products holds the float32 bar of the
     direct kernels against float64 (activations up to ~30, weights spanning three decades)."""
+    _check_winograd_conv(lib, case)
+
+
+@pytest.mark.parametrize("case", _random_winograd_cases(2027, 10),
+                         ids=lambda c: f"b{c[0]}-{c[1]}-c{c[2]}+{c[3]}-o{c[4]}")
+def test_conv3d_winograd_random_shapes_match_float64(lib, case):
+    """The same bar over a seeded sweep of Winograd shapes."""
+    _check_winograd_conv(lib, case)
+
+
+def _check_winograd_conv(lib, case):
     batch, size, c1, c2, cout = case
     print(f"winograd conv case {case}", flush=True)
     rng = np.random.default_rng((hash(case) + 11) % 2**32)
