@@ -487,6 +487,25 @@ def test_tconv3d_gemm_matches_float64(lib, case):
 ], ids=str)
 def test_tconv3d_split_matches_float64(lib, case):
     """Split-fp16 products hold the float32 bar (rel-L2 <= 1e-5) of the transposed conv."""
+    _check_split_tconv(lib, case)
+
+
+def _random_tconv_cases(seed, n):
+    """Seeded transposed-convolution shapes: kernel = stride of 1 or 2 per axis, ragged
+    input and output channel counts (scalar stores where C_out % 4 != 0)."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 4)), tuple(int(v) for v in rng.integers(1, 13, 3)),
+             int(rng.integers(1, 97)), int(rng.integers(1, 65)),
+             tuple(int(k) for k in rng.integers(1, 3, 3))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("case", _random_tconv_cases(2028, 10), ids=str)
+def test_tconv3d_split_random_shapes_match_float64(lib, case):
+    """The same bar over a seeded sweep of transposed-convolution shapes."""
+    _check_split_tconv(lib, case)
+
+
+def _check_split_tconv(lib, case):
     batch, size, cin, cout, k = case
     print(f"split tconv case {case}", flush=True)
     rng = np.random.default_rng(4)
