@@ -405,7 +405,17 @@ NORM_CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", NORM_CASES, ids=str)
+def _random_norm_cases(seed, n):
+    """Seeded InstanceNorm shapes: channel counts with and without a 4-channel vector width,
+    volumes from one voxel up, every combination of the optional parts."""
+    rng = np.random.default_rng(seed)
+    return [(int(rng.integers(1, 5)), tuple(int(v) for v in rng.integers(1, 24, 3)),
+             int(rng.choice([int(rng.integers(1, 13)), 4 * int(rng.integers(1, 81))])),
+             bool(rng.integers(0, 2)), bool(rng.integers(0, 2)), bool(rng.integers(0, 2)),
+             bool(rng.integers(0, 2))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("case", NORM_CASES + _random_norm_cases(2029, 12), ids=str)
 def test_instnorm_lrelu_matches_float64(lib, case):
     batch, spatial, c, affine, use_bias, act, use_res = case
     print(f"norm case {case}", flush=True)
@@ -688,6 +698,36 @@ def test_gather_flip_exact(lib, case):
     sl = tuple(slice(o, o + p) for o, p in zip(offset, patch))
     tile = np.moveaxis(padded[(slice(None),) + sl], 0, -1)
     for v, mask in enumerate(FLIPS_3AX):
+        np.testing.assert_array_equal(got[v], _unflip(tile, mask))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_gather_flip_random_geometry_exact(lib, seed):
+    """Seeded volumes, paddings, tile offsets, patches and view sets: every gathered view is
+    the mirrored tile of the zero-padded volume, bit for bit."""
+    rng = np.random.default_rng(300 + seed)
+    channels = int(rng.integers(1, 5))
+    size = tuple(int(v) for v in rng.integers(1, 16, 3))
+    patch = tuple(int(v) for v in rng.integers(1, 20, 3))
+    before = tuple(int(v) for v in rng.integers(0, 4, 3))
+    padded = [max(s + b + int(rng.integers(0, 4)), p) for s, b, p in zip(size, before, patch)]
+    offset = tuple(int(rng.integers(0, q - p + 1)) for q, p in zip(padded, patch))
+    flips = [int(f) for f in rng.choice(8, int(rng.integers(1, 9)), replace=False)]
+    print(f"gather seed {seed}: c {channels} size {size} patch {patch} before {before} "
+          f"padded {padded} offset {offset} flips {flips}", flush=True)
+    vol = rng.standard_normal((channels, *size)).astype(np.float32)
+    after = [q - s - b for q, s, b in zip(padded, size, before)]
+    full = np.pad(vol, [(0, 0)] + [(b, a) for b, a in zip(before, after)])
+    n = len(flips) * int(np.prod(patch)) * channels
+    buf = torch.full((n,), float("nan"), dtype=torch.float32, device="cuda")
+    dvol = dev(vol)
+    _native.check(lib.nnx_sw_gather_flip(
+        dvol.data_ptr(), channels, _native.i64s(size), _native.ints(before), _native.ints(offset),
+        _native.ints(patch), _native.ints(flips), len(flips), buf.data_ptr(), stream()))
+    got = host(buf).reshape(len(flips), *patch, channels)
+    sl = tuple(slice(o, o + p) for o, p in zip(offset, patch))
+    tile = np.moveaxis(full[(slice(None),) + sl], 0, -1)
+    for v, mask in enumerate(flips):
         np.testing.assert_array_equal(got[v], _unflip(tile, mask))
 
 
