@@ -790,6 +790,78 @@ def test_accumulate_fold_finalize_bitwise(lib, fp16):
     assert int(host(invalid)[0]) == int((~finite).sum())
 
 
+@pytest.mark.parametrize("fp16", [False, True])
+@pytest.mark.parametrize("seed", range(6))
+def test_accumulate_fold_finalize_random_geometry_bitwise(lib, seed, fp16):
+    """Seeded classes, patches, padded volumes, view sets, tile offsets, crops and fold counts:
+    the accumulators, the fold total, the averaged logits and the labels equal the same
+    float32 (or float16) operations in numpy, bit for bit (uncovered voxels give 0/0 and the
+    invalid label)."""
+    rng = np.random.default_rng(500 + seed)
+    K = int(rng.integers(1, 6))
+    patch = tuple(int(v) for v in rng.integers(1, 10, 3))
+    padded = tuple(p + int(rng.integers(0, 6)) for p in patch)
+    flips = [int(f) for f in rng.choice(8, int(rng.integers(1, 9)), replace=False)]
+    offsets = [tuple(int(rng.integers(0, q - p + 1)) for q, p in zip(padded, patch))
+               for _ in range(int(rng.integers(1, 6)))]
+    crop_lo = tuple(int(rng.integers(0, q)) for q in padded)
+    crop = tuple(int(rng.integers(1, q - lo + 1)) for q, lo in zip(padded, crop_lo))
+    nfolds = int(rng.integers(1, 4))
+    print(f"accumulate seed {seed} fp16 {fp16}: K {K} patch {patch} padded {padded} flips {flips} "
+          f"offsets {offsets} crop {crop_lo}+{crop} folds {nfolds}", flush=True)
+    dt = np.float16 if fp16 else np.float32
+    accum = _native.NNX_ACCUM_NNUNET_F16 if fp16 else _native.NNX_ACCUM_F32
+    g = rng.uniform(0.01, 1.0, patch).astype(dt)
+    acc = np.zeros((*padded, K), dtype=dt)
+    norm = np.zeros(padded, dtype=dt)
+    dacc, dnorm, dg = dev(acc), dev(norm), dev(g)
+    for off in offsets:
+        pred = (rng.standard_normal((len(flips), *patch, K)) * 4).astype(np.float32)
+        dpred = dev(pred)
+        _native.check(lib.nnx_sw_accumulate(
+            dpred.data_ptr(), len(flips), _native.ints(flips), K, _native.ints(patch), dg.data_ptr(),
+            _native.ints(off), _native.i64s(padded), accum, dacc.data_ptr(), dnorm.data_ptr(),
+            stream()))
+        m = _unflip(pred[0], flips[0])
+        for v in range(1, len(flips)):
+            m = m + _unflip(pred[v], flips[v])
+        if len(flips) > 1:
+            m = m / np.float32(len(flips))
+        sl = tuple(slice(o, o + p) for o, p in zip(off, patch))
+        w = m * g.astype(np.float32)[..., None]
+        acc[sl] = (acc[sl].astype(np.float32) + w).astype(dt)
+        norm[sl] = (norm[sl].astype(np.float32) + g.astype(np.float32)).astype(dt)
+    np.testing.assert_array_equal(host(dacc), acc)
+    np.testing.assert_array_equal(host(dnorm), norm)
+    total = torch.empty((*crop, K), dtype=dacc.dtype, device="cuda")
+    csl = tuple(slice(o, o + c) for o, c in zip(crop_lo, crop))
+    with np.errstate(divide="ignore", invalid="ignore"):
+        q = (acc.astype(np.float32) / norm.astype(np.float32)[..., None]).astype(dt)[csl]
+    expected = q
+    for f in range(nfolds):
+        _native.check(lib.nnx_sw_fold_add(dacc.data_ptr(), dnorm.data_ptr(), K, _native.i64s(padded),
+                                          _native.ints(crop_lo), _native.i64s(crop), accum,
+                                          int(f == 0), total.data_ptr(), stream()))
+        if f:
+            expected = (expected.astype(np.float32) + q.astype(np.float32)).astype(dt)
+    np.testing.assert_array_equal(host(total), expected)
+    logits = torch.empty_like(total)
+    labels = torch.empty(crop, dtype=torch.int16, device="cuda")
+    invalid = torch.zeros(1, dtype=torch.int32, device="cuda")
+    _native.check(lib.nnx_sw_fold_finalize(total.data_ptr(), K, int(np.prod(crop)), nfolds, accum,
+                                           logits.data_ptr(), labels.data_ptr(), invalid.data_ptr(),
+                                           stream()))
+    avg = expected if nfolds == 1 else \
+        (expected.astype(np.float32) / np.float32(nfolds)).astype(dt)
+    np.testing.assert_array_equal(host(logits), avg)
+    finite = np.isfinite(avg.astype(np.float32)).all(axis=-1)
+    want = np.argmax(np.where(np.isfinite(avg), avg, -np.inf).astype(np.float32), axis=-1)
+    want = want.astype(np.uint16)
+    want[~finite] = 65535
+    np.testing.assert_array_equal(host(labels).view(np.uint16), want)
+    assert int(host(invalid)[0]) == int((~finite).sum())
+
+
 def test_finalize_ties_choose_earliest_and_flags_nonfinite(lib):
     total = np.array([[1.0, 1.0, 0.5], [0.2, 3.0, 3.0], [np.nan, 1.0, 2.0], [-np.inf, -1.0, -1.0]],
                      dtype=np.float32)
