@@ -26,7 +26,14 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("source,target,classes", CASES, ids=str)
+def _random_cases(seed, n):
+    """Seeded source and target grids (size-1 axes included) and class counts."""
+    rng = np.random.default_rng(seed)
+    return [(tuple(int(v) for v in rng.integers(1, 21, 3)), tuple(int(v) for v in rng.integers(1, 31, 3)),
+             int(rng.integers(1, 9))) for _ in range(n)]
+
+
+@pytest.mark.parametrize("source,target,classes", CASES + _random_cases(2030, 8), ids=str)
 @pytest.mark.parametrize("dtype", [np.float32, np.float16], ids=["f32", "f16"])
 def test_restore_labels_match_oracle(device, source, target, classes, dtype):
     print(f"restore {source} -> {target} K={classes} {np.dtype(dtype).name}", flush=True)
