@@ -104,6 +104,59 @@ def test_forward_matches_oracle(device, name):
         net.close()
 
 
+def _random_topology(seed):
+    """A seeded small network: plain or residual (BasicBlockD or BottleneckD), 2-4 stages,
+    ragged widths, 3x3x3 or 1x3x3 kernels, isotropic or anisotropic strides, 1-4 input
+    channels, 1-5 classes; residual patches divisible by the total stride (the residual
+    encoder pools), plain ones of any size (the decoder crops)."""
+    rng = np.random.default_rng(seed)
+    stages = int(rng.integers(2, 5))
+    feats = tuple(int(rng.choice([4, 8, 12, 16, 24, 32, 48])) for _ in range(stages))
+    kernels = tuple((3, 3, 3) if rng.random() < 0.75 else (1, 3, 3) for _ in range(stages))
+    strides = ((1, 1, 1),) + tuple(tuple(int(v) for v in rng.choice([1, 2, 2], 3))
+                                   for _ in range(stages - 1))
+    enc = tuple(int(rng.integers(1, 3)) for _ in range(stages))
+    dec = tuple(int(rng.integers(1, 3)) for _ in range(stages - 1))
+    cin, classes = int(rng.choice([1, 2, 3, 4])), int(rng.integers(1, 6))
+    total = np.prod(np.array(strides), axis=0)
+    if rng.random() < 0.5:
+        bottleneck = tuple(max(2, f // 2) for f in feats) if rng.random() < 0.5 else None
+        spec = ResidualEncoderUNetSpec(cin, classes, feats, kernels, strides, enc, dec,
+                                       bottleneck_channels=bottleneck)
+        patch = tuple(int(t * rng.integers(1, 4)) for t in total)
+        patch = tuple(p * max(1, -(-4 // p)) for p in patch)  # at least 4 voxels an axis
+    else:
+        spec = PlainConvUNetSpec(cin, classes, feats, kernels, strides, enc, dec)
+        patch = tuple(int(v) for v in rng.integers(4, 21, 3))
+    return spec, patch, int(rng.integers(1, 3))
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_topologies_match_oracle(device, seed):
+    """Seeded small topologies no hand-written case above covers, in the float32-product and
+    the default fp16-split precision, at the float32 bar against the oracle."""
+    spec, patch, batch = _random_topology(700 + seed)
+    weights = random_weights(spec, seed=seed, random_affine=True)
+    x = np.random.default_rng(seed).standard_normal((batch, *patch, spec.input_channels))
+    x = x.astype(np.float32)
+    residual = isinstance(spec, ResidualEncoderUNetSpec)
+    ref = OracleNetwork(spec, weights, residual=residual)(x)
+    for precision in ("fp32", "fp32-split"):
+        print(f"random topology {seed}: {spec} patch={patch} batch={batch} precision={precision}",
+              flush=True)
+        net = build_network(spec, precision=precision)
+        net.load_weights(weights)
+        got = net(torch.from_numpy(x).to(device)).cpu().numpy()
+        msg = report(f"random topology {seed} {precision}", got, ref)
+        print(msg, flush=True)
+        assert got.shape == ref.shape
+        assert np.isfinite(got).all(), msg
+        assert np.abs(got - ref).max() <= 1e-3, msg
+        assert rel_l2(got, ref) <= 1e-5, msg
+        assert (got.argmax(-1) == ref.argmax(-1)).mean() >= 0.9999, msg
+        net.close()
+
+
 @pytest.mark.parametrize("name", ["liver-32", "brats-4ch", "autopet-aniso", "resenc-L", "liver-128"])
 def test_bf16_mixed_is_closer_than_bf16(device, name):
     """"bf16-mixed" keeps the full-resolution layers in fp16-split: its logits lie closer to
