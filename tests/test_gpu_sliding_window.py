@@ -51,7 +51,22 @@ POINTWISE_CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", POINTWISE_CASES, ids=str)
+def _random_pointwise_cases(seed, n):
+    """Seeded volumes (some smaller than the patch on an axis), patches, mirror-axis subsets,
+    accumulations and fold counts."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        shape = (int(rng.integers(1, 4)), *(int(v) for v in rng.integers(1, 31, 3)))
+        patch = tuple(int(v) for v in rng.integers(1, 17, 3))
+        axes = tuple(a for a in range(3) if rng.random() < 0.5)
+        accumulation = str(rng.choice(["float32", "nnunet-fp16"]))
+        scales = tuple(float(v) for v in np.round(rng.uniform(0.3, 1.5, int(rng.integers(1, 4))), 2))
+        cases.append((shape, patch, axes, accumulation, scales))
+    return cases
+
+
+@pytest.mark.parametrize("case", POINTWISE_CASES + _random_pointwise_cases(2031, 10), ids=str)
 def test_pointwise_pipeline_bitwise(device, case):
     shape, patch, axes, accumulation, scales = case
     print(f"pointwise case {case}", flush=True)
