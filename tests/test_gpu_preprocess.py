@@ -118,7 +118,15 @@ SPLINE_CASES = [
 ]
 
 
-@pytest.mark.parametrize("shape,new_shape,order", SPLINE_CASES)
+def _random_spline_cases(seed, n):
+    """Seeded grids: up- and downsampling per axis, 1-2 channels, orders 1 and 3."""
+    rng = np.random.default_rng(seed)
+    return [((int(rng.integers(1, 3)), *(int(v) for v in rng.integers(2, 31, 3))),
+             tuple(int(v) for v in rng.integers(2, 41, 3)), int(rng.choice([1, 3])))
+            for _ in range(n)]
+
+
+@pytest.mark.parametrize("shape,new_shape,order", SPLINE_CASES + _random_spline_cases(2032, 6))
 def test_resample_spline_whole_volume(lib, shape, new_shape, order):
     print(f"spline case {shape} -> {new_shape} order {order}", flush=True)
     rng = np.random.default_rng(shape[1] + new_shape[2])
