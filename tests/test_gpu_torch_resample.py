@@ -26,6 +26,9 @@ GOLDEN = Path(__file__).resolve().parent / "golden" / "torch_resampling.npz"
 
 SHAPES = [((5, 7, 9), (9, 4, 13)), ((3, 8, 6), (3, 17, 6)), ((11, 2, 5), (4, 7, 5)),
           ((1, 6, 7), (1, 9, 3)), ((6, 1, 4), (2, 5, 1)), ((16, 20, 24), (40, 50, 10))]
+# seeded grids beside them (size-1 axes included)
+SHAPES += [tuple(tuple(int(v) for v in g) for g in pair) for pair in
+           np.random.default_rng(2033).integers(1, 33, (4, 2, 3))]
 
 
 def _values(rng, channels, shape, dtype):
