@@ -1,0 +1,66 @@
+"""Every C-ABI entry point, called on a CPU host with null data pointers and seeded edge
+values for its sizes and shape arrays, returns (an error status or a size of 0) instead of
+crashing the process: argument checks run before any device call and never trap or throw
+across the ABI.  The calls run in a child process so that a crash fails this test with the
+name and seed of the call instead of ending pytest."""
+
+from __future__ import annotations
+
+import subprocess
+import sys
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parents[1]
+
+# entry points taking structs or callbacks are covered by the dedicated tests in
+# test_host_library.py; the rest get SEEDS argument sets each
+SKIP = {"nnx_model_create", "nnx_sw_predict", "nnx_sw_predict_custom", "nnx_model_destroy",
+        "nnx_last_error", "nnx_version", "nnx_sw_release"}
+SEEDS = 40
+
+CHILD = r"""
+import ctypes, random, sys
+sys.path.insert(0, sys.argv[1])
+from nnunet_mlx import _native
+
+INTS = [0, 1, 2, 3, 4, 7, 8, 16, 31, 32, 33, 64, 128, 320, 1024, 1025, -1, -7, 1 << 20,
+        1 << 30, (1 << 31) - 1, -(1 << 31)]
+FLOATS = [1.0, 0.5, 0.0, -1.0, float("nan"), float("inf"), 1e-30, 3e38]
+skip, seeds = set(sys.argv[2].split(",")), int(sys.argv[3])
+lib = _native.load()
+keep = []
+for name, (restype, argtypes) in _native._SIGNATURES.items():
+    if name in skip:
+        continue
+    fn = getattr(lib, name)
+    for seed in range(seeds):
+        rng = random.Random(f"{name}:{seed}")
+        args = []
+        for t in argtypes:
+            if t in (_native.c_int_p, _native.c_i64_p):
+                base = ctypes.c_int if t is _native.c_int_p else ctypes.c_int64
+                arr = (base * 8)(*[rng.choice(INTS) for _ in range(8)])
+                keep.append(arr)
+                args.append(ctypes.cast(arr, t) if rng.random() > 0.1 else None)
+            elif t in (ctypes.c_int, ctypes.c_int64):
+                args.append(rng.choice(INTS))
+            elif t is ctypes.c_size_t:
+                args.append(abs(rng.choice(INTS)))
+            elif t in (ctypes.c_float, ctypes.c_double):
+                args.append(rng.choice(FLOATS))
+            else:
+                args.append(None)
+        print(name, seed, flush=True)
+        fn(*args)
+print("done", flush=True)
+"""
+
+
+def test_every_entry_point_survives_null_pointers_and_edge_sizes():
+    proc = subprocess.run(
+        [sys.executable, "-c", CHILD, str(ROOT / "nnunet-mlx_amd"), ",".join(sorted(SKIP)),
+         str(SEEDS)],
+        capture_output=True, text=True, timeout=600)
+    last = proc.stdout.strip().splitlines()[-1:] or ["(no call started)"]
+    assert proc.returncode == 0 and last == ["done"], (
+        f"exit {proc.returncode} during the call '{last[0]}': {proc.stderr[-500:]}")
