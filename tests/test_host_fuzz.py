@@ -57,6 +57,14 @@ print("done", flush=True)
 
 
 def test_every_entry_point_survives_null_pointers_and_edge_sizes():
+    import pytest
+    import torch
+
+    # with a device present, a call whose arguments pass the checks would launch a kernel on
+    # the null pointers: this sweep is for hosts without one (counting devices does not
+    # initialise any)
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is visible: the sweep passes null device pointers (CPU hosts only)")
     proc = subprocess.run(
         [sys.executable, "-c", CHILD, str(ROOT / "nnunet-mlx_amd"), ",".join(sorted(SKIP)),
          str(SEEDS)],
